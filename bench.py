@@ -1,0 +1,301 @@
+"""Benchmark of the MXFP4 MoE path on one MI355X.
+
+Default workload: one GPT-OSS-20B-shaped MoE layer at decode batch 1 —
+router 2880->32 (bf16), top-4, 4 experts of gate_up 2880->5760 + down 2880->2880 in MXFP4,
+interleaved SwiGLU, weighted combine. A step is one token through one layer. To keep the
+256 MB MALL from serving the weights, 24 independent layers (10.2 GB of experts) stay
+resident and consecutive steps walk through them with distinct tokens, so every step
+streams its experts from HBM.
+
+Prints ONE JSON line (see the repository's benchmark contract). Other workloads
+(--workload matvec|decode64|prefill|decode1_120b|prefill_120b) print the same kind of line
+for DESIGN.md; the driver runs the default.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from silentotithrandousha_amd import GpuMoeDispatcher, DeviceBuffer  # noqa: E402
+from silentotithrandousha_amd import synthetic as syn  # noqa: E402
+from silentotithrandousha_amd._ffi import check, lib  # noqa: E402
+
+METRIC = "MoE layer tokens/s @GPT-OSS-20B shape (b=1,64,4096) + % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+MXFP4_PEAK_TFLOPS = 10100.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ algorithmic bytes / flops
+# Checkpoint-format bytes of one expert (MXFP4 nibbles + E8M0 scales + bf16 biases).
+def expert_bytes(H, I):
+    nbh, nbi = H // 32, I // 32
+    gu = 2 * I * nbh * 16 + 2 * I * nbh + 2 * I * 2
+    dn = H * nbi * 16 + H * nbi + H * 2
+    return gu, dn
+
+
+def layer_traffic(H, I, E, k, T, active):
+    """Algorithmic HBM bytes of one layer step: `active` experts' weights once, the router
+    (bf16 W + f32 bias) once, activations in and out in f32."""
+    gu, dn = expert_bytes(H, I)
+    return active * (gu + dn) + E * H * 2 + E * 4 + 2 * T * H * 4
+
+
+def layer_flops(H, I, E, k, T):
+    return 2.0 * T * E * H + 2.0 * T * k * (2 * I * H + H * I)
+
+
+# ------------------------------------------------------------------ resident synthetic layers
+class Layers:
+    def __init__(self, disp, H, I, E, n_layers, seed=1234):
+        self.disp, self.H, self.I, self.E = disp, H, I, E
+        nbh, nbi = H // 32, I // 32
+        sizes = dict(gub=E * 2 * I * nbh * 16, gus=E * 2 * I * nbh, gubias=E * 2 * I * 4,
+                     db=E * H * nbi * 16, ds=E * H * nbi, dbias=E * H * 4)
+        stage = {n: DeviceBuffer(s) for n, s in sizes.items()}
+        L = lib()
+        rng = np.random.default_rng(seed)
+        for l in range(n_layers):
+            s0 = seed * 1000 + l * 16
+            check(L.moe_synth_fill_device(stage["gub"].ptr, sizes["gub"], 0, s0 + 1, 0, 255, None))
+            check(L.moe_synth_fill_device(stage["gus"].ptr, sizes["gus"], 0, s0 + 2, 118, 130, None))
+            check(L.moe_synth_fill_device(stage["gubias"].ptr, sizes["gubias"] // 4, 3, s0 + 3, 0.01, 0, None))
+            check(L.moe_synth_fill_device(stage["db"].ptr, sizes["db"], 0, s0 + 4, 0, 255, None))
+            check(L.moe_synth_fill_device(stage["ds"].ptr, sizes["ds"], 0, s0 + 5, 118, 130, None))
+            check(L.moe_synth_fill_device(stage["dbias"].ptr, sizes["dbias"] // 4, 3, s0 + 6, 0.01, 0, None))
+            check(L.moe_preload_layer_device(disp.ctx, l, E, stage["gub"].ptr, stage["gus"].ptr,
+                                             stage["gubias"].ptr, stage["db"].ptr, stage["ds"].ptr,
+                                             stage["dbias"].ptr, None))
+            rw = syn.bf16_bits(rng.normal(0, 0.02, size=(E, H)).astype(np.float32))
+            rb = np.zeros(E, np.float32)
+            check(L.moe_preload_router(disp.ctx, l, E, rw.ctypes.data, rb.ctypes.data))
+            disp.synchronize()
+            if l % 6 == 5 or l == n_layers - 1:
+                log(f"resident layers {l + 1}/{n_layers}")
+        for b in stage.values():
+            b.close()
+
+
+def event_timer():
+    """Wall time of device work on the context stream, bracketed by synchronisation."""
+    return time.perf_counter
+
+
+# ------------------------------------------------------------------ decode / prefill bench
+def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
+    L = lib()
+    disp = GpuMoeDispatcher(H, I, 7.0)
+    disp.set_fused_decode(args.fused)
+    log(f"synthesising {n_layers} layers x {E} experts ({n_layers * E * sum(expert_bytes(H, I)) / 1e9:.2f} GB MXFP4)")
+    Layers(disp, H, I, E, n_layers)
+    P = max(n_layers * 10, 8) if T == 1 else 2 * n_layers
+    x = DeviceBuffer(P * T * H * 4)
+    y = DeviceBuffer(P * T * H * 4)
+    check(L.moe_synth_fill_device(x.ptr, P * T * H, 2, 99, 1.0, 0, None))
+    disp.synchronize()
+
+    def step(i, stream=None):
+        j = i % P
+        check(L.moe_layer_forward_device(disp.ctx, i % n_layers, x.ptr + j * T * H * 4, T, k,
+                                         y.ptr + j * T * H * 4, stream))
+
+    log("warmup")
+    for i in range(args.warmup):
+        step(i)
+    disp.synchronize()
+
+    graph = None
+    G = P if args.graph else 0
+    if args.graph:
+        check(L.moe_graph_begin(disp.ctx))
+        for i in range(G):
+            step(i)
+        g = ctypes.c_void_p()
+        check(L.moe_graph_end(disp.ctx, ctypes.byref(g)))
+        graph = g.value
+        check(L.moe_graph_launch(disp.ctx, graph))  # upload / first replay untimed
+        disp.synchronize()
+
+    log(f"timed region: {args.steps} steps ({'graph x' + str(G) if graph else 'eager'})")
+    disp.synchronize()
+    t0 = time.perf_counter()
+    if graph:
+        n_full, rem = divmod(args.steps, G)
+        for _ in range(n_full):
+            check(L.moe_graph_launch(disp.ctx, graph))
+        for i in range(rem):
+            step(i)
+    else:
+        for i in range(args.steps):
+            step(i)
+    disp.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    # per-kernel durations: HIP events around every launch, same steps, eager
+    log("kernel timing region")
+    disp.set_timing(True)
+    disp.reset_timing()
+    n_kt = min(args.steps, max(240, G))
+    for i in range(n_kt):
+        step(i)
+    disp.synchronize()
+    kt = {name: disp.get_timing(kid) for kid, name in
+          enumerate(["route", "bucket", "gate_up", "down", "combine", "decode_gate_up",
+                     "decode_down"])}
+    disp.set_timing(False)
+    if graph:
+        check(L.moe_graph_destroy(graph))
+
+    tokens_per_s = T * args.steps / elapsed
+    active = min(E, T * k) if T == 1 else E  # expected distinct experts per step
+    traffic = layer_traffic(H, I, E, k, T, active)
+    flops = layer_flops(H, I, E, k, T)
+    gu_b, dn_b = expert_bytes(H, I)
+    dom = "decode_gate_up" if kt["decode_gate_up"][1] else "gate_up"
+    gu_ms, gu_n = kt[dom]
+    gu_avg_s = gu_ms / max(gu_n, 1) / 1e3
+    gu_bytes = active * gu_b + T * H * 4 + T * k * I * 4
+    res = {
+        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded, BASELINE distributions; random-init weights, device-generated)",
+        "config": {"workload": workload, "name": config_name, "hidden": H, "intermediate": I,
+                   "experts": E, "top_k": k, "tokens_per_step": T, "resident_layers": n_layers,
+                   "weights": "MXFP4 E2M1 + E8M0 (checkpoint layout repacked on preload)",
+                   "arithmetic": "exact MXFP4->bf16 decode x f32 activation as bf16 hi+lo, f32 MFMA accumulate",
+                   "graph_replay": bool(graph), "fused_decode": bool(args.fused and T == 1)},
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_decode_gate_up" if dom == "decode_gate_up" else "k_expert_gemv<gate_up>",
+                     "achieved": round(gu_bytes / gu_avg_s / 1e9, 1) if gu_n else None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_bytes / gu_avg_s / 1e9 / HBM_PEAK_GBS, 4) if gu_n else None,
+                     "traffic": None,
+                     "algorithmic_bytes_per_launch": gu_bytes,
+                     "avg_launch_us": round(gu_avg_s * 1e6, 3)},
+        "layer_roofline": {"algorithmic_bytes_per_step": traffic, "flops_per_step": flops,
+                           "achieved_GBps": round(traffic / (ms_per_step / 1e3) / 1e9, 1),
+                           "frac_hbm": round(traffic / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "achieved_TFLOPs": round(flops / (ms_per_step / 1e3) / 1e12, 2),
+                           "frac_mxfp4_peak": round(flops / (ms_per_step / 1e3) / 1e12 / MXFP4_PEAK_TFLOPS, 5)},
+        "kernel_us": {n: round(v[0] * 1e3 / max(v[1], 1), 3) for n, v in kt.items() if v[1]},
+    }
+    disp.close()
+    return res
+
+
+def run_matvec_bench(args):
+    """y = W x, W 2880x2880 MXFP4; 64 distinct copies back to back."""
+    L = lib()
+    from silentotithrandousha_amd import mxfp4_matvec, mxfp4_pack
+    R = C = 2880
+    copies = 96
+    disp = GpuMoeDispatcher(C, C, 7.0)
+    nb = C // 32
+    blocks = DeviceBuffer(R * nb * 16)
+    scales = DeviceBuffer(R * nb)
+    packed = []
+    for c in range(copies):
+        check(L.moe_synth_fill_device(blocks.ptr, R * nb * 16, 0, 7000 + 2 * c, 0, 255, None))
+        check(L.moe_synth_fill_device(scales.ptr, R * nb, 0, 7001 + 2 * c, 118, 130, None))
+        packed.append(mxfp4_pack(blocks, scales, R, C))
+    x = DeviceBuffer(C * 4)
+    y = DeviceBuffer(R * 4)
+    check(L.moe_synth_fill_device(x.ptr, C, 2, 5, 1.0, 0, None))
+    disp.synchronize()
+    for i in range(args.warmup):
+        mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
+    disp.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
+    disp.synchronize()
+    el = time.perf_counter() - t0
+    byts = R * nb * 17 + C * 4 + R * 4
+    return {"metric": "MXFP4 matvec 2880x2880 GB/s", "value": round(byts * args.steps / el / 1e9, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(el * 1e3 / args.steps, 6), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "config1 matvec 2880x2880", "copies": copies}}
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(seconds, H, I, E, k):
+    """The reference's live CPU MoE block restated in C (oracle/): router + top-4, cold fp16
+    expert cache (MXFP4 -> fp16 decode of the 4 selected experts, session.rs:860-941) and
+    cpu_expert_ffn with the NEON matvec order, one thread per selected expert (rayon over
+    k slots, session.rs:953-972), then the combine. Bounded sample, rank 0, N=1 only."""
+    from oracle import orc
+    layers = [syn.make_layer(H, I, E, seed=500 + i) for i in range(2)]
+    xs = syn.hidden(64, H, seed=501)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        lay = layers[n % 2]
+        x = xs[n % 64]
+        logits = orc.router_logits(lay["router_w"], lay["router_b"], x, E, H)
+        idx, w, _, _ = orc.topk(logits, k)
+        orc.live_moe_token(x, lay, idx[0], w[0], k)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 3) or n >= 1000:
+            break
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": k, "kind": "port",
+            "sample": f"{n} tokens of the config-2 layer (2 synthetic layers, cold fp16 expert "
+                      f"cache: MXFP4->fp16 dequant + fp16xf32 matvec in the reference's NEON "
+                      f"order, {k} threads as rayon over the top-{k} slots), {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4800)
+    ap.add_argument("--warmup", type=int, default=480)
+    ap.add_argument("--workload", default="decode1",
+                    choices=["decode1", "decode64", "prefill", "matvec", "decode1_120b", "prefill_120b"])
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--no-graph", dest="graph", action="store_false")
+    ap.add_argument("--no-fused", dest="fused", action="store_false",
+                    help="single-token steps through the multi-kernel path")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", dest="cpu", action="store_false")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
+              "sharding of this path is described in DESIGN.md and not run here.", file=sys.stderr)
+        sys.exit(2)
+    rank = int(os.environ.get("RANK", "0"))
+    H = I = 2880
+    if args.workload == "matvec":
+        res = run_matvec_bench(args)
+    elif args.workload == "decode1":
+        res = run_layer_bench(args, H, I, 32, 4, 1, args.layers, "config2 gpt-oss-20b moe layer decode b=1", "decode1")
+    elif args.workload == "decode64":
+        res = run_layer_bench(args, H, I, 32, 4, 64, args.layers, "config3 gpt-oss-20b moe layer decode b=64", "decode64")
+    elif args.workload == "prefill":
+        res = run_layer_bench(args, H, I, 32, 4, 4096, args.layers, "config4 gpt-oss-20b moe prefill 4096 tokens", "prefill")
+    elif args.workload == "decode1_120b":
+        res = run_layer_bench(args, H, I, 128, 4, 1, args.layers, "config5 gpt-oss-120b moe layer decode b=1", "decode1_120b")
+    else:
+        res = run_layer_bench(args, H, I, 128, 4, 2048, args.layers, "config5 gpt-oss-120b moe layer 2048 tokens", "prefill_120b")
+    if args.cpu and rank == 0 and args.workload == "decode1":
+        log("cpu baseline")
+        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, H, I, 32, 4)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,234 @@
+/*
+ * mxfp4_moe.h — C ABI of the MI355X (gfx950) MXFP4 mixture-of-experts path.
+ *
+ * Drop-in replacement for the GPU backend of gabearro/SilentOTITHRanDouSha's GPT-OSS MoE
+ * block. Each entry point names the reference item it replaces (file:line in that repo).
+ * All entry points return 0 (MOE_OK) or a MOE_ERR_* code; the message of the last failure
+ * on the calling thread is returned by moe_last_error() (this replaces the reference's
+ * Result<_, String>). No C++ exception crosses this boundary.
+ *
+ * Layout conventions (the checkpoint's, weights.rs:17-27 and :283-316):
+ *   gate_up blocks [E, 2*I, H/32, 16] u8   — interleaved rows: row 2i = gate i, 2i+1 = up i
+ *   gate_up scales [E, 2*I, H/32]     u8   — E8M0
+ *   gate_up bias   [E, 2*I]           f32
+ *   down    blocks [E, H, I/32, 16]   u8
+ *   down    scales [E, H, I/32]       u8
+ *   down    bias   [E, H]             f32
+ *   Block byte j of block b holds element 32b+2j in its low nibble and 32b+2j+1 in its high.
+ *   router weight  [E, H] bf16 bits (as stored in the checkpoint), bias [E] f32.
+ *
+ * Pointers: host pointers unless the name ends in _device, whose arguments are device
+ * pointers (HBM) and a stream (a hipStream_t passed as void*, NULL = the context's stream).
+ * Host-pointer calls are synchronous (the reference's commit()+wait_until_completed()).
+ * Device calls are asynchronous on the given stream.
+ *
+ * Threading: a context owns device scratch that every dispatch writes (as the reference's
+ * GpuMoeDispatcher does through shared buffers, moe_dispatch.rs:245-251). Calls on one
+ * context must be serialised by the caller; distinct contexts are independent.
+ */
+#ifndef MXFP4_MOE_H
+#define MXFP4_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moe_ctx moe_ctx;
+
+enum moe_status {
+  MOE_OK = 0,
+  MOE_ERR_INVALID = 1,   /* bad argument, shape or length */
+  MOE_ERR_STATE = 2,     /* call out of order: layer / router / LM head not loaded */
+  MOE_ERR_HIP = 3,       /* HIP runtime error (message names the call) */
+  MOE_ERR_NO_DEVICE = 4, /* no gfx950 device visible */
+  MOE_ERR_OOM = 5        /* device allocation failed */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *moe_last_error(void);
+/* Library version string. */
+const char *moe_version(void);
+
+/* ------------------------------------------------------------------ context */
+
+/* GpuMoeDispatcher::new(hidden_size, inter_size, swiglu_clamp) — moe_dispatch.rs:60-146.
+ * hidden_size and inter_size must be positive multiples of 32 (MXFP4 block length).
+ * swiglu_clamp is GptOssConfig::swiglu_limit (config.rs:50, default 7.0). */
+int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ctx **out);
+/* Drop (no reference counterpart beyond Rust's Drop of GpuMoeDispatcher). */
+void moe_destroy(moe_ctx *ctx);
+
+/* Adaptive top-k of session.rs:168-201 / :569-583 (GPT_OSS_ADAPTIVE_MOE_TOPK and friends).
+ * Off by default, as in the reference. enabled=0 turns it off. */
+int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_min_prob,
+                          float top1_min_margin, float top2_min_mass);
+
+/* Options (no reference counterpart). MOE_OPT_FUSED_DECODE: 1 (default) runs single-token
+ * forwards as two fused kernels (router + top-k + gate_up + SwiGLU; down + combine); 0 uses
+ * the five-kernel path that larger batches take. Results agree to the matmul tolerance. */
+enum moe_option { MOE_OPT_FUSED_DECODE = 1 };
+int moe_set_option(moe_ctx *ctx, int option, int64_t value);
+
+/* ------------------------------------------------------------------ weights */
+
+/* GpuMoeDispatcher::preload_experts — moe_dispatch.rs:149-229, one layer per call.
+ * Copies one layer's experts (checkpoint layout above) into HBM, repacked for the kernels.
+ * The repack is a lossless permutation; moe_dequant_expert reads it back. Re-preloading a
+ * layer index replaces it. Short bias arrays are not accepted: pass full [E,2I] / [E,H]. */
+int moe_preload_layer(moe_ctx *ctx, size_t layer, size_t n_experts,
+                      const uint8_t *gate_up_blocks, const uint8_t *gate_up_scales,
+                      const float *gate_up_bias, const uint8_t *down_blocks,
+                      const uint8_t *down_scales, const float *down_bias);
+/* Same, with the checkpoint tensors already in device memory (e.g. memory-mapped upload). */
+int moe_preload_layer_device(moe_ctx *ctx, size_t layer, size_t n_experts,
+                             const uint8_t *gate_up_blocks, const uint8_t *gate_up_scales,
+                             const float *gate_up_bias, const uint8_t *down_blocks,
+                             const uint8_t *down_scales, const float *down_bias, void *stream);
+/* Router weights of one layer (LayerWeights::router_weight/bias, weights.rs:44-46, loaded at
+ * weights.rs:280-281). In the reference the router runs on the ANE inside
+ * build_decode_output_proj_router (executables.rs:301-313); here it runs on the GPU. */
+int moe_preload_router(moe_ctx *ctx, size_t layer, size_t n_experts,
+                       const uint16_t *weight_bf16, const float *bias);
+/* Same with f32 weights; every value must be exactly representable in bf16 (true for
+ * weights loaded through bf16_to_f32, weights.rs:141-147), else MOE_ERR_INVALID. */
+int moe_preload_router_f32(moe_ctx *ctx, size_t layer, size_t n_experts, const float *weight,
+                           const float *bias);
+
+/* ------------------------------------------------------------------ per-expert dispatch */
+
+/* GpuMoeDispatcher::dispatch_expert_preloaded — moe_dispatch.rs:232-324.
+ * output[H] = clamp(down(SwiGLU(gate_up(input))), +-65504) for one preloaded expert, with the
+ * GPT-OSS activation of session.rs:101-123 (not the Metal shader's, see DESIGN). */
+int moe_dispatch_expert_preloaded(moe_ctx *ctx, const float *input, size_t layer,
+                                  size_t expert_idx, float *output);
+
+/* GpuMoeDispatcher::dispatch_expert — moe_dispatch.rs:327-469. One expert from caller-owned
+ * checkpoint tensors of that expert alone (no [E] dimension). Block and scale lengths must
+ * equal the expert's sizes; bias lengths may be short and are zero-padded (:352-359). */
+int moe_dispatch_expert(moe_ctx *ctx, const float *input, const uint8_t *gate_up_blocks,
+                        size_t gate_up_blocks_len, const uint8_t *gate_up_scales,
+                        size_t gate_up_scales_len, const float *gate_up_bias,
+                        size_t gate_up_bias_len, const uint8_t *down_blocks,
+                        size_t down_blocks_len, const uint8_t *down_scales,
+                        size_t down_scales_len, const float *down_bias, size_t down_bias_len,
+                        float *output);
+
+/* One tuple of dispatch_experts_batched (moe_dispatch.rs:476). */
+typedef struct moe_expert_ref {
+  size_t expert_idx; /* carried for the caller, unused (as in the reference) */
+  float weight;
+  const uint8_t *gate_up_blocks;
+  size_t gate_up_blocks_len;
+  const uint8_t *gate_up_scales;
+  size_t gate_up_scales_len;
+  const float *gate_up_bias;
+  size_t gate_up_bias_len;
+  const uint8_t *down_blocks;
+  size_t down_blocks_len;
+  const uint8_t *down_scales;
+  size_t down_scales_len;
+  const float *down_bias;
+  size_t down_bias_len;
+} moe_expert_ref;
+
+/* GpuMoeDispatcher::dispatch_experts_batched — moe_dispatch.rs:473-607.
+ * output[H] = sum over experts in order of weight * expert_output, where non-finite expert
+ * output elements are skipped (:594-603). n = 0 gives zeros. */
+int moe_dispatch_experts_batched(moe_ctx *ctx, const float *input, size_t n,
+                                 const moe_expert_ref *experts, float *output);
+
+/* ------------------------------------------------------------------ LM head */
+
+/* GpuMoeDispatcher::init_lm_head — moe_dispatch.rs:611-621. weights [vocab, H] f32. */
+int moe_init_lm_head(moe_ctx *ctx, const float *weights, size_t vocab_size);
+/* GpuMoeDispatcher::dispatch_lm_head — moe_dispatch.rs:624-683. logits[vocab] = W input.
+ * Returns MOE_ERR_STATE where the reference panics ("call init_lm_head first"). */
+int moe_dispatch_lm_head(moe_ctx *ctx, const float *input, size_t vocab_size, float *logits);
+
+/* ------------------------------------------------------------------ path-level entry points */
+
+/* Router + top-k + renormalisation for n_tokens hidden states — session.rs:818-841 with the
+ * fp32 router of session.rs:495-520 evaluated in the library's canonical summation order
+ * (64 strided fused partial sums + xor butterfly, then + bias). idx/weights: [n_tokens, top_k];
+ * slots beyond an adaptive count hold idx -1, weight 0. logits (optional, may be NULL):
+ * [n_tokens, E]. */
+int moe_router_topk(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens, size_t top_k,
+                    int32_t *idx, float *weights, float *logits);
+
+/* The MoE block of Session::decode_step_inner — session.rs:818-980: router, top-k,
+ * per-expert SwiGLU FFN, weighted combine in slot order. x, y: [n_tokens, H]. */
+int moe_layer_forward(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens,
+                      size_t top_k, float *y);
+/* Same on device buffers, asynchronous on `stream`. */
+int moe_layer_forward_device(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens,
+                             size_t top_k, float *y, void *stream);
+
+/* ------------------------------------------------------------------ MXFP4 primitives */
+
+/* dequant_mxfp4_row / dequant_expert_{gate_up,down}_into — weights.rs:350-423, bit-exact:
+ * out[r, 32b+2j] = LUT[lo] * f32_from_bits(scale << 23) (scale 0 -> +0.0, 255 -> +inf).
+ * blocks [rows, cols/32, 16], scales [rows, cols/32], out [rows, cols] f32; device buffers. */
+int moe_mxfp4_dequant_device(const uint8_t *blocks, const uint8_t *scales, size_t rows,
+                             size_t cols, float *out, void *stream);
+/* Decode of one preloaded expert matrix from its resident (repacked) copy, in the
+ * reference's logical layout: which = 0 -> gate_up [2I, H] (interleaved rows as in the
+ * checkpoint), 1 -> down [H, I]. out is a device buffer. Proves the resident copy lossless. */
+int moe_dequant_expert_device(moe_ctx *ctx, size_t layer, size_t expert_idx, int which,
+                              float *out, void *stream);
+/* Bytes of the resident (repacked) form of a [rows, cols] MXFP4 matrix. */
+size_t moe_mxfp4_packed_size(size_t rows, size_t cols);
+/* Repack checkpoint-layout MXFP4 (device) into the resident form (device, packed_size bytes). */
+int moe_mxfp4_pack_device(const uint8_t *blocks, const uint8_t *scales, size_t rows, size_t cols,
+                          uint8_t *packed, void *stream);
+/* y[rows] = W x for a packed MXFP4 matrix (the reference's dequant + matvec, weights.rs:350-371
+ * with session.rs:75-85). x, y: device f32. Uses ctx scratch for the split of x. */
+int moe_mxfp4_matvec_device(moe_ctx *ctx, const uint8_t *packed, size_t rows, size_t cols,
+                            const float *x, float *y, void *stream);
+
+/* ------------------------------------------------------------------ device memory helpers */
+/* Thin wrappers so hosts without a HIP runtime binding (ctypes, Rust FFI) can stage data. */
+int moe_device_alloc(size_t bytes, void **ptr);
+int moe_device_free(void *ptr);
+int moe_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int moe_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int moe_memset_device(void *dst, int value, size_t bytes);
+int moe_synchronize(moe_ctx *ctx);
+/* The context's stream (a hipStream_t) for callers that enqueue their own work. */
+void *moe_stream(moe_ctx *ctx);
+
+/* Seeded synthetic fill of device memory for benchmarks (no reference counterpart): kind 0 =
+ * bytes uniform in [lo, hi]; kind 1 = bf16 bits of N(0, sigma) rounded to nearest even;
+ * kind 2 = f32 N(0, sigma); kind 3 = f32 of bf16-rounded N(0, sigma). n = element count. */
+int moe_synth_fill_device(void *dst, size_t n, int kind, uint64_t seed, float a, float b,
+                          void *stream);
+
+/* ------------------------------------------------------------------ HIP graphs */
+/* Capture of device-pointer calls on the context stream into a HIP graph, for callers whose
+ * per-call GPU work is shorter than the host launch path (batch-1 decode). No reference
+ * counterpart (Metal command buffers were re-encoded per call, moe_dispatch.rs:404-458).
+ * Between begin and end only *_device calls with stream NULL may be issued; the context
+ * workspace must already be sized by one uncaptured call of the same shape, and timing must
+ * be off. The graph reads the buffers it was captured with at replay time. */
+int moe_graph_begin(moe_ctx *ctx);
+int moe_graph_end(moe_ctx *ctx, void **graph_exec);
+int moe_graph_launch(moe_ctx *ctx, void *graph_exec);
+int moe_graph_destroy(void *graph_exec);
+
+/* ------------------------------------------------------------------ timing */
+/* Per-kernel GPU time of the last device forward calls, accumulated with HIP events on the
+ * stream the kernels run on when enabled (no reference counterpart). */
+int moe_set_timing(moe_ctx *ctx, int enabled);
+/* kernel: 0 route, 1 bucket, 2 gate_up, 3 down, 4 combine, 5 single-token router+gate_up,
+ * 6 single-token down+combine.
+ * Returns accumulated milliseconds
+ * and launch count since the last reset; synchronises the context stream. */
+int moe_get_timing(moe_ctx *ctx, int kernel, double *ms, uint64_t *launches);
+int moe_reset_timing(moe_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MXFP4_MOE_H */

@@ -1,0 +1,204 @@
+"""ctypes front end of the CPU oracle (oracle/liborc.so) — test infrastructure only.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module,
+as the checker or as the timed CPU baseline. The product library never loads it.
+The C sources cite the reference lines each function restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liborc.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_sz = ctypes.c_size_t
+
+
+class Adaptive(ctypes.Structure):
+    """orc_adaptive: the GPT_OSS_ADAPTIVE_* settings of session.rs:168-201."""
+    _fields_ = [("enabled", ctypes.c_int), ("min_k", ctypes.c_size_t),
+                ("top1_min_prob", ctypes.c_float), ("top1_min_margin", ctypes.c_float),
+                ("top2_min_mass", ctypes.c_float)]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    L = ctypes.CDLL(_LIB_PATH)
+    L.orc_dequant_mxfp4_row.argtypes = [_u8p, _u8p, _sz, _f32p]
+    L.orc_dequant_mxfp4_matrix.argtypes = [_u8p, _u8p, _sz, _sz, _f32p]
+    L.orc_dequant_gate_up_reordered.argtypes = [_u8p, _u8p, _sz, _sz, _f32p]
+    L.orc_reorder_gate_up_bias.argtypes = [_f32p, _sz, _f32p]
+    L.orc_f16_mul_scalar.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+    L.orc_f16_mul_scalar.restype = ctypes.c_uint16
+    L.orc_dequant_mxfp4_row_f16.argtypes = [_u8p, _u8p, _sz, _u16p]
+    L.orc_dequant_gate_up_reordered_f16.argtypes = [_u8p, _u8p, _sz, _sz, _u16p]
+    L.orc_dequant_down_f16.argtypes = [_u8p, _u8p, _sz, _sz, _u16p]
+    L.orc_f32_to_f16_rne.argtypes = [ctypes.c_float]
+    L.orc_f32_to_f16_rne.restype = ctypes.c_uint16
+    L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_f16_to_f32.restype = ctypes.c_float
+    L.orc_f32_to_bf16_rne.argtypes = [ctypes.c_float]
+    L.orc_f32_to_bf16_rne.restype = ctypes.c_uint16
+    L.orc_expert_ffn_f32.argtypes = [_f32p, _sz, _u8p, _u8p, _f32p, _u8p, _u8p, _f32p, _sz, _sz,
+                                     ctypes.c_float, _f32p, ctypes.c_void_p]
+    L.orc_mxfp4_matvec_f32.argtypes = [_u8p, _u8p, _sz, _sz, _f32p, _f32p]
+    L.orc_router_logits.argtypes = [_u16p, _f32p, _f32p, _sz, _sz, _sz, _f32p]
+    L.orc_router_logits_seq.argtypes = [_u16p, _f32p, _f32p, _sz, _sz, _sz, _f32p]
+    L.orc_topk.argtypes = [_f32p, _sz, _sz, _sz, ctypes.c_void_p, _i32p, _f32p, ctypes.c_void_p,
+                           ctypes.c_void_p]
+    L.orc_moe_layer_f32.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_float, _u16p, _f32p,
+                                    _u8p, _u8p, _f32p, _u8p, _u8p, _f32p, ctypes.c_void_p, _f32p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    L.orc_combine.argtypes = [_f32p, _f32p, _sz, _sz, ctypes.c_int, _f32p]
+    L.orc_matvec_f16xf32.argtypes = [_u16p, _f32p, _f32p, _sz, _sz]
+    L.orc_live_moe_token.argtypes = [_f32p, _sz, _sz, _sz, _i32p, _f32p, _u8p, _u8p, _f32p, _u8p,
+                                     _u8p, _f32p, ctypes.c_int, _f32p]
+    L.orc_live_moe_token.restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def dequant_mxfp4(blocks, scales, rows, cols):
+    """weights.rs:350-423: checkpoint-layout MXFP4 -> f32 [rows, cols]."""
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_dequant_mxfp4_matrix(_c(blocks, np.uint8).reshape(-1), _c(scales, np.uint8).reshape(-1),
+                                   rows, cols, out.reshape(-1))
+    return out
+
+
+def dequant_mxfp4_row(blocks, scales):
+    nb = len(scales)
+    out = np.empty(nb * 32, np.float32)
+    lib().orc_dequant_mxfp4_row(_c(blocks, np.uint8).reshape(-1), _c(scales, np.uint8).reshape(-1),
+                                nb, out)
+    return out
+
+
+def dequant_mxfp4_row_f16(blocks, scales):
+    nb = len(scales)
+    out = np.empty(nb * 32, np.uint16)
+    lib().orc_dequant_mxfp4_row_f16(_c(blocks, np.uint8).reshape(-1),
+                                    _c(scales, np.uint8).reshape(-1), nb, out)
+    return out
+
+
+def mxfp4_matvec(blocks, scales, rows, cols, x):
+    y = np.empty(rows, np.float32)
+    lib().orc_mxfp4_matvec_f32(_c(blocks, np.uint8).reshape(-1), _c(scales, np.uint8).reshape(-1),
+                               rows, cols, _c(x, np.float32).reshape(-1), y)
+    return y
+
+
+def expert_ffn(x, gu_blocks, gu_scales, gu_bias, d_blocks, d_scales, d_bias, H, I, limit=7.0,
+               want_h=False):
+    x = _c(x, np.float32).reshape(-1, H)
+    T = x.shape[0]
+    y = np.empty((T, H), np.float32)
+    h = np.empty((T, I), np.float32) if want_h else None
+    lib().orc_expert_ffn_f32(x.reshape(-1), T, _c(gu_blocks, np.uint8).reshape(-1),
+                             _c(gu_scales, np.uint8).reshape(-1), _c(gu_bias, np.float32).reshape(-1),
+                             _c(d_blocks, np.uint8).reshape(-1), _c(d_scales, np.uint8).reshape(-1),
+                             _c(d_bias, np.float32).reshape(-1), H, I, limit, y.reshape(-1),
+                             _ptr(h))
+    return (y, h) if want_h else y
+
+
+def router_logits(w_bf16, bias, x, E, H, sequential=False):
+    x = _c(x, np.float32).reshape(-1, H)
+    T = x.shape[0]
+    out = np.empty((T, E), np.float32)
+    f = lib().orc_router_logits_seq if sequential else lib().orc_router_logits
+    f(_c(w_bf16, np.uint16).reshape(-1), _c(bias, np.float32).reshape(-1), x.reshape(-1), T, E, H,
+      out.reshape(-1))
+    return out
+
+
+def topk(logits, k, adaptive=None):
+    logits = _c(logits, np.float32)
+    T, E = logits.shape
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    probs = np.empty((T, E), np.float32)
+    kused = np.empty(T, np.int32)
+    ad = ctypes.byref(adaptive) if adaptive is not None else None
+    lib().orc_topk(logits.reshape(-1), T, E, k, ad, idx.reshape(-1), w.reshape(-1), _ptr(probs),
+                   _ptr(kused))
+    return idx, w, probs, kused
+
+
+def moe_layer(x, layer, k, limit=7.0, adaptive=None):
+    """session.rs:818-980 MoE block on the fp32 path. `layer` is a dict of checkpoint tensors."""
+    H = layer["H"]
+    I = layer["I"]
+    E = layer["E"]
+    x = _c(x, np.float32).reshape(-1, H)
+    T = x.shape[0]
+    y = np.empty((T, H), np.float32)
+    logits = np.empty((T, E), np.float32)
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    ad = ctypes.byref(adaptive) if adaptive is not None else None
+    lib().orc_moe_layer_f32(x.reshape(-1), T, H, I, E, k, limit, _c(layer["router_w"], np.uint16).reshape(-1),
+                            _c(layer["router_b"], np.float32).reshape(-1),
+                            _c(layer["gu_blocks"], np.uint8).reshape(-1),
+                            _c(layer["gu_scales"], np.uint8).reshape(-1),
+                            _c(layer["gu_bias"], np.float32).reshape(-1),
+                            _c(layer["d_blocks"], np.uint8).reshape(-1),
+                            _c(layer["d_scales"], np.uint8).reshape(-1),
+                            _c(layer["d_bias"], np.float32).reshape(-1), ad, y.reshape(-1),
+                            _ptr(logits), _ptr(idx), _ptr(w))
+    return y, logits, idx, w
+
+
+def combine(outs, w, skip_nonfinite=False):
+    outs = _c(outs, np.float32)
+    n, H = outs.shape
+    y = np.empty(H, np.float32)
+    lib().orc_combine(outs.reshape(-1), _c(w, np.float32), n, H, int(skip_nonfinite), y)
+    return y
+
+
+def matvec_f16xf32(a_f16, x, rows, cols):
+    y = np.empty(rows, np.float32)
+    lib().orc_matvec_f16xf32(_c(a_f16, np.uint16).reshape(-1), _c(x, np.float32).reshape(-1), y,
+                             rows, cols)
+    return y
+
+
+def live_moe_token(x, layer, idx, w, n_threads):
+    """One token through the reference's live CPU MoE block (cold expert cache)."""
+    H = layer["H"]
+    I = layer["I"]
+    y = np.empty(H, np.float32)
+    rc = lib().orc_live_moe_token(_c(x, np.float32).reshape(-1), H, I, len(idx), _c(idx, np.int32),
+                                  _c(w, np.float32), _c(layer["gu_blocks"], np.uint8).reshape(-1),
+                                  _c(layer["gu_scales"], np.uint8).reshape(-1),
+                                  _c(layer["gu_bias"], np.float32).reshape(-1),
+                                  _c(layer["d_blocks"], np.uint8).reshape(-1),
+                                  _c(layer["d_scales"], np.uint8).reshape(-1),
+                                  _c(layer["d_bias"], np.float32).reshape(-1), n_threads, y)
+    assert rc == 0
+    return y

@@ -1,0 +1,410 @@
+// Device helpers shared by the kernels of the MXFP4 MoE path (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace moe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ scalar helpers
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// x = hi + lo, both bf16; a non-finite hi carries the value alone.
+__device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) {
+  hi = f32_to_bf16_rne(x);
+  float h = bf16_to_f32(hi);
+  lo = f32_to_bf16_rne(isfinite(h) ? x - h : 0.0f);
+}
+
+__device__ __forceinline__ float canon_nan(float v) {
+  return isnan(v) ? __uint_as_float(0x7FC00000u) : v;
+}
+
+// Rust f32::clamp: a NaN stays NaN.
+__device__ __forceinline__ float rclamp(float v, float lo, float hi) {
+  if (v < lo) v = lo;
+  if (v > hi) v = hi;
+  return v;
+}
+
+// E2M1 nibble -> f32 bits: sign | (e == 0 ? 0.5*m : 2^(e-1) * (1 + m/2)).
+__device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
+  uint32_t mag = n & 7u;
+  uint32_t bits = mag == 0 ? 0u : (mag == 1 ? 0x3F000000u : (((mag >> 1) + 126u) << 23) | ((mag & 1u) << 22));
+  return __uint_as_float(bits | ((n & 8u) << 28));
+}
+
+// GPT-OSS SwiGLU of session.rs:109-117: gate = min(g, L) (NaN-ignoring), up = clamp(u, +-L),
+// glu = gate / (1 + exp(-gate * 1.702)), h = (up + 1) * glu.
+__device__ __forceinline__ float swiglu(float g, float u, float limit) {
+  float gate = fminf(g, limit);
+  float up = rclamp(u, -limit, limit);
+  float glu = gate / (1.0f + expf(-gate * 1.702f));
+  return (up + 1.0f) * glu;
+}
+
+// 8 nibbles (one dword of a block) -> 8 bf16, element order preserved (low nibble first).
+__device__ __forceinline__ bf16x8 decode8(uint32_t w, float sc) {
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
+  uint4 u;
+  u.x = __builtin_bit_cast(uint32_t, p0);
+  u.y = __builtin_bit_cast(uint32_t, p1);
+  u.z = __builtin_bit_cast(uint32_t, p2);
+  u.w = __builtin_bit_cast(uint32_t, p3);
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Ranking of session.rs:822-825 made total: greater logit first, equal logits (including
+// +0 / -0) -> lower index first, NaN after every number.
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+  bool an = isnan(a), bn = isnan(b);
+  if (an || bn) return (an && bn) ? ia < ib : bn;
+  if (a > b) return true;
+  if (a < b) return false;
+  return ia < ib;
+}
+
+// Value of lane (lane ^ O) for a compile-time O: DPP quad permutes for 1 and 2, ds_swizzle
+// (bitmask mode) for 4..16, ds_bpermute for 32.
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+  const int i = __float_as_int(v);
+  if constexpr (O == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false));
+  else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false));
+  else if constexpr (O < 32) return __int_as_float(__builtin_amdgcn_ds_swizzle(i, 0x1F | (O << 10)));
+  else return __shfl_xor(v, 32);
+}
+
+// Xor butterfly p_l <- p_l + p_{l^o} for o = 32, 16, ..., 1; every lane ends with the same sum.
+__device__ __forceinline__ float wave_sum_xor(float p) {
+  p = p + xor_lane<32>(p);
+  p = p + xor_lane<16>(p);
+  p = p + xor_lane<8>(p);
+  p = p + xor_lane<4>(p);
+  p = p + xor_lane<2>(p);
+  p = p + xor_lane<1>(p);
+  return p;
+}
+
+__device__ __forceinline__ float wave_max(float m) {
+  m = fmaxf(m, xor_lane<32>(m));
+  m = fmaxf(m, xor_lane<16>(m));
+  m = fmaxf(m, xor_lane<8>(m));
+  m = fmaxf(m, xor_lane<4>(m));
+  m = fmaxf(m, xor_lane<2>(m));
+  m = fmaxf(m, xor_lane<1>(m));
+  return m;
+}
+
+// Canonical order: lane l accumulates k = l, l+64, ... (k < H) with fused multiply-adds; the
+// 64 partials are combined by a xor butterfly (32, 16, ..., 1); then the bias is added.
+// Device layout of the router ("lane-major"): for expert e and lane l the weights
+// W[e][l + 64 i], i = 0..KIp-1, are contiguous (KIp = ceil(H/64) rounded up to 8, zero
+// padded), so a lane reads its whole chain with KIp/8 16-byte loads. x is staged in LDS with
+// zeros past H; padded terms are fmaf(0, 0, p) = p exactly (p starts at +0 and can never
+// become -0), so the chain equals the unpadded one. NQ = KIp/8 (0: runtime loop).
+template <int NQ>
+__device__ __forceinline__ float router_dot(const uint16_t *w_lane, const float *s_x, int nq,
+                                            int lane) {
+  float p = 0.0f;
+  const uint4 *wq = reinterpret_cast<const uint4 *>(w_lane);
+  if (NQ > 0) {
+    uint4 v[NQ > 0 ? NQ : 1];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) v[q] = wq[q];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+      const uint32_t u[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+      for (int h = 0; h < 8; h++) {
+        const uint16_t b = (uint16_t)(u[h >> 1] >> (16 * (h & 1)));
+        p = __builtin_fmaf(bf16_to_f32(b), s_x[lane + 64 * (8 * q + h)], p);
+      }
+    }
+  } else {
+    for (int q = 0; q < nq; q++) {
+      const uint4 vq = wq[q];
+      const uint32_t u[4] = {vq.x, vq.y, vq.z, vq.w};
+      for (int h = 0; h < 8; h++) {
+        const uint16_t b = (uint16_t)(u[h >> 1] >> (16 * (h & 1)));
+        p = __builtin_fmaf(bf16_to_f32(b), s_x[lane + 64 * (8 * q + h)], p);
+      }
+    }
+  }
+  return wave_sum_xor(p);
+}
+
+// Router logits of RB experts e0 + r*estride (r < RB) for the calling wavefront, RNQ 16-byte
+// loads per lane chain, split in two so the loads can be issued early: router_load issues
+// every weight load of the batch; router_compute runs the RB chains interleaved, each in the
+// canonical order, and lane 0 writes s_logit[e] for e < E.
+template <int RNQ, int RB>
+struct RouterRegs {
+  uint4 v[RB][RNQ];
+};
+
+template <int RNQ, int RB>
+__device__ __forceinline__ void router_load(RouterRegs<RNQ, RB> &R, const uint16_t *rw, int E,
+                                            int e0, int estride, int lane) {
+#pragma unroll
+  for (int r = 0; r < RB; r++) {
+    const int e = min(e0 + r * estride, E - 1);
+    const uint4 *wq = reinterpret_cast<const uint4 *>(rw + ((size_t)e * 64 + lane) * RNQ * 8);
+#pragma unroll
+    for (int q = 0; q < RNQ; q++) R.v[r][q] = wq[q];
+  }
+}
+
+// xr[i] = x[lane + 64 i] (0 past H) for i < 8 * RNQ, in registers.
+template <int RNQ, int RB>
+__device__ __forceinline__ void router_compute(const RouterRegs<RNQ, RB> &R, const float *rb,
+                                               const float *xr, int E, int e0, int estride,
+                                               int lane, float *s_logit) {
+  float p[RB];
+#pragma unroll
+  for (int r = 0; r < RB; r++) p[r] = 0.0f;
+#pragma unroll
+  for (int q = 0; q < RNQ; q++) {
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+      const float xv = xr[8 * q + h];
+#pragma unroll
+      for (int r = 0; r < RB; r++) {
+        const uint4 &w = R.v[r][q];
+        const uint32_t u = h < 2 ? w.x : (h < 4 ? w.y : (h < 6 ? w.z : w.w));
+        p[r] = __builtin_fmaf(bf16_to_f32((uint16_t)(u >> (16 * (h & 1)))), xv, p[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RB; r++) p[r] = wave_sum_xor(p[r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+      const int e = e0 + r * estride;
+      if (e < E) s_logit[e] = canon_nan(p[r] + rb[e]);
+    }
+  }
+}
+
+// Epilogue of one 16-row tile x 8-entry chunk. acc holds rows 4*(lane/16)+i of column
+// lane%16 (entry (lane%16)/2, term hi/lo); hi and lo columns are summed across lane pairs.
+template <int MODE>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, const f32x4 &acc,
+                                              const uint8_t *rec, int beg, int c0, int nent,
+                                              int t, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  float r[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) r[i] = acc[i] + xor_lane<1>(acc[i]);
+  const int el = c0 + (j >> 1);
+  if ((j & 1) || el >= nent) return;
+  const int ge = beg + el;
+  const int r0 = t * 16 + g * 4;
+  if (MODE == GEMV_GATE_UP) {
+    const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
+    const int I = (int)a.d.rows / 2;
+    const float h0 = swiglu(r[0] + bias[r0], r[1] + bias[r0 + 1], a.limit);
+    const float h1 = swiglu(r[2] + bias[r0 + 2], r[3] + bias[r0 + 3], a.limit);
+    uint16_t hi0, lo0, hi1, lo1;
+    split_bf16(h0, hi0, lo0);
+    split_bf16(h1, hi1, lo1);
+    uint16_t *hs = reinterpret_cast<uint16_t *>(a.out) + (size_t)ge * 2 * I;
+    const int ii = r0 / 2;
+    *reinterpret_cast<uint32_t *>(hs + ii) = (uint32_t)hi0 | ((uint32_t)hi1 << 16);
+    *reinterpret_cast<uint32_t *>(hs + I + ii) = (uint32_t)lo0 | ((uint32_t)lo1 << 16);
+  } else if (MODE == GEMV_DOWN) {
+    const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
+    float *o = reinterpret_cast<float *>(a.out) + (size_t)ge * a.d.rows + r0;
+    float4 v4;
+    v4.x = canon_nan(rclamp(r[0] + bias[r0], -65504.0f, 65504.0f));
+    v4.y = canon_nan(rclamp(r[1] + bias[r0 + 1], -65504.0f, 65504.0f));
+    v4.z = canon_nan(rclamp(r[2] + bias[r0 + 2], -65504.0f, 65504.0f));
+    v4.w = canon_nan(rclamp(r[3] + bias[r0 + 3], -65504.0f, 65504.0f));
+    *reinterpret_cast<float4 *>(o) = v4;
+  } else {
+    float *o = reinterpret_cast<float *>(a.out) + (size_t)ge * a.d.rows + r0;
+    *reinterpret_cast<float4 *>(o) =
+        make_float4(canon_nan(r[0]), canon_nan(r[1]), canon_nan(r[2]), canon_nan(r[3]));
+  }
+}
+
+// ------------------------------------------------------------------ top-k of one token
+
+struct TopkCfg {
+  int E, k;
+  int adaptive, min_k;
+  float top1_min, margin_min, top2_mass;
+};
+
+// Integer key with the order of ranks_before: NaN lowest, -0 equal to +0, otherwise the float
+// order (sign-magnitude mapped to an unsigned order).
+__device__ __forceinline__ uint32_t rank_key(float v) {
+  if (isnan(v)) return 0u;
+  if (v == 0.0f) v = 0.0f;
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Softmax over all experts (session.rs:511-520: max ignoring NaN, exp, sum, divide if the sum
+// is positive; the sum is a tree here, so probabilities can differ from the sequential sum in
+// the last bits), order by ranks_before (session.rs:822-825 totalised, through rank_key),
+// optional adaptive count (session.rs:569-583), renormalisation over the kept slots
+// (session.rs:826-839). Wavefront 0 does the work with logits in registers and other lanes'
+// keys read with v_readlane; every thread of the block calls (two barriers). s_logit[E] is
+// read. On return s_order[s] holds the expert of slot s (-1 past the kept count), s_w[s] its
+// weight and *s_sel the kept count. s_pn: kMaxTopK floats of scratch.
+__device__ __forceinline__ void block_topk(const TopkCfg &c, const float *s_logit, float *s_pn,
+                                           int *s_order, float *s_w, int *s_sel) {
+  const int E = c.E;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    constexpr int Q = kMaxExperts / 64;
+    float l[Q], p[Q];
+    uint32_t key[Q];
+    float m = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+      const int e = lane + 64 * q;
+      l[q] = s_logit[min(e, E - 1)];
+      key[q] = rank_key(l[q]);
+      if (e < E) m = fmaxf(m, l[q]);
+    }
+    m = wave_max(m);
+    float ls = 0.0f;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+      p[q] = lane + 64 * q < E ? expf(l[q] - m) : 0.0f;
+      ls = ls + p[q];
+    }
+    const float sum = wave_sum_xor(ls);
+    const bool norm = sum > 0.0f;
+    int rank[Q] = {};
+#pragma unroll
+    for (int qf = 0; qf < Q; qf++) {
+      const int nf = min(64, E - 64 * qf);
+      for (int fl = 0; fl < nf; fl++) {
+        const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)key[qf], fl);
+        const int f = 64 * qf + fl;
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+          rank[q] += (kf > key[q] || (kf == key[q] && f < lane + 64 * q)) ? 1 : 0;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+      if (lane + 64 * q < E && rank[q] < c.k) {
+        s_order[rank[q]] = lane + 64 * q;
+        s_pn[rank[q]] = norm ? p[q] / sum : p[q];
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int kk = c.k < E ? c.k : E;
+    int sel = kk;
+    if (c.adaptive && kk > 1) {
+      const float p1 = s_pn[0], p2 = s_pn[1];
+      const float margin = fmaxf(p1 - p2, 0.0f);
+      if (p1 >= c.top1_min && margin >= c.margin_min)
+        sel = 1;
+      else if (p1 + p2 >= c.top2_mass)
+        sel = 2;
+      const int mk = c.min_k < kk ? c.min_k : kk;
+      if (sel < mk) sel = mk;
+      if (sel > kk) sel = kk;
+    }
+    float top_sum = 0.0f;
+    for (int s = 0; s < sel; s++) top_sum = top_sum + s_pn[s];
+    const bool ok = isfinite(top_sum) && top_sum > 0.0f;
+    for (int s = 0; s < c.k; s++) {
+      if (s < sel) {
+        s_w[s] = ok ? canon_nan(s_pn[s] / top_sum) : 1.0f / (float)sel;
+      } else {
+        s_order[s] = -1;
+        s_w[s] = 0.0f;
+      }
+    }
+    *s_sel = sel;
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ one 16-row MXFP4 tile
+
+// Registers of one tile: every 16-byte weight chunk and scale word a lane needs.
+template <int NSMAX>
+struct TileRegs {
+  uint4 raw[NSMAX];
+  uint32_t sw[(NSMAX + 3) / 4];
+};
+
+// Issues every weight and scale load of tile t of a resident matrix (layout.hpp). Lanes of
+// missing blocks (the partial last step) and !ok tiles load nothing and hold zeros.
+template <int NSMAX>
+__device__ __forceinline__ void tile_load(TileRegs<NSMAX> &r, const uint8_t *mat, const PackDims &d,
+                                          int t, bool ok, int lane) {
+  const size_t tt = ok ? (size_t)t : 0;
+  const uint4 *wp = reinterpret_cast<const uint4 *>(mat) + tt * 16 * d.nb;
+  const uint32_t *sp = reinterpret_cast<const uint32_t *>(mat + pack_weight_bytes(d)) + tt * d.nq * 64;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < (NSMAX + 3) / 4; q++) r.sw[q] = (ok && q < (int)d.nq) ? sp[q * 64 + lane] : 0u;
+#pragma unroll
+  for (int s = 0; s < NSMAX; s++) {
+    r.raw[s] = make_uint4(0u, 0u, 0u, 0u);
+    if (ok && s < (int)d.ns && 4 * s + g < (int)d.nb) r.raw[s] = wp[s * 64 + lane];
+  }
+}
+
+// MFMA sweep of a loaded tile against one B row pair in LDS (brow: the lane's hi or lo row of
+// K bf16 as uint4, valid when bv). Returns the lane's 4 accumulators (rows 4*(lane/16)+i of
+// column lane%16).
+template <int NSMAX>
+__device__ __forceinline__ f32x4 tile_mfma(const TileRegs<NSMAX> &r, const PackDims &d,
+                                           const uint4 *brow, bool bv, int lane) {
+  const int g = lane >> 4;
+  // four independent accumulators (one per 8-element slice of a block) keep the dependent
+  // MFMA chain a quarter as long; they are summed at the end
+  f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+#pragma unroll
+  for (int s = 0; s < NSMAX; s++) {
+    if (s < (int)d.ns) {
+      const int b = 4 * s + g;
+      const float sc = __uint_as_float(((r.sw[s / 4] >> (8 * (s % 4))) & 0xFFu) << 23);
+      const bf16x8 A0 = decode8(r.raw[s].x, sc), A1 = decode8(r.raw[s].y, sc);
+      const bf16x8 A2 = decode8(r.raw[s].z, sc), A3 = decode8(r.raw[s].w, sc);
+      uint4 b0 = make_uint4(0u, 0u, 0u, 0u), b1 = b0, b2 = b0, b3 = b0;
+      if (bv && b < (int)d.nb) {
+        b0 = brow[4 * b];
+        b1 = brow[4 * b + 1];
+        b2 = brow[4 * b + 2];
+        b3 = brow[4 * b + 3];
+      }
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, as_bf16x8(b0), acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, as_bf16x8(b1), acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A2, as_bf16x8(b2), acc2, 0, 0, 0);
+      acc3 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A3, as_bf16x8(b3), acc3, 0, 0, 0);
+    }
+  }
+  return (acc0 + acc1) + (acc2 + acc3);
+}
+
+}  // namespace moe

@@ -1,0 +1,609 @@
+// HIP kernels of the MXFP4 MoE path, written for gfx950 (CDNA4, wave64).
+//
+//   k_route        router GEMV in the canonical order + top-k + softmax renorm + bf16 split
+//                  (session.rs:495-520, :818-841)
+//   k_bucket       deterministic token -> expert grouping (stable counting sort)
+//   k_expert_gemv  MXFP4 x bf16(hi,lo) on v_mfma_f32_16x16x32_bf16, one wavefront per
+//                  16-row tile, with the gate_up SwiGLU epilogue (session.rs:101-117), the
+//                  down bias + clamp epilogue (session.rs:119-123) or a raw output
+//   k_combine      weighted sum over slots in rank order (session.rs:974-980)
+//   k_dequant_*    bit-exact decode of weights.rs:350-371 (checkpoint or resident layout)
+//   k_pack_*       checkpoint layout -> resident tile16 layout (layout.hpp)
+//
+// Numerics of the GEMV: the weight decode (v_cvt_scalef32_pk_bf16_fp4) is exact because
+// E2M1 * 2^k has at most two significant bits; activations enter as x = hi + lo with hi, lo
+// bf16 (16 significant bits, |x - (hi+lo)| <= 2^-17 |x|); products are exact and accumulate
+// in f32 inside the MFMA.
+#include <hip/hip_runtime.h>
+
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace moe {
+
+// ------------------------------------------------------------------ router + top-k
+
+constexpr int kRouteThreads = 1024;
+
+template <int KI>
+__global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
+  __shared__ float s_logit[kMaxExperts];
+  __shared__ float s_p[kMaxExperts];
+  __shared__ int s_order[kMaxTopK];
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int nw = kRouteThreads / 64;
+  const int H = a.H, E = a.E;
+  const int nq = ((H + 63) / 64 + 7) / 8;  // uint4 per lane chain
+  const int Hp = nq * 8 * 64;
+  const float *x = a.x + (size_t)t * H;
+  extern __shared__ float s_x[];  // Hp floats
+  uint16_t *xs = a.xsplit + (size_t)t * 2 * H;
+  for (int k = threadIdx.x; k < Hp; k += kRouteThreads) {
+    const float v = k < H ? x[k] : 0.0f;
+    s_x[k] = v;
+    if (k < H) {
+      uint16_t hi, lo;
+      split_bf16(v, hi, lo);
+      xs[k] = hi;
+      xs[H + k] = lo;
+    }
+  }
+  __syncthreads();
+  for (int e = wv; e < E; e += nw) {
+    const float p = router_dot<KI>(a.w + ((size_t)e * 64 + lane) * nq * 8, s_x, nq, lane);
+    if (lane == 0) s_logit[e] = canon_nan(p + a.bias[e]);
+  }
+  __syncthreads();
+
+  for (int e = threadIdx.x; e < E; e += kRouteThreads) a.logits[(size_t)t * E + e] = s_logit[e];
+  __shared__ float s_w[kMaxTopK];
+  __shared__ int s_sel;
+  const TopkCfg c{E, a.k, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
+  block_topk(c, s_logit, s_p, s_order, s_w, &s_sel);
+  if (threadIdx.x < a.k) {
+    const size_t o = (size_t)t * a.k + threadIdx.x;
+    a.idx[o] = s_order[threadIdx.x];
+    a.wts[o] = s_w[threadIdx.x];
+  }
+  if (a.fuse_bucket && threadIdx.x == 0) {  // single token: the expert list is the slot list
+    const int sel = s_sel;
+    *a.n_active = sel;
+    for (int s = 0; s < sel; s++) {
+      a.active_ids[s] = s_order[s];
+      a.active_off[s] = s;
+      a.entry_src[s] = 0;
+    }
+    a.active_off[sel] = sel;
+    for (int s = 0; s < a.k; s++) a.pos[s] = s < sel ? s : -1;
+  }
+}
+
+hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
+  if (a.E < 1 || a.E > kMaxExperts || a.k < 1 || a.k > kMaxTopK || a.k > a.E || a.T < 1 ||
+      a.H < 1 || (a.fuse_bucket && a.T != 1))
+    return hipErrorInvalidValue;
+  const int nq = ((a.H + 63) / 64 + 7) / 8;
+  const size_t lds = (size_t)nq * 8 * 64 * sizeof(float);
+  if (lds > 65536) return hipErrorInvalidValue;
+  const dim3 g(a.T), b(kRouteThreads);
+  switch (nq) {  // 2880 -> 45 chain terms -> 6 loads per lane
+    case 1: hipLaunchKernelGGL(k_route<1>, g, b, lds, s, a); break;
+    case 2: hipLaunchKernelGGL(k_route<2>, g, b, lds, s, a); break;
+    case 6: hipLaunchKernelGGL(k_route<6>, g, b, lds, s, a); break;
+    default: hipLaunchKernelGGL(k_route<0>, g, b, lds, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ bucketing
+
+// Groups the T*k (token, slot) entries by expert. Active experts are listed in ascending id;
+// entries of one expert are ordered by t*k + slot. pos[t*k + slot] = entry index (or -1).
+__global__ __launch_bounds__(1024) void k_bucket(const int32_t *idx, int T, int k, int E,
+                                                 int32_t *n_active, int32_t *active_ids,
+                                                 int32_t *active_off, int32_t *entry_src,
+                                                 int32_t *pos) {
+  __shared__ int s_count[kMaxExperts];
+  __shared__ int s_base[kMaxExperts];
+  __shared__ int s_wave[16][kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int N = T * k;
+  for (int e = tid; e < E; e += 1024) s_count[e] = 0;
+  for (int i = tid; i < 16 * kMaxExperts; i += 1024) (&s_wave[0][0])[i] = 0;
+  __syncthreads();
+  for (int n = tid; n < N; n += 1024) {
+    int e = idx[n];
+    if (e >= 0) atomicAdd(&s_count[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int na = 0, off = 0;
+    for (int e = 0; e < E; e++) {
+      s_base[e] = off;
+      if (s_count[e] > 0) {
+        active_ids[na] = e;
+        active_off[na] = off;
+        off += s_count[e];
+        na++;
+      }
+    }
+    active_off[na] = off;
+    *n_active = na;
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < N; c0 += 1024) {
+    const int n = c0 + tid;
+    const int e = n < N ? idx[n] : -1;
+    // lanes of this wavefront holding the same value (9-bit match through ballots)
+    const uint32_t v = (uint32_t)(e + 1);
+    uint64_t same = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 9; bit++) {
+      uint64_t b = __ballot((v >> bit) & 1u);
+      same &= ((v >> bit) & 1u) ? b : ~b;
+    }
+    const int rank_in_wave = __popcll(same & ((1ull << lane) - 1ull));
+    const bool leader = (same & ((1ull << lane) - 1ull)) == 0;
+    if (leader && e >= 0) s_wave[wv][e] = __popcll(same);
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += 1024) {  // exclusive prefix over wavefronts
+      int run = 0;
+      for (int w = 0; w < 16; w++) {
+        int c = s_wave[w][ee];
+        s_wave[w][ee] = run;
+        run += c;
+      }
+      s_count[ee] = run;  // this chunk's total for expert ee
+    }
+    __syncthreads();
+    if (e >= 0) {
+      int ge = s_base[e] + s_wave[wv][e] + rank_in_wave;
+      entry_src[ge] = n / k;
+      pos[n] = ge;
+    } else if (n < N) {
+      pos[n] = -1;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += 1024) s_base[ee] += s_count[ee];
+    for (int i = tid; i < 16 * kMaxExperts; i += 1024) (&s_wave[0][0])[i] = 0;
+    __syncthreads();
+  }
+}
+
+hipError_t launch_bucket(const int32_t *idx, int T, int k, int E, int32_t *n_active,
+                         int32_t *active_ids, int32_t *active_off, int32_t *entry_src,
+                         int32_t *pos, hipStream_t s) {
+  if (E < 1 || E > kMaxExperts || k < 1 || T < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(1024), 0, s, idx, T, k, E, n_active, active_ids,
+                     active_off, entry_src, pos);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ MXFP4 GEMV on MFMA
+
+// Small-batch variant (at most NE entries per expert, at most NSMAX steps per tile): a
+// workgroup is 4 wavefronts on 4 consecutive tiles of one expert. Each wavefront issues every
+// weight and scale load of its tile before computing, so a tile's 23 KB are in flight at
+// once; the workgroup stages its entries' B operands (hi/lo rows) in LDS first.
+template <int MODE, int NE, int NSMAX>
+__global__ __launch_bounds__(256) void k_expert_gemv_small(GemvArgs a) {
+  extern __shared__ uint4 s_b[];
+  constexpr int SBMAX = 3 * NE;  // staging loads per thread: NE * 2 rows of <= 384 uint4
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tiles = (int)a.d.tiles;
+  const int tgs = (tiles + 3) >> 2;
+  const int act = blockIdx.x / tgs;
+  const int t = (blockIdx.x - act * tgs) * 4 + wv;
+  if (act >= a.max_active) return;
+  // independent loads (one round trip); the arrays hold max_active (+1) entries
+  const int n_act = *a.n_active;
+  const int expert = a.active_ids[act];
+  const int beg = a.active_off[act];
+  int nent = a.active_off[act + 1] - beg;
+  if (act >= n_act) return;
+  if (nent > NE) nent = NE;
+  const uint8_t *rec = a.base + (size_t)expert * a.stride;
+  const uint8_t *mat = rec + a.mat_off;
+  const bool tile_ok = t < tiles;
+  const int j = lane & 15;
+  const int row_u4 = (int)a.d.nb * 4;  // uint4 per (entry, term) row of K bf16
+
+  // 1. B operand rows of this expert's entries (read first: the barrier waits only for them)
+  int src[NE];
+#pragma unroll
+  for (int e = 0; e < NE; e++)
+    src[e] = e < nent ? (a.entry_src ? a.entry_src[beg + e] : beg + e) : 0;
+  const int nstg = nent * 2 * row_u4;
+  uint4 stg[SBMAX];
+#pragma unroll
+  for (int i = 0; i < SBMAX; i++) {
+    // always a valid address (row 0 of entry 0 when idx is past the staged range)
+    const int idx = threadIdx.x + 256 * i;
+    const int ci = idx < nstg ? idx : 0;
+    const int e = ci / (2 * row_u4), r = ci - e * 2 * row_u4;
+    int se = src[0];
+#pragma unroll
+    for (int q = 1; q < NE; q++) se = (e == q) ? src[q] : se;
+    stg[i] = reinterpret_cast<const uint4 *>(a.bsrc)[(size_t)se * 2 * row_u4 + r];
+  }
+  // 2. every weight and scale load of the tile
+  TileRegs<NSMAX> r;
+  tile_load<NSMAX>(r, mat, a.d, t, tile_ok, lane);
+#pragma unroll
+  for (int i = 0; i < SBMAX; i++) {
+    const int idx = threadIdx.x + 256 * i;
+    if (idx < nstg) s_b[idx] = stg[i];
+  }
+  __syncthreads();
+  if (!tile_ok) return;
+
+  // 3. MFMA sweep over the tile
+  const int ent = j >> 1, term = j & 1;
+  const f32x4 acc = tile_mfma<NSMAX>(r, a.d, s_b + (size_t)(ent * 2 + term) * row_u4, ent < nent, lane);
+  gemv_epilogue<MODE>(a, acc, rec, beg, 0, nent, t, lane);
+}
+
+constexpr int kSmallNsMax = 24;  // tiles of up to 96 blocks (K <= 3072)
+
+template <int MODE, int NE>
+static hipError_t launch_small(const GemvArgs &a, hipStream_t s) {
+  const size_t lds = (size_t)NE * 2 * a.d.nb * 32 * 2;
+  static bool attr_set = false;
+  if (!attr_set && lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_expert_gemv_small<MODE, NE, kSmallNsMax>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const size_t wgs = (size_t)a.max_active * ((a.d.tiles + 3) / 4);
+  hipLaunchKernelGGL((k_expert_gemv_small<MODE, NE, kSmallNsMax>), dim3((unsigned)wgs), dim3(256),
+                     lds, s, a);
+  return hipGetLastError();
+}
+
+// One wavefront computes one 16-row tile of one active expert's matrix against the B
+// operands of that expert's entries, CH chunks of 8 entries at a time. MFMA columns:
+// column j of a chunk is entry j/2, term j%2 (hi, lo). The MFMA result for lane l holds
+// rows 4*(l/16)+i (i = 0..3) of column l%16; hi and lo columns are summed across lane pairs.
+template <int MODE, int CH>
+__global__ __launch_bounds__(256) void k_expert_gemv(GemvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tiles = (int)a.d.tiles;
+  const int act = wid / tiles;
+  const int t = wid - act * tiles;
+  if (act >= a.max_active) return;
+  if (act >= *a.n_active) return;
+  const int expert = a.active_ids[act];
+  const int beg = a.active_off[act];
+  const int nent = a.active_off[act + 1] - beg;
+  const uint8_t *rec = a.base + (size_t)expert * a.stride;
+  const uint8_t *mat = rec + a.mat_off;
+  const int nb = (int)a.d.nb, ns = (int)a.d.ns, nq = (int)a.d.nq;
+  const uint4 *wp = reinterpret_cast<const uint4 *>(mat) + (size_t)t * 16 * nb;
+  const uint32_t *sp = reinterpret_cast<const uint32_t *>(mat + pack_weight_bytes(a.d)) +
+                       (size_t)t * nq * 64;
+  const int g = lane >> 4, j = lane & 15;
+  const size_t K = (size_t)nb * 32;
+
+  for (int c0 = 0; c0 < nent; c0 += 8 * CH) {
+    f32x4 acc[CH];
+    const uint16_t *bp[CH];
+    bool bval[CH];
+#pragma unroll
+    for (int cc = 0; cc < CH; cc++) {
+      acc[cc] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const int el = c0 + 8 * cc + (j >> 1);
+      bval[cc] = el < nent;
+      const int src = bval[cc] ? (a.entry_src ? a.entry_src[beg + el] : beg + el) : 0;
+      bp[cc] = a.bsrc + ((size_t)src * 2 + (j & 1)) * K;
+    }
+    for (int q = 0; q < nq; q++) {
+      const uint32_t sw = sp[q * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int s = q * 4 + i;
+        if (s >= ns) break;
+        const int b = 4 * s + g;
+        const bool v = b < nb;
+        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+        if (v) raw = wp[s * 64 + lane];
+        const float sc = __uint_as_float(((sw >> (8 * i)) & 0xFFu) << 23);
+        const bf16x8 A0 = decode8(raw.x, sc), A1 = decode8(raw.y, sc);
+        const bf16x8 A2 = decode8(raw.z, sc), A3 = decode8(raw.w, sc);
+#pragma unroll
+        for (int cc = 0; cc < CH; cc++) {
+          uint4 b0 = make_uint4(0u, 0u, 0u, 0u), b1 = b0, b2 = b0, b3 = b0;
+          if (v && bval[cc]) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(bp[cc] + 32 * (size_t)b);
+            b0 = src[0];
+            b1 = src[1];
+            b2 = src[2];
+            b3 = src[3];
+          }
+          acc[cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, as_bf16x8(b0), acc[cc], 0, 0, 0);
+          acc[cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, as_bf16x8(b1), acc[cc], 0, 0, 0);
+          acc[cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A2, as_bf16x8(b2), acc[cc], 0, 0, 0);
+          acc[cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A3, as_bf16x8(b3), acc[cc], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < CH; cc++) gemv_epilogue<MODE>(a, acc[cc], rec, beg, c0 + 8 * cc, nent, t, lane);
+  }
+}
+
+template <int MODE>
+static hipError_t launch_gemv_mode(const GemvArgs &a, hipStream_t s) {
+  if (a.d.ns <= (uint32_t)kSmallNsMax && a.max_entries_per_expert <= 8) {
+    if (a.max_entries_per_expert <= 1) return launch_small<MODE, 1>(a, s);
+    if (a.max_entries_per_expert <= 2) return launch_small<MODE, 2>(a, s);
+    if (a.max_entries_per_expert <= 4) return launch_small<MODE, 4>(a, s);
+    return launch_small<MODE, 8>(a, s);
+  }
+  const size_t waves = (size_t)a.max_active * a.d.tiles;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  if (a.max_entries_per_expert <= 8)
+    hipLaunchKernelGGL((k_expert_gemv<MODE, 1>), grid, block, 0, s, a);
+  else if (a.max_entries_per_expert <= 16)
+    hipLaunchKernelGGL((k_expert_gemv<MODE, 2>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((k_expert_gemv<MODE, 4>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv(GemvMode mode, const GemvArgs &a, hipStream_t s) {
+  if (a.d.rows == 0 || a.d.rows % 16 || a.d.nb == 0 || a.max_active < 1 || !a.base || !a.bsrc ||
+      !a.out || !a.n_active || !a.active_ids || !a.active_off)
+    return hipErrorInvalidValue;
+  if ((size_t)a.max_active * a.d.tiles > (size_t)0x7FFFFFFF * 4) return hipErrorInvalidValue;
+  switch (mode) {
+    case GEMV_GATE_UP: return launch_gemv_mode<GEMV_GATE_UP>(a, s);
+    case GEMV_DOWN: return launch_gemv_mode<GEMV_DOWN>(a, s);
+    default: return launch_gemv_mode<GEMV_RAW>(a, s);
+  }
+}
+
+// ------------------------------------------------------------------ combine
+
+// y[t, d] = sum over slots s (rank order) of w[t, s] * o[pos[t, s], d], accumulated from 0
+// with separate rounding of each product and sum (session.rs:975-980). skip_nonfinite drops
+// non-finite o elements (moe_dispatch.rs:598-601).
+__global__ __launch_bounds__(256) void k_combine(const float *o, const int32_t *pos,
+                                                 const float *w, int T, int k, int H,
+                                                 int skip_nonfinite, float *y) {
+  const int h4 = H / 4;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)T * h4) return;
+  const int t = (int)(i / h4), d4 = (int)(i % h4);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = 0; s < k; s++) {
+    const int p = pos[(size_t)t * k + s];
+    if (p < 0) continue;
+    const float ws = w[(size_t)t * k + s];
+    const float4 v = reinterpret_cast<const float4 *>(o + (size_t)p * H)[d4];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      if (skip_nonfinite && !isfinite(vv[c])) continue;
+      acc[c] = acc[c] + ws * vv[c];
+    }
+  }
+  reinterpret_cast<float4 *>(y + (size_t)t * H)[d4] =
+      make_float4(canon_nan(acc[0]), canon_nan(acc[1]), canon_nan(acc[2]), canon_nan(acc[3]));
+}
+
+hipError_t launch_combine(const float *o, const int32_t *pos, const float *w, int T, int k, int H,
+                          int skip_nonfinite, float *y, hipStream_t s) {
+  if (H % 4 || T < 1 || k < 1) return hipErrorInvalidValue;
+  const size_t n = (size_t)T * (H / 4);
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, o, pos, w, T,
+                     k, H, skip_nonfinite, y);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ split
+
+__global__ __launch_bounds__(256) void k_split(const float *x, size_t n_rows, size_t K,
+                                               uint16_t *xs) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_rows * K) return;
+  const size_t r = i / K, k = i % K;
+  uint16_t hi, lo;
+  split_bf16(x[i], hi, lo);
+  xs[r * 2 * K + k] = hi;
+  xs[r * 2 * K + K + k] = lo;
+}
+
+hipError_t launch_split(const float *x, size_t n_rows, size_t K, uint16_t *xsplit, hipStream_t s) {
+  const size_t n = n_rows * K;
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_split, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n_rows, K,
+                     xsplit);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ bit-exact dequant
+
+__device__ __forceinline__ void decode_block_f32(uint4 raw, uint32_t sbyte, float *out) {
+  const float sc = __uint_as_float(sbyte << 23);  // weights.rs:359
+  const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+  float4 *o4 = reinterpret_cast<float4 *>(out);
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    float v[8];
+#pragma unroll
+    for (int bb = 0; bb < 4; bb++) {
+      const uint32_t byte = (wv[d] >> (8 * bb)) & 0xFFu;
+      v[2 * bb] = canon_nan(e2m1_to_f32(byte & 0xFu) * sc);
+      v[2 * bb + 1] = canon_nan(e2m1_to_f32(byte >> 4) * sc);
+    }
+    o4[2 * d] = make_float4(v[0], v[1], v[2], v[3]);
+    o4[2 * d + 1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_dequant_hf(const uint8_t *blocks, const uint8_t *scales,
+                                                    size_t n_blocks, float *out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_blocks) return;
+  const uint4 raw = reinterpret_cast<const uint4 *>(blocks)[i];
+  decode_block_f32(raw, scales[i], out + i * 32);
+}
+
+hipError_t launch_dequant_hf(const uint8_t *blocks, const uint8_t *scales, size_t rows,
+                             size_t cols, float *out, hipStream_t s) {
+  if (cols % 32) return hipErrorInvalidValue;
+  const size_t n = rows * (cols / 32);
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_dequant_hf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, blocks,
+                     scales, n, out);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_dequant_packed(const uint8_t *packed, PackDims d,
+                                                        float *out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)d.rows * d.nb) return;
+  const size_t row = i / d.nb;
+  const uint32_t b = (uint32_t)(i % d.nb);
+  const size_t t = row / 16;
+  const uint32_t rl = (uint32_t)(row % 16), s = b / 4, g = b % 4, l = 16 * g + rl;
+  const uint4 raw = reinterpret_cast<const uint4 *>(packed)[t * 16 * d.nb + 64 * s + l];
+  const uint32_t *sw = reinterpret_cast<const uint32_t *>(packed + pack_weight_bytes(d));
+  const uint32_t word = sw[(t * d.nq + s / 4) * 64 + l];
+  decode_block_f32(raw, (word >> (8 * (s % 4))) & 0xFFu, out + i * 32);
+}
+
+hipError_t launch_dequant_packed(const uint8_t *packed, size_t rows, size_t cols, float *out,
+                                 hipStream_t s) {
+  if (cols % 32 || rows % 16) return hipErrorInvalidValue;
+  const PackDims d = pack_dims(rows, cols);
+  const size_t n = rows * d.nb;
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_dequant_packed, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, packed,
+                     d, out);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ repack
+
+__global__ __launch_bounds__(256) void k_pack_weights(const uint8_t *blocks, PackDims d,
+                                                      uint8_t *packed) {
+  const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;  // destination chunk
+  if (c >= (size_t)d.rows * d.nb) return;
+  const size_t per_tile = (size_t)16 * d.nb;
+  const size_t t = c / per_tile;
+  const uint32_t p = (uint32_t)(c % per_tile), s = p / 64, l = p % 64;
+  const size_t row = t * 16 + (l & 15);
+  const uint32_t b = 4 * s + (l >> 4);
+  reinterpret_cast<uint4 *>(packed)[c] =
+      reinterpret_cast<const uint4 *>(blocks)[row * d.nb + b];
+}
+
+__global__ __launch_bounds__(256) void k_pack_scales(const uint8_t *scales, PackDims d,
+                                                     uint8_t *packed) {
+  const size_t wi = (size_t)blockIdx.x * 256 + threadIdx.x;  // destination word
+  if (wi >= (size_t)d.tiles * d.nq * 64) return;
+  const size_t t = wi / ((size_t)d.nq * 64);
+  const uint32_t q = (uint32_t)((wi / 64) % d.nq), l = (uint32_t)(wi % 64);
+  const size_t row = t * 16 + (l & 15);
+  uint32_t word = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < 4; i++) {
+    const uint32_t s = 4 * q + i, b = 4 * s + (l >> 4);
+    if (s < d.ns && b < d.nb) word |= (uint32_t)scales[row * d.nb + b] << (8 * i);
+  }
+  reinterpret_cast<uint32_t *>(packed + pack_weight_bytes(d))[wi] = word;
+}
+
+hipError_t launch_pack(const uint8_t *blocks, const uint8_t *scales, size_t rows, size_t cols,
+                       uint8_t *packed, hipStream_t s) {
+  if (cols % 32 || rows % 16 || !rows || !cols) return hipErrorInvalidValue;
+  const PackDims d = pack_dims(rows, cols);
+  const size_t nc = (size_t)d.rows * d.nb, nw = (size_t)d.tiles * d.nq * 64;
+  hipLaunchKernelGGL(k_pack_weights, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s, blocks,
+                     d, packed);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_pack_scales, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, scales,
+                     d, packed);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ synthetic data
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void k_synth(void *dst, size_t n, int kind, uint64_t seed,
+                                               float a, float b) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t r = splitmix64(seed * 0xD1342543DE82EF95ull + i);
+  if (kind == 0) {
+    const uint32_t lo = (uint32_t)a, hi = (uint32_t)b;
+    reinterpret_cast<uint8_t *>(dst)[i] = (uint8_t)(lo + (uint32_t)(r % (uint64_t)(hi - lo + 1)));
+    return;
+  }
+  const uint64_t r2 = splitmix64(r ^ 0x5851F42D4C957F2Dull);
+  const float u1 = ((float)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  const float u2 = (float)(r2 >> 40) * (1.0f / 16777216.0f);
+  const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2) * a;
+  if (kind == 1)
+    reinterpret_cast<uint16_t *>(dst)[i] = f32_to_bf16_rne(z);
+  else if (kind == 2)
+    reinterpret_cast<float *>(dst)[i] = z;
+  else
+    reinterpret_cast<float *>(dst)[i] = bf16_to_f32(f32_to_bf16_rne(z));
+}
+
+hipError_t launch_synth(void *dst, size_t n, int kind, uint64_t seed, float a, float b,
+                        hipStream_t s) {
+  if (kind < 0 || kind > 3) return hipErrorInvalidValue;
+  if (kind == 0 && !(a >= 0.0f && b <= 255.0f && a <= b)) return hipErrorInvalidValue;
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_synth, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, n, kind,
+                     seed, a, b);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ LM head (f32 GEMV)
+
+// logits[v] = W[v, :] . x ; one wavefront per row, float4 loads, xor-butterfly reduction.
+__global__ __launch_bounds__(256) void k_lm_head(const float *w, const float *x, size_t vocab,
+                                                 size_t H, float *y) {
+  const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= vocab) return;
+  const float4 *wr = reinterpret_cast<const float4 *>(w + row * H);
+  const float4 *xv = reinterpret_cast<const float4 *>(x);
+  float acc = 0.0f;
+  for (size_t k = lane; k < H / 4; k += 64) {
+    const float4 a = wr[k], b = xv[k];
+    acc = __builtin_fmaf(a.x, b.x, acc);
+    acc = __builtin_fmaf(a.y, b.y, acc);
+    acc = __builtin_fmaf(a.z, b.z, acc);
+    acc = __builtin_fmaf(a.w, b.w, acc);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o);
+  if (lane == 0) y[row] = acc;
+}
+
+hipError_t launch_lm_head(const float *w, const float *x, size_t vocab, size_t H, float *y,
+                          hipStream_t s) {
+  if (H % 4 || !vocab) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_lm_head, dim3((unsigned)((vocab + 3) / 4)), dim3(256), 0, s, w, x, vocab,
+                     H, y);
+  return hipGetLastError();
+}
+
+}  // namespace moe

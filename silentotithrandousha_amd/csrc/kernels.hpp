@@ -1,0 +1,92 @@
+// Kernel launch interface (host side). Every launcher checks its own shape assumptions
+// before enqueuing and returns the HIP error of the launch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "layout.hpp"
+
+namespace moe {
+
+constexpr int kMaxExperts = 256;  // router / bucketing LDS tables
+constexpr int kMaxTopK = 16;
+
+enum GemvMode { GEMV_GATE_UP = 0, GEMV_DOWN = 1, GEMV_RAW = 2 };
+
+struct RouteArgs {
+  const uint16_t *w;     // lane-major router: [E][64][KIp] bf16 bits (see router_dot)
+  const float *bias;     // [E]
+  const float *x;        // [T, H]
+  int T, E, H, k;
+  int adaptive, min_k;
+  float top1_min, margin_min, top2_mass;
+  float *logits;         // [T, E]
+  int32_t *idx;          // [T, k]
+  float *wts;            // [T, k]
+  uint16_t *xsplit;      // [T, 2, H] bf16 hi / lo
+  int fuse_bucket;       // T == 1: also write the expert list
+  int32_t *n_active, *active_ids, *active_off, *entry_src, *pos;
+};
+
+struct GemvArgs {
+  const uint8_t *base;     // first expert record of the region
+  size_t stride;           // bytes between expert records
+  size_t mat_off;          // packed matrix offset inside a record
+  size_t bias_off;         // f32 bias offset inside a record (ignored for GEMV_RAW)
+  PackDims d;              // matrix dimensions
+  const int32_t *n_active; // device scalar: active experts this call
+  const int32_t *active_ids, *active_off;
+  const int32_t *entry_src;  // B row of each entry (NULL: the entry itself)
+  const uint16_t *bsrc;      // [rows_b, 2, K] bf16 hi/lo operands, K = d.nb * 32
+  void *out;                 // GATE_UP: u16 [entry, 2, rows/2]; DOWN/RAW: f32 [entry, rows]
+  float limit;
+  int max_active;            // grid covers max_active * d.tiles wavefronts
+  int max_entries_per_expert;
+};
+
+// Single-token MoE layer in two launches (decode.hip).
+struct DecodeArgs {
+  const uint16_t *rw;  // lane-major router (see router_dot)
+  const float *rb;     // [E]
+  int rnq, Hr;         // 16-byte loads per router lane chain; router x length (64 * 8 * rnq)
+  const uint8_t *base; // expert records of the layer
+  size_t stride, gu_off, dn_off, gub_off, dnb_off;
+  PackDims gu, dn;
+  int H, I, E, k;
+  float limit;
+  int adaptive, min_k;
+  float top1_min, margin_min, top2_mass;
+  const float *x;      // [H]
+  float *y;            // [H]
+  float *logits;       // [E]   written by gate_up block 0
+  int32_t *idx;        // [k]   written by gate_up block 0, read by down
+  float *wts;          // [k]
+  uint16_t *hsplit;    // [k, 2, I]
+  int n_gu_wg_per_slot;
+};
+
+bool decode_supported(const DecodeArgs &a);
+hipError_t launch_decode_gate_up(const DecodeArgs &a, hipStream_t s);
+hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
+
+hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+hipError_t launch_bucket(const int32_t *idx, int T, int k, int E, int32_t *n_active,
+                         int32_t *active_ids, int32_t *active_off, int32_t *entry_src,
+                         int32_t *pos, hipStream_t s);
+hipError_t launch_gemv(GemvMode mode, const GemvArgs &a, hipStream_t s);
+hipError_t launch_combine(const float *o, const int32_t *pos, const float *w, int T, int k, int H,
+                          int skip_nonfinite, float *y, hipStream_t s);
+hipError_t launch_split(const float *x, size_t n_rows, size_t K, uint16_t *xsplit, hipStream_t s);
+hipError_t launch_dequant_hf(const uint8_t *blocks, const uint8_t *scales, size_t rows,
+                             size_t cols, float *out, hipStream_t s);
+hipError_t launch_dequant_packed(const uint8_t *packed, size_t rows, size_t cols, float *out,
+                                 hipStream_t s);
+hipError_t launch_pack(const uint8_t *blocks, const uint8_t *scales, size_t rows, size_t cols,
+                       uint8_t *packed, hipStream_t s);
+hipError_t launch_synth(void *dst, size_t n, int kind, uint64_t seed, float a, float b,
+                        hipStream_t s);
+hipError_t launch_lm_head(const float *w, const float *x, size_t vocab, size_t H, float *y,
+                          hipStream_t s);
+
+}  // namespace moe

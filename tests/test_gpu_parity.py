@@ -1,0 +1,356 @@
+"""GPU parity tests: the HIP path through the C ABI against the CPU oracle.
+
+Bar: bit-exact for the MXFP4 decode, the router logits and the top-k indices; 1e-3 relative
+L2 (REL_L2_TOL) for matmul outputs against the fp32 reference path on the same inputs.
+"""
+import numpy as np
+import pytest
+
+from silentotithrandousha_amd import DeviceBuffer, GpuMoeDispatcher, mxfp4_dequant, mxfp4_matvec, mxfp4_pack
+from silentotithrandousha_amd import synthetic as syn
+from tests.helpers import REL_L2_TOL, assert_bit_exact, assert_rel_l2, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+H20, I20, E20 = 2880, 2880, 32
+
+
+def exhaustive_mxfp4():
+    """256 rows (one per E8M0 byte) x 1 block whose 16 bytes hold every nibble twice."""
+    blocks = np.zeros((256, 1, 16), np.uint8)
+    for j in range(16):
+        blocks[:, 0, j] = j | ((15 - j) << 4)
+    scales = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    return blocks, scales
+
+
+@pytest.fixture(scope="module")
+def layer20():
+    return syn.make_layer(H20, I20, E20, seed=20)
+
+
+@pytest.fixture(scope="module")
+def disp20(layer20):
+    d = GpuMoeDispatcher(H20, I20, 7.0)
+    d.preload_layer(0, layer20)
+    yield d
+    d.close()
+
+
+# ---------------------------------------------------------------- decode
+
+def test_dequant_exhaustive_bit_exact(orc):
+    blocks, scales = exhaustive_mxfp4()
+    got = mxfp4_dequant(blocks, scales, 256, 32)
+    want = orc.dequant_mxfp4(blocks, scales, 256, 32)
+    assert_bit_exact(got, want, "16x256 nibble/scale table")
+
+
+def test_dequant_random_matrix_bit_exact(orc):
+    rng = np.random.default_rng(1)
+    rows, cols = 96, 2880
+    blocks = rng.integers(0, 256, size=(rows, cols // 32, 16), dtype=np.uint8)
+    scales = rng.integers(0, 256, size=(rows, cols // 32), dtype=np.uint8)
+    assert_bit_exact(mxfp4_dequant(blocks, scales, rows, cols),
+                     orc.dequant_mxfp4(blocks, scales, rows, cols), "random 96x2880")
+
+
+def test_resident_copy_lossless(orc):
+    """preload repacks; decoding the resident copy gives the checkpoint decode bit for bit."""
+    H, I, E = 256, 128, 2
+    L = syn.make_layer(H, I, E, seed=3, router=False)
+    rng = np.random.default_rng(4)
+    L["gu_scales"] = rng.integers(0, 256, size=L["gu_scales"].shape, dtype=np.uint8)
+    L["d_scales"] = rng.integers(0, 256, size=L["d_scales"].shape, dtype=np.uint8)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    for e in range(E):
+        gu = d.dequant_expert(0, e, 0)
+        dn = d.dequant_expert(0, e, 1)
+        assert_bit_exact(gu, orc.dequant_mxfp4(L["gu_blocks"][e], L["gu_scales"][e], 2 * I, H),
+                         f"gate_up expert {e}")
+        assert_bit_exact(dn, orc.dequant_mxfp4(L["d_blocks"][e], L["d_scales"][e], H, I),
+                         f"down expert {e}")
+    d.close()
+
+
+# ---------------------------------------------------------------- MXFP4 matvec (config 1)
+
+def _matvec(disp, blocks, scales, rows, cols, x):
+    b = DeviceBuffer.from_array(blocks)
+    s = DeviceBuffer.from_array(scales)
+    packed = mxfp4_pack(b, s, rows, cols)
+    xd = DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
+    yd = DeviceBuffer(rows * 4)
+    mxfp4_matvec(disp, packed, rows, cols, xd, yd)
+    disp.synchronize()
+    return yd.download(np.float32, rows)
+
+
+def test_matvec_config1(orc):
+    rows = cols = 2880
+    rng = np.random.default_rng(11)
+    blocks = rng.integers(0, 256, size=(rows, cols // 32, 16), dtype=np.uint8)
+    scales = rng.integers(118, 131, size=(rows, cols // 32), dtype=np.uint8)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    d = GpuMoeDispatcher(cols, cols, 7.0)
+    got = _matvec(d, blocks, scales, rows, cols, x)
+    want = orc.mxfp4_matvec(blocks, scales, rows, cols, x)
+    e = assert_rel_l2(got, want, "2880x2880 MXFP4 matvec")
+    assert e < 1e-5, f"matvec error {e:.2e} larger than the hi/lo split allows"
+    d.close()
+
+
+def test_matvec_one_hot_columns_exact(orc):
+    """x = e_k returns column k of W exactly: the in-kernel decode is bit-exact (up to the
+    sign of zero, which a sum cannot carry)."""
+    rows, cols = 64, 256
+    rng = np.random.default_rng(12)
+    blocks = rng.integers(0, 256, size=(rows, cols // 32, 16), dtype=np.uint8)
+    scales = rng.integers(100, 160, size=(rows, cols // 32), dtype=np.uint8)
+    W = orc.dequant_mxfp4(blocks, scales, rows, cols)
+    d = GpuMoeDispatcher(cols, cols, 7.0)
+    for k in [0, 1, 2, 7, 8, 31, 32, 33, 100, 255]:
+        x = np.zeros(cols, np.float32)
+        x[k] = 1.0
+        got = _matvec(d, blocks, scales, rows, cols, x)
+        assert np.array_equal(got, W[:, k]), f"column {k}"
+    d.close()
+
+
+def test_matvec_ragged_shapes(orc):
+    """Block counts that are not a multiple of 4 (partial last step) and of 16 (partial
+    last scale word)."""
+    rng = np.random.default_rng(13)
+    d = GpuMoeDispatcher(32, 32, 7.0)
+    for rows, nb in [(16, 1), (32, 2), (16, 3), (48, 5), (16, 17), (32, 90)]:
+        cols = 32 * nb
+        blocks = rng.integers(0, 256, size=(rows, nb, 16), dtype=np.uint8)
+        scales = rng.integers(118, 131, size=(rows, nb), dtype=np.uint8)
+        x = rng.normal(0, 1, cols).astype(np.float32)
+        got = _matvec(d, blocks, scales, rows, cols, x)
+        assert_rel_l2(got, orc.mxfp4_matvec(blocks, scales, rows, cols, x), f"{rows}x{cols}",
+                      tol=1e-5)
+    d.close()
+
+
+def test_matvec_edge_scales(orc):
+    """E8M0 bytes 0 (scale +0.0) and 255 (scale +inf in the reference decode, NaN in the OCP
+    MX spec). Rows touching a 255 block are non-finite exactly where the fp32 path is; the
+    GEMV does not promise the reference's choice between +-inf and NaN there, because the
+    activation enters as hi + lo and inf * lo can be inf * 0 (the bit-exact dequant kernel
+    keeps the reference's +inf)."""
+    rows, cols = 32, 64
+    rng = np.random.default_rng(14)
+    blocks = rng.integers(0, 256, size=(rows, 2, 16), dtype=np.uint8)
+    scales = rng.integers(120, 128, size=(rows, 2), dtype=np.uint8)
+    scales[3, 0] = 0
+    scales[5, 1] = 0
+    scales[9, 0] = 255
+    blocks[9, 0, :] = 0x22  # no zero nibbles: +-inf products only
+    scales[11, 1] = 255     # contains zero nibbles: 0 * inf = NaN
+    blocks[11, 1, 0] = 0x10
+    x = np.abs(rng.normal(0, 1, cols).astype(np.float32)) + 0.5
+    d = GpuMoeDispatcher(cols, cols, 7.0)
+    got = _matvec(d, blocks, scales, rows, cols, x)
+    want = orc.mxfp4_matvec(blocks, scales, rows, cols, x)
+    assert np.array_equal(np.isfinite(got), np.isfinite(want)), (got[[9, 11]], want[[9, 11]])
+    assert not np.isfinite(want[9]) and not np.isfinite(want[11])
+    fin = np.isfinite(want)
+    assert rel_l2(got[fin], want[fin]) < 1e-5
+    d.close()
+
+
+# ---------------------------------------------------------------- router + top-k
+
+def test_router_logits_and_topk_bit_exact(orc, disp20, layer20):
+    x = syn.hidden(16, H20, seed=21)
+    idx, w, logits = disp20.router_topk(0, x, 4, want_logits=True, n_experts=E20)
+    want_logits = orc.router_logits(layer20["router_w"], layer20["router_b"], x, E20, H20)
+    assert_bit_exact(logits, want_logits, "router logits (canonical order)")
+    widx, ww, _, _ = orc.topk(want_logits, 4)
+    assert np.array_equal(idx, widx)
+    assert np.max(np.abs(w - ww) / ww) < 1e-6
+    assert np.allclose(w.sum(1), 1.0, atol=1e-6)
+
+
+def test_topk_ties_and_nan(orc):
+    """Equal logits rank by lower index; NaN logits rank last (session.rs:822-825 order,
+    totalised)."""
+    H, E = 64, 8
+    w = np.zeros((E, H), np.float32)
+    w[:, 0] = [0.5, 1.0, 1.0, 0.25, 1.0, -1.0, 0.0, 0.75]
+    wb = syn.bf16_bits(w)
+    wb[6, 1] = 0x7FC0  # NaN weight -> NaN logit for expert 6
+    b = np.zeros(E, np.float32)
+    L = syn.make_layer(H, 32, E, seed=5, router=False)
+    L["router_w"], L["router_b"] = wb, b
+    d = GpuMoeDispatcher(H, 32, 7.0)
+    d.preload_layer(0, L)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = 2.0
+    x[0, 1] = 1.0
+    for k in (1, 3, 4, 8):
+        idx, ww, logits = d.router_topk(0, x, k, want_logits=True, n_experts=E)
+        widx, www, _, _ = orc.topk(orc.router_logits(wb, b, x, E, H), k)
+        assert np.array_equal(idx, widx), (k, idx, widx)
+        assert list(idx[0][:3]) == [1, 2, 4][:k]
+    assert np.isnan(logits[0, 6]) and idx[0, -1] == 6
+    d.close()
+
+
+# ---------------------------------------------------------------- expert FFN
+
+@pytest.mark.parametrize("scales", [(118, 130), (108, 114)], ids=["baseline", "mild"])
+def test_expert_preloaded_matches_fp32(orc, scales):
+    L = syn.make_layer(H20, I20, 2, seed=30 + scales[0], scale_lo=scales[0], scale_hi=scales[1],
+                       router=False)
+    d = GpuMoeDispatcher(H20, I20, 7.0)
+    d.preload_layer(0, L)
+    x = syn.hidden(1, H20, seed=31)[0]
+    for e in range(2):
+        got = d.dispatch_expert_preloaded(x, 0, e)
+        want = orc.expert_ffn(x, *syn.expert_slice(L, e), H20, I20)
+        assert_rel_l2(got, want[0], f"expert {e} scales {scales}")
+    d.close()
+
+
+def test_dispatch_expert_raw_and_batched(orc):
+    H, I = 512, 256
+    L = syn.make_layer(H, I, 3, seed=40, scale_lo=112, scale_hi=120, router=False)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    x = syn.hidden(1, H, seed=41)[0]
+    outs = []
+    for e in range(3):
+        got = d.dispatch_expert(x, *syn.expert_slice(L, e))
+        want = orc.expert_ffn(x, *syn.expert_slice(L, e), H, I)[0]
+        assert_rel_l2(got, want, f"dispatch_expert {e}")
+        outs.append(want)
+    # short bias slices are zero-padded (moe_dispatch.rs:352-359)
+    gb, gs, gbias, db, ds, dbias = syn.expert_slice(L, 0)
+    got = d.dispatch_expert(x, gb, gs, gbias[:100], db, ds, dbias[:7])
+    gb2 = np.zeros_like(gbias); gb2[:100] = gbias[:100]
+    db2 = np.zeros_like(dbias); db2[:7] = dbias[:7]
+    assert_rel_l2(got, orc.expert_ffn(x, gb, gs, gb2, db, ds, db2, H, I)[0], "short biases")
+    ws = [0.5, 0.3, 0.2]
+    got = d.dispatch_experts_batched(x, [(e, ws[e], *syn.expert_slice(L, e)) for e in range(3)])
+    assert_rel_l2(got, orc.combine(np.stack(outs), np.array(ws, np.float32), skip_nonfinite=True),
+                  "batched")
+    d.close()
+
+
+# ---------------------------------------------------------------- layer forward
+
+@pytest.mark.parametrize("T", [1, 2, 64])
+def test_layer_forward_20b(orc, disp20, layer20, T):
+    x = syn.hidden(T, H20, seed=100 + T)
+    got = disp20.layer_forward(0, x, 4)
+    want, logits, idx, w = orc.moe_layer(x, layer20, 4)
+    gidx, gw = disp20.router_topk(0, x, 4)
+    assert np.array_equal(gidx, idx)
+    assert_rel_l2(got, want, f"20B layer T={T}")
+
+
+# ---------------------------------------------------------------- fused single-token layer
+
+def test_fused_decode_matches_oracle_and_unfused(orc, disp20, layer20):
+    xs = syn.hidden(6, H20, seed=300)
+    for i in range(6):
+        x = xs[i:i + 1]
+        want, _, idx, _ = orc.moe_layer(x, layer20, 4)
+        disp20.set_fused_decode(True)
+        fused = disp20.layer_forward(0, x, 4)
+        disp20.set_fused_decode(False)
+        unfused = disp20.layer_forward(0, x, 4)
+        disp20.set_fused_decode(True)
+        assert_rel_l2(fused, want, f"fused token {i}")
+        assert_rel_l2(unfused, want, f"unfused token {i}")
+        # both paths run the same per-column arithmetic; they may differ only in combine order
+        assert rel_l2(fused, unfused) < 1e-6
+
+
+def test_fused_decode_repeated_calls_and_graph_replay(orc, disp20, layer20):
+    """The fused kernel clears its own counters: back-to-back launches and graph replays give
+    the eager result every time."""
+    import ctypes
+    from silentotithrandousha_amd._ffi import check, lib
+    H = H20
+    xs = syn.hidden(3, H, seed=301)
+    want = [orc.moe_layer(xs[i:i + 1], layer20, 4)[0][0] for i in range(3)]
+    xd = DeviceBuffer.from_array(xs)
+    yd = DeviceBuffer(3 * H * 4)
+    for rep in range(3):
+        for i in range(3):
+            check(lib().moe_layer_forward_device(disp20.ctx, 0, xd.ptr + i * H * 4, 1, 4,
+                                                 yd.ptr + i * H * 4, None))
+        disp20.synchronize()
+        got = yd.download(np.float32, (3, H))
+        for i in range(3):
+            assert_rel_l2(got[i], want[i], f"eager rep {rep} token {i}")
+    check(lib().moe_graph_begin(disp20.ctx))
+    for i in range(3):
+        check(lib().moe_layer_forward_device(disp20.ctx, 0, xd.ptr + i * H * 4, 1, 4,
+                                             yd.ptr + i * H * 4, None))
+    g = ctypes.c_void_p()
+    check(lib().moe_graph_end(disp20.ctx, ctypes.byref(g)))
+    try:
+        for rep in range(4):
+            check(lib().moe_memset_device(yd.ptr, 0, 3 * H * 4))
+            check(lib().moe_graph_launch(disp20.ctx, g.value))
+            disp20.synchronize()
+            got = yd.download(np.float32, (3, H))
+            for i in range(3):
+                assert_rel_l2(got[i], want[i], f"graph replay {rep} token {i}")
+            # eager work between replays
+            disp20.layer_forward(0, xs[0:1], 4)
+    finally:
+        check(lib().moe_graph_destroy(g.value))
+
+
+def test_fused_decode_tiny_shape_more_router_blocks(orc):
+    """E = 32 with a 64-wide expert: router blocks outnumber gate_up blocks."""
+    H, I, E = 64, 32, 32
+    L = syn.make_layer(H, I, E, seed=310, scale_lo=120, scale_hi=124)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    for i, x in enumerate(syn.hidden(4, H, seed=311)):
+        want, _, idx, _ = orc.moe_layer(x[None], L, 4)
+        assert_rel_l2(d.layer_forward(0, x[None], 4), want, f"tiny token {i}")
+    d.close()
+
+
+def test_adaptive_topk_fused_and_unfused(orc):
+    H, I, E = 256, 128, 8
+    L = syn.make_layer(H, I, E, seed=320, scale_lo=116, scale_hi=122, router_sigma=0.2)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    # parameters chosen so that the kept count takes the values 1, 2 and 4 on these tokens
+    ad = orc.Adaptive(1, 1, 0.7, 0.4, 0.85)
+    d.set_adaptive_topk(True, 1, 0.7, 0.4, 0.85)
+    xs = syn.hidden(16, H, seed=321, sigma=1.0)
+    used = set()
+    for fused in (True, False):
+        d.set_fused_decode(fused)
+        for i in range(16):
+            want, _, idx, w = orc.moe_layer(xs[i:i + 1], L, 4, adaptive=ad)
+            used.add(int((idx[0] >= 0).sum()))
+            gidx, gw = d.router_topk(0, xs[i:i + 1], 4)
+            assert np.array_equal(gidx, idx)
+            assert_rel_l2(d.layer_forward(0, xs[i:i + 1], 4), want, f"adaptive fused={fused} {i}")
+    assert used == {1, 2, 4}, used
+    d.close()
+
+
+def test_120b_layer_decode(orc):
+    """GPT-OSS-120B shape (128 experts, top-4) at batch 1 and 8."""
+    E = 128
+    L = syn.make_layer(H20, I20, E, seed=330)
+    d = GpuMoeDispatcher(H20, I20, 7.0)
+    d.preload_layer(0, L)
+    for T in (1, 8):
+        x = syn.hidden(T, H20, seed=331 + T)
+        want, _, idx, _ = orc.moe_layer(x, L, 4)
+        gidx, _ = d.router_topk(0, x, 4)
+        assert np.array_equal(gidx, idx)
+        assert_rel_l2(d.layer_forward(0, x, 4), want, f"120B T={T}")
+    d.close()
