@@ -354,3 +354,26 @@ def test_120b_layer_decode(orc):
         assert np.array_equal(gidx, idx)
         assert_rel_l2(d.layer_forward(0, x, 4), want, f"120B T={T}")
     d.close()
+
+
+# ---------------------------------------------------------------- committed fixture
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_tiny_layer_fixture(fused):
+    """The committed tiny layer (tests/golden/tiny_layer.npz, float64 numpy restatement):
+    indices exact, outputs within the matmul tolerance, on both single-token paths."""
+    import os
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_layer.npz"))
+    lay = {k: f[k] for k in f.files}
+    H, I, E, k = int(f["H"]), int(f["I"]), int(f["E"]), int(f["k"])
+    lay.update(H=H, I=I, E=E)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, lay)
+    d.set_fused_decode(fused)
+    idx, w = d.router_topk(0, f["x"], k)
+    assert np.array_equal(idx, f["idx"])
+    assert np.allclose(w, f["w"], rtol=1e-5)
+    for t in range(3):
+        assert_rel_l2(d.layer_forward(0, f["x"][t:t + 1], k)[0], f["y"][t], f"token {t}")
+    assert_rel_l2(d.layer_forward(0, f["x"], k), f["y"], "3 tokens")
+    d.close()
