@@ -1,6 +1,6 @@
 """Benchmark of the MXFP4 MoE path on one MI355X.
 
-Default workload: one GPT-OSS-20B-shaped MoE layer at decode batch 1 —
+Default workload (config 2 of the benchmark's configuration list): one GPT-OSS-20B-shaped MoE layer at decode batch 1 —
 router 2880->32 (bf16), top-4, 4 experts of gate_up 2880->5760 + down 2880->2880 in MXFP4,
 interleaved SwiGLU, weighted combine. A step is one token through one layer. To keep the
 256 MB MALL from serving the weights, 24 independent layers (10.2 GB of experts) stay
@@ -9,7 +9,7 @@ streams its experts from HBM.
 
 Prints ONE JSON line (see the repository's benchmark contract). Other workloads
 (--workload matvec|decode64|prefill|decode1_120b|prefill_120b) print the same kind of line
-for DESIGN.md; the driver runs the default.
+as well; the driver runs the default.
 """
 import argparse
 import ctypes
@@ -94,7 +94,10 @@ def event_timer():
 
 
 # ------------------------------------------------------------------ decode / prefill bench
-def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
+def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers_per_step=1,
+                    mfma_bound=False):
+    """A step is `layers_per_step` consecutive resident layers, each on its own T tokens
+    (layers_per_step = 24 for the 24-layer prefill of config 4)."""
     L = lib()
     disp = GpuMoeDispatcher(H, I, 7.0)
     disp.set_fused_decode(args.fused)
@@ -107,17 +110,21 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
     disp.synchronize()
 
     def step(i, stream=None):
-        j = i % P
-        check(L.moe_layer_forward_device(disp.ctx, i % n_layers, x.ptr + j * T * H * 4, T, k,
-                                         y.ptr + j * T * H * 4, stream))
+        for u in range(layers_per_step):
+            c = i * layers_per_step + u
+            j = c % P
+            check(L.moe_layer_forward_device(disp.ctx, c % n_layers, x.ptr + j * T * H * 4, T, k,
+                                             y.ptr + j * T * H * 4, stream))
 
     log("warmup")
     for i in range(args.warmup):
         step(i)
     disp.synchronize()
 
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
     graph = None
-    G = P if args.graph else 0
+    G = (P if layers_per_step == 1 else 1) if args.graph else 0
     if args.graph:
         check(L.moe_graph_begin(disp.ctx))
         for i in range(G):
@@ -148,7 +155,7 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
     log("kernel timing region")
     disp.set_timing(True)
     disp.reset_timing()
-    n_kt = min(args.steps, max(240, G))
+    n_kt = min(args.steps, max(240 // layers_per_step, G))
     for i in range(n_kt):
         step(i)
     disp.synchronize()
@@ -160,21 +167,23 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
         check(L.moe_graph_destroy(graph))
 
     tokens_per_s = T * args.steps / elapsed
-    active = min(E, T * k) if T == 1 else E  # expected distinct experts per step
-    traffic = layer_traffic(H, I, E, k, T, active)
-    flops = layer_flops(H, I, E, k, T)
+    active = min(E, T * k) if T == 1 else E  # expected distinct experts per layer
+    traffic = layer_traffic(H, I, E, k, T, active) * layers_per_step
+    flops = layer_flops(H, I, E, k, T) * layers_per_step
     gu_b, dn_b = expert_bytes(H, I)
     dom = "decode_gate_up" if kt["decode_gate_up"][1] else "gate_up"
     gu_ms, gu_n = kt[dom]
     gu_avg_s = gu_ms / max(gu_n, 1) / 1e3
     gu_bytes = active * gu_b + T * H * 4 + T * k * I * 4
+    gu_flops = 2.0 * T * k * 2 * I * H
     res = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded, BASELINE distributions; random-init weights, device-generated)",
+        "data": "synthetic (seeded; nibbles uniform, E8M0 118..130, router N(0,0.02) bf16, biases N(0,0.01) bf16, x N(0,1); device-generated)",
         "config": {"workload": workload, "name": config_name, "hidden": H, "intermediate": I,
-                   "experts": E, "top_k": k, "tokens_per_step": T, "resident_layers": n_layers,
+                   "experts": E, "top_k": k, "tokens_per_layer": T, "layers_per_step": layers_per_step,
+                   "resident_layers": n_layers,
                    "weights": "MXFP4 E2M1 + E8M0 (checkpoint layout repacked on preload)",
                    "arithmetic": "exact MXFP4->bf16 decode x f32 activation as bf16 hi+lo, f32 MFMA accumulate",
                    "graph_replay": bool(graph), "fused_decode": bool(args.fused and T == 1)},
@@ -183,9 +192,10 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
                      "achieved": round(gu_bytes / gu_avg_s / 1e9, 1) if gu_n else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / gu_avg_s / 1e9 / HBM_PEAK_GBS, 4) if gu_n else None,
-                     "traffic": None,
+                     "traffic": args.traffic_kib * 1024 if args.traffic_kib else None,
                      "algorithmic_bytes_per_launch": gu_bytes,
-                     "avg_launch_us": round(gu_avg_s * 1e6, 3)},
+                     "avg_launch_us": round(gu_avg_s * 1e6, 3),
+                     "mfma_TFLOPs": round(gu_flops / gu_avg_s / 1e12, 2) if gu_n else None},
         "layer_roofline": {"algorithmic_bytes_per_step": traffic, "flops_per_step": flops,
                            "achieved_GBps": round(traffic / (ms_per_step / 1e3) / 1e9, 1),
                            "frac_hbm": round(traffic / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -193,12 +203,19 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name):
                            "frac_mxfp4_peak": round(flops / (ms_per_step / 1e3) / 1e12 / MXFP4_PEAK_TFLOPS, 5)},
         "kernel_us": {n: round(v[0] * 1e3 / max(v[1], 1), 3) for n, v in kt.items() if v[1]},
     }
+    if mfma_bound and gu_n:
+        # dense regime: the MFMA roofline against the MXFP4 peak (the arithmetic runs on the
+        # bf16 MFMA with a hi+lo split of the activations, i.e. 2x these flops)
+        res["roofline"].update(bound="mfma", achieved=round(gu_flops / gu_avg_s / 1e12, 2),
+                               peak=MXFP4_PEAK_TFLOPS, unit="TFLOP/s",
+                               frac=round(gu_flops / gu_avg_s / 1e12 / MXFP4_PEAK_TFLOPS, 5),
+                               hbm_GBps=round(gu_bytes / gu_avg_s / 1e9, 1))
     disp.close()
     return res
 
 
 def run_matvec_bench(args):
-    """y = W x, W 2880x2880 MXFP4; 64 distinct copies back to back."""
+    """Config 1: y = W x, W 2880x2880 MXFP4; 64 distinct copies back to back."""
     L = lib()
     from silentotithrandousha_amd import mxfp4_matvec, mxfp4_pack
     R = C = 2880
@@ -232,6 +249,19 @@ def run_matvec_bench(args):
             "config": {"workload": "config1 matvec 2880x2880", "copies": copies}}
 
 
+def copy_calibration(mib):
+    """One plain device-to-device copy of `mib` MiB (the runtime's blit kernel,
+    __amd_rocclr_copyBuffer): under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch
+    calibrate the counters against a known byte count."""
+    n = mib << 20
+    a, b = DeviceBuffer(n), DeviceBuffer(n)
+    check(lib().moe_memset_device(a.ptr, 1, n))
+    check(lib().moe_memcpy_d2d(b.ptr, a.ptr, n))
+    log(f"copy calibration: {mib} MiB device-to-device")
+    a.close()
+    b.close()
+
+
 # ------------------------------------------------------------------ CPU baseline
 def cpu_baseline(seconds, H, I, E, k):
     """The reference's live CPU MoE block restated in C (oracle/): router + top-4, cold fp16
@@ -262,8 +292,8 @@ def cpu_baseline(seconds, H, I, E, k):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4800)
-    ap.add_argument("--warmup", type=int, default=480)
+    ap.add_argument("--steps", type=int, default=None, help="default: per workload")
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode1",
                     choices=["decode1", "decode64", "prefill", "matvec", "decode1_120b", "prefill_120b"])
     ap.add_argument("--layers", type=int, default=24)
@@ -272,10 +302,19 @@ def main():
                     help="single-token steps through the multi-kernel path")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
+    ap.add_argument("--traffic-kib", type=float, default=0.0,
+                    help="HBM KiB per launch of the dominant kernel from calibrated rocprofv3 "
+                         "--pmc FETCH_SIZE + WRITE_SIZE runs, reported as roofline.traffic")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="run one device copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
+    dsteps, dwarm = {"decode1": (4800, 480), "decode1_120b": (4800, 480), "matvec": (4800, 480),
+                     "decode64": (960, 96), "prefill": (8, 2), "prefill_120b": (48, 8)}[args.workload]
+    args.steps = dsteps if args.steps is None else args.steps
+    args.warmup = dwarm if args.warmup is None else args.warmup
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "sharding of this path is described in DESIGN.md and not run here.", file=sys.stderr)
+              "sharding of this path (expert parallel / row split) is a design note, not built.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
     H = I = 2880
@@ -286,7 +325,9 @@ def main():
     elif args.workload == "decode64":
         res = run_layer_bench(args, H, I, 32, 4, 64, args.layers, "config3 gpt-oss-20b moe layer decode b=64", "decode64")
     elif args.workload == "prefill":
-        res = run_layer_bench(args, H, I, 32, 4, 4096, args.layers, "config4 gpt-oss-20b moe prefill 4096 tokens", "prefill")
+        res = run_layer_bench(args, H, I, 32, 4, 4096, args.layers,
+                              "config4 gpt-oss-20b moe prefill 4096 tokens x 24 layers", "prefill",
+                              layers_per_step=args.layers, mfma_bound=True)
     elif args.workload == "decode1_120b":
         res = run_layer_bench(args, H, I, 128, 4, 1, args.layers, "config5 gpt-oss-120b moe layer decode b=1", "decode1_120b")
     else:

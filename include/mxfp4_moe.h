@@ -87,6 +87,18 @@ int moe_preload_layer_device(moe_ctx *ctx, size_t layer, size_t n_experts,
                              const uint8_t *gate_up_blocks, const uint8_t *gate_up_scales,
                              const float *gate_up_bias, const uint8_t *down_blocks,
                              const uint8_t *down_scales, const float *down_bias, void *stream);
+/* One expert of GpuMoeDispatcher::preload_experts — moe_dispatch.rs:149-229, whose loop
+ * creates per-expert device buffers from each ExpertMxfp4 (weights.rs:17-27). Tensors are that
+ * expert's alone (no [E] dimension); lengths as for moe_dispatch_expert (blocks and scales
+ * exact, biases may be short and are zero-padded). A layer is usable by the path-level calls
+ * once all n_experts of it are preloaded; a different n_experts for a layer discards it. */
+int moe_preload_expert(moe_ctx *ctx, size_t layer, size_t n_experts, size_t expert_idx,
+                       const uint8_t *gate_up_blocks, size_t gate_up_blocks_len,
+                       const uint8_t *gate_up_scales, size_t gate_up_scales_len,
+                       const float *gate_up_bias, size_t gate_up_bias_len,
+                       const uint8_t *down_blocks, size_t down_blocks_len,
+                       const uint8_t *down_scales, size_t down_scales_len,
+                       const float *down_bias, size_t down_bias_len);
 /* Router weights of one layer (LayerWeights::router_weight/bias, weights.rs:44-46, loaded at
  * weights.rs:280-281). In the reference the router runs on the ANE inside
  * build_decode_output_proj_router (executables.rs:301-313); here it runs on the GPU. */
@@ -101,7 +113,9 @@ int moe_preload_router_f32(moe_ctx *ctx, size_t layer, size_t n_experts, const f
 
 /* GpuMoeDispatcher::dispatch_expert_preloaded — moe_dispatch.rs:232-324.
  * output[H] = clamp(down(SwiGLU(gate_up(input))), +-65504) for one preloaded expert, with the
- * GPT-OSS activation of session.rs:101-123 (not the Metal shader's, see DESIGN). */
+ * GPT-OSS activation of session.rs:101-123: gate = min(g, clamp), up = clamp(u, +-clamp),
+ * (up + 1) * gate * sigmoid(1.702 gate). The unused Metal shader (moe_shader.metal:4-101)
+ * computes a different activation and decodes E8M0 255 as 0; its semantics are not followed. */
 int moe_dispatch_expert_preloaded(moe_ctx *ctx, const float *input, size_t layer,
                                   size_t expert_idx, float *output);
 
@@ -194,6 +208,9 @@ int moe_device_alloc(size_t bytes, void **ptr);
 int moe_device_free(void *ptr);
 int moe_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int moe_memcpy_d2h(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy (the runtime's blit kernel); also the known-size copy that calibrates
+ * the FETCH_SIZE / WRITE_SIZE counters in profiles. */
+int moe_memcpy_d2d(void *dst, const void *src, size_t bytes);
 int moe_memset_device(void *dst, int value, size_t bytes);
 int moe_synchronize(moe_ctx *ctx);
 /* The context's stream (a hipStream_t) for callers that enqueue their own work. */

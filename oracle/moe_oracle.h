@@ -6,8 +6,14 @@
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and
  * only as the checker or as the timed CPU baseline; the HIP library never links it.
  *
- * Every function names the reference lines it restates. Pinning (what checks each
- * function against something other than itself) is listed in oracle/PINNING.md.
+ * Every function names the reference lines it restates. Pinning (what checks each function
+ * against something other than itself) lives in tests/test_oracle.py: the committed
+ * closed-form decode table and float64 restatement under tests/golden/, brute-force top-k,
+ * order-sensitive vectors for the router and the NEON matvec, special cases of the SwiGLU.
+ * Parity unpinned (no vector can exist offline): the ANE fp16 router numerics the fp32
+ * router replaces (executables.rs:260-317), macOS libm expf last-ulp behaviour
+ * (session.rs:114), and the `half` 2.7.1 crate calls themselves (pinned only by their closed
+ * forms: bf16/f16 -> f32 exact, f32 -> f16 IEEE round-to-nearest-even).
  *
  * Floating-point rules: compiled with -ffp-contract=off so every `a * b + c` written as
  * separate operations rounds twice, as Rust does (Rust never contracts to FMA); fused

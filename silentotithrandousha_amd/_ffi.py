@@ -54,6 +54,8 @@ SIGNATURES = {
     "moe_set_option": (_int, [_vp, _int, ctypes.c_int64]),
     "moe_preload_layer": (_int, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
     "moe_preload_layer_device": (_int, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "moe_preload_expert": (_int, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz,
+                                  _vp, _sz, _vp, _sz]),
     "moe_preload_router": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "moe_preload_router_f32": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "moe_dispatch_expert_preloaded": (_int, [_vp, _vp, _sz, _sz, _vp]),
@@ -74,6 +76,7 @@ SIGNATURES = {
     "moe_device_free": (_int, [_vp]),
     "moe_memcpy_h2d": (_int, [_vp, _vp, _sz]),
     "moe_memcpy_d2h": (_int, [_vp, _vp, _sz]),
+    "moe_memcpy_d2d": (_int, [_vp, _vp, _sz]),
     "moe_memset_device": (_int, [_vp, _int, _sz]),
     "moe_synchronize": (_int, [_vp]),
     "moe_stream": (_vp, [_vp]),

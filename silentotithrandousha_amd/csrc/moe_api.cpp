@@ -71,6 +71,8 @@ struct DevBuf {
 struct Layer {
   DevBuf experts;  // n_experts * stride
   size_t n_experts = 0;
+  std::vector<uint8_t> loaded;  // per expert: its record has been written
+  size_t n_loaded = 0;
   DevBuf router;   // lane-major bf16 [E][64][KIp] then [E] f32
   size_t router_experts = 0;
 };
@@ -252,9 +254,18 @@ int run_experts(moe_ctx *c, const uint8_t *base, int max_active, int max_entries
   return MOE_OK;
 }
 
-int check_layer(moe_ctx *c, size_t layer, bool need_router) {
+// expert < 0: every expert of the layer must be preloaded; else that one expert.
+int check_layer(moe_ctx *c, size_t layer, bool need_router, long expert = -1) {
   if (layer >= c->layers.size() || !c->layers[layer].experts.p)
     return fail(MOE_ERR_STATE, "layer %zu has no preloaded experts", layer);
+  if (expert >= 0) {
+    if ((size_t)expert >= c->layers[layer].n_experts)
+      return fail(MOE_ERR_INVALID, "expert %ld >= %zu", expert, c->layers[layer].n_experts);
+    if (!c->layers[layer].loaded[expert])
+      return fail(MOE_ERR_STATE, "layer %zu expert %ld is not preloaded", layer, expert);
+  } else if (c->layers[layer].n_loaded != c->layers[layer].n_experts)
+    return fail(MOE_ERR_STATE, "layer %zu has %zu of its %zu experts preloaded", layer,
+                c->layers[layer].n_loaded, c->layers[layer].n_experts);
   if (need_router && !c->layers[layer].router.p)
     return fail(MOE_ERR_STATE, "layer %zu has no router weights", layer);
   return MOE_OK;
@@ -506,9 +517,36 @@ static int preload_common(moe_ctx *c, size_t layer, size_t n_experts) {
   if (layer > 4096) return fail(MOE_ERR_INVALID, "layer index %zu too large", layer);
   if (c->layers.size() <= layer) c->layers.resize(layer + 1);
   Layer &Ly = c->layers[layer];
-  if (Ly.experts.cap < n_experts * c->L.stride) Ly.experts.release();
-  RETURN_IF(Ly.experts.ensure(n_experts * c->L.stride));
-  Ly.n_experts = n_experts;
+  if (Ly.n_experts != n_experts) {  // a new expert count discards the layer's experts
+    if (Ly.experts.cap < n_experts * c->L.stride) Ly.experts.release();
+    RETURN_IF(Ly.experts.ensure(n_experts * c->L.stride));
+    Ly.n_experts = n_experts;
+    Ly.loaded.assign(n_experts, 0);
+    Ly.n_loaded = 0;
+  }
+  return MOE_OK;
+}
+
+static void mark_loaded(Layer &Ly, size_t e) {
+  if (!Ly.loaded[e]) {
+    Ly.loaded[e] = 1;
+    Ly.n_loaded++;
+  }
+}
+
+int moe_preload_expert(moe_ctx *c, size_t layer, size_t n_experts, size_t expert_idx,
+                       const uint8_t *gub, size_t gub_len, const uint8_t *gus, size_t gus_len,
+                       const float *gubias, size_t gubias_len, const uint8_t *db, size_t db_len,
+                       const uint8_t *ds, size_t ds_len, const float *dbias, size_t dbias_len) {
+  if (!c) return fail(MOE_ERR_INVALID, "null context");
+  if (expert_idx >= n_experts)
+    return fail(MOE_ERR_INVALID, "expert %zu >= n_experts %zu", expert_idx, n_experts);
+  RETURN_IF(preload_common(c, layer, n_experts));
+  Layer &Ly = c->layers[layer];
+  RETURN_IF(upload_expert(c, (uint8_t *)Ly.experts.p + expert_idx * c->L.stride, gub, gub_len,
+                          gus, gus_len, gubias, gubias_len, db, db_len, ds, ds_len, dbias,
+                          dbias_len));
+  mark_loaded(Ly, expert_idx);
   return MOE_OK;
 }
 
@@ -523,6 +561,7 @@ int moe_preload_layer(moe_ctx *c, size_t layer, size_t n_experts, const uint8_t 
     RETURN_IF(upload_expert(c, base + e * c->L.stride, gub + e * eb.gub, eb.gub, gus + e * eb.gus,
                             eb.gus, gubias + e * eb.gubias, eb.gubias, db + e * eb.db, eb.db,
                             ds + e * eb.ds, eb.ds, dbias + e * eb.dbias, eb.dbias));
+  for (size_t e = 0; e < n_experts; e++) mark_loaded(c->layers[layer], e);
   return MOE_OK;
 }
 
@@ -538,6 +577,7 @@ int moe_preload_layer_device(moe_ctx *c, size_t layer, size_t n_experts, const u
     RETURN_IF(pack_expert(c, base + e * c->L.stride, gub + e * eb.gub, gus + e * eb.gus,
                           gubias + e * eb.gubias, db + e * eb.db, ds + e * eb.ds,
                           dbias + e * eb.dbias, s));
+  for (size_t e = 0; e < n_experts; e++) mark_loaded(c->layers[layer], e);
   return MOE_OK;
 }
 
@@ -582,9 +622,7 @@ int moe_dispatch_expert_preloaded(moe_ctx *c, const float *input, size_t layer, 
                                   float *output) {
   RETURN_IF(use_dev(c));
   if (!input || !output) return fail(MOE_ERR_INVALID, "null input or output");
-  RETURN_IF(check_layer(c, layer, false));
-  if (expert >= c->layers[layer].n_experts)
-    return fail(MOE_ERR_INVALID, "expert %zu >= %zu", expert, c->layers[layer].n_experts);
+  RETURN_IF(check_layer(c, layer, false, (long)expert));
   RETURN_IF(ensure_work(c, 1, 1, 1));
   HIP_TRY(hipMemcpyAsync(c->w.x, input, c->H * 4, hipMemcpyHostToDevice, c->stream));
   HIP_TRY(launch_split(c->w.x, 1, c->H, c->w.xsplit, c->stream));
@@ -742,9 +780,8 @@ int moe_mxfp4_dequant_device(const uint8_t *blocks, const uint8_t *scales, size_
 int moe_dequant_expert_device(moe_ctx *c, size_t layer, size_t expert, int which, float *out,
                               void *stream) {
   RETURN_IF(use_dev(c));
-  RETURN_IF(check_layer(c, layer, false));
-  if (expert >= c->layers[layer].n_experts || (which != 0 && which != 1) || !out)
-    return fail(MOE_ERR_INVALID, "bad expert / which / out");
+  RETURN_IF(check_layer(c, layer, false, (long)expert));
+  if ((which != 0 && which != 1) || !out) return fail(MOE_ERR_INVALID, "bad which / out");
   const uint8_t *rec = (const uint8_t *)c->layers[layer].experts.p + expert * c->L.stride;
   if (which == 0)
     HIP_TRY(launch_dequant_packed(rec + c->L.gu_off, 2 * c->I, c->H, out, pick(c, stream)));
@@ -816,6 +853,10 @@ int moe_memcpy_h2d(void *dst, const void *src, size_t bytes) {
 }
 int moe_memcpy_d2h(void *dst, const void *src, size_t bytes) {
   HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return MOE_OK;
+}
+int moe_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
   return MOE_OK;
 }
 int moe_memset_device(void *dst, int value, size_t bytes) {

@@ -108,6 +108,16 @@ class GpuMoeDispatcher:
         for i, layer in enumerate(layers):
             self.preload_layer(i, layer)
 
+    def preload_expert(self, layer_idx, n_experts, expert_idx, gu_blocks, gu_scales, gu_bias,
+                       d_blocks, d_scales, d_bias):
+        """One ExpertMxfp4 (weights.rs:17-27) of preload_experts' per-expert loop."""
+        t = [_c(gu_blocks, np.uint8), _c(gu_scales, np.uint8), _c(gu_bias, np.float32),
+             _c(d_blocks, np.uint8), _c(d_scales, np.uint8), _c(d_bias, np.float32)]
+        args = []
+        for a in t:
+            args += [_p(a), a.size]
+        check(lib().moe_preload_expert(self._ctx, layer_idx, n_experts, expert_idx, *args))
+
     def set_fused_decode(self, on):
         from ._ffi import MOE_OPT_FUSED_DECODE
         check(lib().moe_set_option(self._ctx, MOE_OPT_FUSED_DECODE, int(bool(on))))
