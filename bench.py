@@ -161,7 +161,7 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
     disp.synchronize()
     kt = {name: disp.get_timing(kid) for kid, name in
           enumerate(["route", "bucket", "gate_up", "down", "combine", "decode_gate_up",
-                     "decode_down"])}
+                     "decode_down", "decode_layer"])}
     disp.set_timing(False)
     if graph:
         check(L.moe_graph_destroy(graph))
@@ -171,11 +171,16 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
     traffic = layer_traffic(H, I, E, k, T, active) * layers_per_step
     flops = layer_flops(H, I, E, k, T) * layers_per_step
     gu_b, dn_b = expert_bytes(H, I)
-    dom = "decode_gate_up" if kt["decode_gate_up"][1] else "gate_up"
+    dom = ("decode_layer" if kt["decode_layer"][1] else
+           "decode_gate_up" if kt["decode_gate_up"][1] else "gate_up")
     gu_ms, gu_n = kt[dom]
     gu_avg_s = gu_ms / max(gu_n, 1) / 1e3
-    gu_bytes = active * gu_b + T * H * 4 + T * k * I * 4
-    gu_flops = 2.0 * T * k * 2 * I * H
+    if dom == "decode_layer":  # the whole layer in one launch
+        gu_bytes = layer_traffic(H, I, E, k, T, active)
+        gu_flops = layer_flops(H, I, E, k, T)
+    else:
+        gu_bytes = active * gu_b + T * H * 4 + T * k * I * 4
+        gu_flops = 2.0 * T * k * 2 * I * H
     res = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6),
@@ -188,7 +193,8 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
                    "arithmetic": "exact MXFP4->bf16 decode x f32 activation as bf16 hi+lo, f32 MFMA accumulate",
                    "graph_replay": bool(graph), "fused_decode": bool(args.fused and T == 1)},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_decode_gate_up" if dom == "decode_gate_up" else "k_expert_gemv<gate_up>",
+                     "kernel": {"decode_layer": "k_decode_layer", "decode_gate_up": "k_decode_gate_up",
+                                "gate_up": "k_expert_gemv<gate_up>"}[dom],
                      "achieved": round(gu_bytes / gu_avg_s / 1e9, 1) if gu_n else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / gu_avg_s / 1e9 / HBM_PEAK_GBS, 4) if gu_n else None,

@@ -66,10 +66,16 @@ void moe_destroy(moe_ctx *ctx);
 int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_min_prob,
                           float top1_min_margin, float top2_min_mass);
 
-/* Options (no reference counterpart). MOE_OPT_FUSED_DECODE: 1 (default) runs single-token
- * forwards as two fused kernels (router + top-k + gate_up + SwiGLU; down + combine); 0 uses
- * the five-kernel path that larger batches take. Results agree to the matmul tolerance. */
-enum moe_option { MOE_OPT_FUSED_DECODE = 1 };
+/* Options (no reference counterpart).
+ * MOE_OPT_FUSED_DECODE selects how single-token forwards run: 2 (default) one launch (router,
+ * top-k, gate_up, SwiGLU, down and combine, with the down weights streaming during gate_up;
+ * up to 64 experts), 1 two launches (router + gate_up; down + combine), 0 the five-kernel
+ * path that batches take. Shapes a mode does not support take the next lower one. Results
+ * agree to the matmul tolerance; routing is identical.
+ * MOE_OPT_SPIN_LIMIT: polls before a cross-block wait of the one-launch kernel gives up
+ * (default 2^20); a wait that gives up makes the outputs NaN and the next moe_synchronize or
+ * moe_layer_forward return MOE_ERR_HIP (which clears the condition). */
+enum moe_option { MOE_OPT_FUSED_DECODE = 1, MOE_OPT_SPIN_LIMIT = 2 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 
 /* ------------------------------------------------------------------ weights */
@@ -239,7 +245,7 @@ int moe_graph_destroy(void *graph_exec);
  * stream the kernels run on when enabled (no reference counterpart). */
 int moe_set_timing(moe_ctx *ctx, int enabled);
 /* kernel: 0 route, 1 bucket, 2 gate_up, 3 down, 4 combine, 5 single-token router+gate_up,
- * 6 single-token down+combine.
+ * 6 single-token down+combine, 7 single-token layer in one launch.
  * Returns accumulated milliseconds
  * and launch count since the last reset; synchronises the context stream. */
 int moe_get_timing(moe_ctx *ctx, int kernel, double *ms, uint64_t *launches);

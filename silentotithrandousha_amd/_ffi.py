@@ -18,6 +18,7 @@ MOE_ERR_NO_DEVICE = 4
 MOE_ERR_OOM = 5
 
 MOE_OPT_FUSED_DECODE = 1
+MOE_OPT_SPIN_LIMIT = 2
 
 _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256, 2) void k_decode_gate_up(DecodeArgs a) {
     }
     __syncthreads();
     for (int e = wv; e < E; e += 4) {
-      const float p = router_dot<0>(a.rw + ((size_t)e * 64 + lane) * a.rnq * 8, s_xr, a.rnq, lane);
+      const float p = router_dot<0>(a.rw + (size_t)e * a.rnq * 512, s_xr, a.rnq, lane);
       if (lane == 0) s_logit[e] = canon_nan(p + a.rb[e]);
     }
   }

@@ -1,0 +1,412 @@
+// Single-token MoE layer for gfx950 in ONE launch — the MoE block of
+// Session::decode_step_inner (session.rs:818-980) for one token, with the down projection's
+// weight stream overlapping the gate_up phase.
+//
+// Blocks of 4 wavefronts (3 per CU, so all blocks of the GPT-OSS shape are resident at once),
+// two roles by block index:
+//   [0, k*NGS)        gate_up blocks: block (slot s, i) streams the 4 gate_up tiles (64 rows)
+//                     of slot s's expert that produce h[32i, 32i+32), one tile per wavefront.
+//   [k*NGS, +H/16)    down blocks: one 16-row output tile, wavefront = slot; bias, clamp and the
+//                     slot-ordered combine into y.
+// Router: wavefront w of the grid (w < E) computes logit w in the canonical order (same
+// arithmetic as k_route) and writes it, tagged, into kReplicas copies of the logit vector;
+// block b reads copy b % kReplicas and runs the top-k itself (identical arithmetic everywhere,
+// so every block selects the same experts and weights). Block 0 also writes the logits,
+// indices and weights.
+// Matmuls: v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as stored (no decode
+// instructions) and the activation as kTerms fp8 terms with E8M0 scales (split8_fp8):
+// x is split by every gate_up block into LDS; each gate_up block splits its 32 h values and
+// publishes them; down blocks copy the h terms of the kept slots into LDS.
+//
+// Cross-block signalling without fences over the L2: every value read by another block
+// (logits, h terms, flags) is written with agent-scope relaxed atomic stores (write-through)
+// and read with agent-scope loads that bypass the L2 (relaxed atomic loads, or LDS-direct
+// loads with the same cache policy); a writer waits for its stores to complete (s_waitcnt)
+// before it raises the flag that publishes them. No address is polled by more than
+// ceil(blocks / kReplicas) blocks.
+//   * logits: every block adds 1 to its copy's counter after reading the copy; the block that
+//     brings it to the copy's reader count clears the copy and the counter;
+//   * h of slot s: every gate_up block of slot s adds 1 to counter s after its h stores are
+//     complete; the block that brings it to NGS resets it to 0 and raises h_ready[s] in every
+//     down block's mailbox; a down block clears its mailbox when done.
+// So counters, copies and mailboxes are zero again when the kernel ends and the next launch
+// (or graph replay) starts clean. The blocks that wait on gate_up blocks have higher indices, and
+// workgroups are dispatched in index order, so waiting blocks never hold back the blocks they
+// wait for; the router wavefronts are in the lowest blocks. Every wait is bounded by
+// `spin_limit` polls; a wait that runs out sets the sticky error word, the block writes NaN to
+// its outputs, and later launches return NaN at once until the host clears the error (it
+// reports it at its next synchronisation).
+#include <algorithm>
+
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace moe {
+
+constexpr int kLayerWaves = 4;
+constexpr int kLayerThreads = 64 * kLayerWaves;
+constexpr int kLayerNs = 24;  // steps per tile: K <= 3072
+constexpr int kLayerNq = kLayerNs / 4;
+using Act = ActRecord<kLayerNs>;  // x and h records: 4 fp8 terms of up to 3072 values
+
+constexpr int kReplicas = 16;
+
+struct LogitCopy {       // kCopyBytes apart
+  uint64_t logit[64];    // (1 << 32) | f32 bits of logit e, 0 when empty
+  uint32_t readers_done;
+};
+constexpr size_t kCopyBytes = 640;
+static_assert(sizeof(LogitCopy) <= kCopyBytes, "copy layout");
+
+struct LayerMailbox {    // one per down block, 64 bytes apart
+  uint32_t h_ready[4];   // slot s's h terms are complete
+};
+
+struct LayerSyncHdr {
+  uint32_t err;          // sticky: a bounded wait ran out
+  uint32_t pad0[63];
+  uint32_t cnt[4][64];   // gate_up blocks done per slot (256 bytes apart)
+};
+
+size_t layer_sync_bytes(int max_blocks) {
+  return sizeof(LayerSyncHdr) + kReplicas * kCopyBytes + (size_t)max_blocks * 64;
+}
+
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent64(const uint64_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent64(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this wavefront issued has completed.
+__device__ __forceinline__ void wait_mem() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ LogitCopy *logit_copy(void *sync, int r) {
+  return reinterpret_cast<LogitCopy *>(reinterpret_cast<uint8_t *>(sync) + sizeof(LayerSyncHdr) +
+                                       (size_t)r * kCopyBytes);
+}
+__device__ __forceinline__ LayerMailbox *mailbox(void *sync, int d) {
+  return reinterpret_cast<LayerMailbox *>(reinterpret_cast<uint8_t *>(sync) + sizeof(LayerSyncHdr) +
+                                          kReplicas * kCopyBytes + (size_t)d * 64);
+}
+
+// Logit of expert e in the canonical order (router_compute's arithmetic for one expert);
+// every lane returns it. xr[i] = x[lane + 64 i], zero past H.
+template <int RNQ>
+__device__ __forceinline__ float router_logit(const uint16_t *rw, const float *rb, const float *xr,
+                                              int e, int lane) {
+  const uint4 *wq = reinterpret_cast<const uint4 *>(rw + (size_t)e * RNQ * 512) + lane;
+  uint4 v[RNQ];
+#pragma unroll
+  for (int q = 0; q < RNQ; q++) v[q] = wq[q * 64];
+  float p = 0.0f;
+#pragma unroll
+  for (int q = 0; q < RNQ; q++) {
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+      const uint32_t u = h < 2 ? v[q].x : (h < 4 ? v[q].y : (h < 6 ? v[q].z : v[q].w));
+      p = __builtin_fmaf(bf16_to_f32((uint16_t)(u >> (16 * (h & 1)))), xr[8 * q + h], p);
+    }
+  }
+  return canon_nan(wave_sum_xor(p) + rb[e]);
+}
+
+// Wavefront 0 of a block: wait for the E tagged logits in copy `cp`, run the top-k. Returns
+// false when the wait ran out. lane e's logit in *l.
+__device__ __forceinline__ bool await_routing(LogitCopy *cp, const TopkCfg &c, uint32_t spin_limit,
+                                              int lane, float *l, int *s_order, float *s_w, int *s_sel) {
+  const int E = c.E;
+  uint64_t v = 0;
+  for (uint32_t n = 0;; n++) {
+    v = lane < E ? ld_agent64(&cp->logit[lane]) : (1ull << 32);
+    if (__all((v >> 32) == 1ull)) break;
+    if (n >= spin_limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  *l = __uint_as_float((uint32_t)v);
+  wave_topk64(c, *l, lane, s_order, s_w, s_sel);
+  return true;
+}
+
+// Wavefront 0, after its routing read: count this block as a reader of copy `cp`; the last of
+// its `readers` clears it for the next launch.
+__device__ __forceinline__ void release_copy(LogitCopy *cp, int readers, int E, int lane) {
+  uint32_t old = 0;
+  if (lane == 0)
+    old = __hip_atomic_fetch_add(&cp->readers_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
+  if (old == (uint32_t)readers - 1) {
+    if (lane < E) st_agent64(&cp->logit[lane], 0ull);
+    if (lane == 0) st_agent(&cp->readers_done, 0u);
+  }
+}
+
+template <int RNQ>
+__global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_decode_layer(LayerArgs la) {
+  extern __shared__ uint4 smem[];
+  __shared__ int s_order[kMaxTopK];
+  __shared__ float s_w[kMaxTopK];
+  __shared__ int s_sel;
+  __shared__ int s_flag;
+  __shared__ float s_h32[32];
+  __shared__ float s_o[4][16];
+
+  const DecodeArgs &a = la.d;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int H = a.H, E = a.E, K = a.k;
+  const int NGS = la.n_gu_per_slot;
+  const int n_gu = K * NGS, n_blk = n_gu + la.n_dn;
+  LayerSyncHdr *hdr = reinterpret_cast<LayerSyncHdr *>(la.sync);
+  LogitCopy *cp = logit_copy(la.sync, b % kReplicas);
+  const int readers = n_blk / kReplicas + ((b % kReplicas) < (n_blk % kReplicas) ? 1 : 0);
+  const uint32_t err0 = ld_agent(&hdr->err);  // tested late: the load overlaps the router
+  const TopkCfg tc{E, K, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
+  constexpr int XI = 8 * RNQ;  // x values per lane of the router chain
+  const int j = lane & 15, g = lane >> 4;
+
+  // ---------------------------------------------------------------- router wavefronts
+  const int gw = b * kLayerWaves + wv;
+  if (gw < E) {
+    float xr[XI];
+#pragma unroll
+    for (int i = 0; i < XI; i++) xr[i] = a.x[min(lane + 64 * i, H - 1)];
+#pragma unroll
+    for (int i = 0; i < XI; i++)
+      if (lane + 64 * i >= H) xr[i] = 0.0f;
+    for (int e = gw; e < E; e += n_blk * kLayerWaves) {
+      const float lg = router_logit<RNQ>(a.rw, a.rb, xr, e, lane);
+      if (lane < kReplicas) st_agent64(&logit_copy(la.sync, lane)->logit[e], (1ull << 32) | __float_as_uint(lg));
+    }
+  }
+
+  if (b < n_gu) {
+    // ================================================================ gate_up block
+    // 1. x as kTerms fp8 terms in LDS, 8 values per thread (a quad of lanes = one 32-block);
+    //    blocks past H up to nbpx are zeros.
+    uint8_t *s_x = reinterpret_cast<uint8_t *>(smem);  // activation record of x
+    for (int u = tid; u < 16 * kLayerNs; u += kLayerThreads) {  // uniform trip count per quad
+      float xv[8];
+      if (8 * u < H) {
+        const float4 v0 = reinterpret_cast<const float4 *>(a.x)[2 * u];
+        const float4 v1 = reinterpret_cast<const float4 *>(a.x)[2 * u + 1];
+        xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+        xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = 0.0f;
+      }
+      uint2 q[kTerms];
+      uint32_t s4;
+      split8_fp8(xv, q, s4);
+      const int bb = u >> 2;
+#pragma unroll
+      for (int t = 0; t < kTerms; t++) *reinterpret_cast<uint2 *>(s_x + Act::term(t, bb) + 8 * (u & 3)) = q[t];
+      if ((u & 3) == 0) {
+#pragma unroll
+        for (int t = 0; t < kTerms; t++) s_x[Act::scale(t, bb)] = (uint8_t)(s4 >> (8 * t));
+      }
+    }
+    // 2. routing
+    if (wv == 0) {
+      float l;
+      const bool ok = await_routing(cp, tc, la.spin_limit, lane, &l, s_order, s_w, &s_sel);
+      release_copy(cp, readers, E, lane);
+      if (lane == 0) s_flag = !ok;
+      if (b == 0 && ok) {
+        if (lane < E) a.logits[lane] = l;
+        if (lane < K) {
+          a.idx[lane] = s_order[lane];
+          a.wts[lane] = s_w[lane];
+        }
+      }
+    }
+    __syncthreads();
+    const bool timeout = s_flag;
+    const int sel = s_sel;
+    const int slot = b / NGS;
+    if (timeout || err0 || slot >= sel) {  // uniform over the block; no barrier follows
+      if (timeout && tid == 0) st_agent(&hdr->err, 1u);
+      return;
+    }
+    // 3. this wavefront's gate_up tile (rows 16t .. 16t+15 -> h[8t, 8t+8)); bias with it
+    const int hb = b - slot * NGS;
+    const int t = hb * 4 + wv;
+    const uint8_t *rec = a.base + (size_t)s_order[slot] * a.stride;
+    TileRegs<kLayerNs> r;
+    tile_load<kLayerNs>(r, rec + a.gu_off, a.gu, t, true, lane);
+    const float4 bias = reinterpret_cast<const float4 *>(rec + a.gub_off)[t * 4 + g];
+    uint32_t bsw[kLayerNq];
+    load_bsw<kLayerNs>(s_x, bsw, lane);
+    const f32x4 acc = tile_mfma_f8<kLayerNs>(r, s_x, bsw, lane);
+    float v[4];
+    sum_terms(acc, v);
+    if (j == 0) {
+      s_h32[wv * 8 + 2 * g] = swiglu(v[0] + bias.x, v[1] + bias.y, a.limit);
+      s_h32[wv * 8 + 2 * g + 1] = swiglu(v[2] + bias.z, v[3] + bias.w, a.limit);
+    }
+    __syncthreads();
+    // 4. h[32 hb, 32 hb + 32) as kTerms fp8 terms -> this slot's h record (lanes 0..3 of
+    //    wavefront 0 hold 8 values each)
+    if (wv == 0) {
+      if (lane < 4) {
+        float hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) hv[i] = s_h32[8 * lane + i];
+        uint2 q[kTerms];
+        uint32_t s4;
+        split8_fp8(hv, q, s4);
+        uint8_t *rec_h = la.hterm + (size_t)slot * Act::kBytes;
+#pragma unroll
+        for (int tt = 0; tt < kTerms; tt++) {
+          uint32_t *dst = reinterpret_cast<uint32_t *>(rec_h + Act::term(tt, hb) + 8 * lane);
+          st_agent(dst, q[tt].x);
+          st_agent(dst + 1, q[tt].y);
+        }
+        if (lane == 0) {
+#pragma unroll
+          for (int tt = 0; tt < kTerms; tt++)
+            __hip_atomic_store(rec_h + Act::scale(tt, hb), (uint8_t)(s4 >> (8 * tt)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      wait_mem();
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(&hdr->cnt[slot][0], 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      s_flag = old == (uint32_t)NGS - 1;
+    }
+    __syncthreads();
+    if (s_flag) {  // the last gate_up block of this slot: its h terms are complete
+      if (tid == 0) st_agent(&hdr->cnt[slot][0], 0u);
+      for (int d = tid; d < la.n_dn; d += kLayerThreads) st_agent(&mailbox(la.sync, d)->h_ready[slot], 1u);
+    }
+    return;
+  }
+
+  // ================================================================== down block
+  const int t = b - n_gu, slot = wv;
+  LayerMailbox *my = mailbox(la.sync, t);
+  uint8_t *s_h = reinterpret_cast<uint8_t *>(smem);  // [slot] activation records of h
+  // 1. routing
+  if (wv == 0) {
+    float l;
+    const bool ok = await_routing(cp, tc, la.spin_limit, lane, &l, s_order, s_w, &s_sel);
+    release_copy(cp, readers, E, lane);
+    if (lane == 0) s_flag = !ok || err0;
+  }
+  __syncthreads();
+  bool timeout = s_flag;
+  const int sel = timeout ? 0 : s_sel;
+  const bool ok = slot < sel && slot < K;
+  const uint8_t *rec = a.base + (size_t)(ok ? s_order[slot] : 0) * a.stride;
+  // 2. the down tile and its bias, streamed while gate_up runs
+  TileRegs<kLayerNs> r;
+  tile_load<kLayerNs>(r, rec + a.dn_off, a.dn, ok ? t : 0, ok, lane);
+  const float4 bias = reinterpret_cast<const float4 *>(rec + a.dnb_off)[(ok ? t : 0) * 4 + g];
+  // 3. wait for h of the kept slots
+  if (tid == 0 && !timeout) {
+    for (int s = 0; s < sel && !timeout; s++) {
+      for (uint32_t n = 0;; n++) {
+        if (ld_agent(&my->h_ready[s])) break;
+        if (n >= la.spin_limit) {
+          timeout = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    s_flag = timeout;
+  }
+  __syncthreads();
+  timeout = s_flag;
+  // 4. h records of the kept slots -> LDS, 1 KB per wavefront instruction, straight into LDS
+  //    (the buffer and the LDS area extend 1 KB past the last record for the rounding)
+  if (!timeout) {
+    const int nchunk = (sel * Act::kBytes + 1023) / 1024;
+    for (int cix = wv; cix < nchunk; cix += kLayerWaves)
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const uint4 *>(la.hterm + (size_t)cix * 1024) + lane,
+          (__attribute__((address_space(3))) void *)(s_h + (size_t)cix * 1024), 16, 0, 16);
+    wait_mem();
+  }
+  __syncthreads();
+  if (ok && !timeout) {
+    const uint8_t *hrec = s_h + (size_t)slot * Act::kBytes;
+    uint32_t bsw[kLayerNq];
+    load_bsw<kLayerNs>(hrec, bsw, lane);
+    const f32x4 acc = tile_mfma_f8<kLayerNs>(r, hrec, bsw, lane);
+    float v[4];
+    sum_terms(acc, v);
+    if (j == 0) {
+      s_o[slot][g * 4 + 0] = canon_nan(rclamp(v[0] + bias.x, -65504.0f, 65504.0f));
+      s_o[slot][g * 4 + 1] = canon_nan(rclamp(v[1] + bias.y, -65504.0f, 65504.0f));
+      s_o[slot][g * 4 + 2] = canon_nan(rclamp(v[2] + bias.z, -65504.0f, 65504.0f));
+      s_o[slot][g * 4 + 3] = canon_nan(rclamp(v[3] + bias.w, -65504.0f, 65504.0f));
+    }
+  }
+  __syncthreads();
+  if (tid < 16) {  // session.rs:974-980: y = 0; y += w_s * out_s in slot order
+    float y = 0.0f;
+    if (timeout) {
+      y = __uint_as_float(0x7FC00000u);
+    } else {
+      for (int s = 0; s < 4 && s < K; s++)
+        if (s < sel) y = y + s_w[s] * s_o[s][tid];
+    }
+    a.y[t * 16 + tid] = canon_nan(y);
+  }
+  if (tid == 0) {
+    if (timeout) st_agent(&hdr->err, 1u);
+    for (int s = 0; s < 4; s++) st_agent(&my->h_ready[s], 0u);
+  }
+}
+
+size_t decode_layer_lds(const LayerArgs &) { return (size_t)4 * Act::kBytes + 1024; }
+
+// Derived geometry of the one-launch kernel for la.d (the host fills la.d, sync, hterm and
+// spin_limit).
+void layer_geometry(LayerArgs &la) {
+  la.n_gu_per_slot = (int)(la.d.gu.tiles / 4);
+  la.n_dn = (int)la.d.dn.tiles;
+}
+
+size_t layer_hterm_bytes() { return (size_t)4 * Act::kBytes + 1024; }
+
+bool decode_layer_supported(const LayerArgs &la) {
+  const DecodeArgs &a = la.d;
+  return a.k >= 1 && a.k <= 4 && a.E >= 1 && a.E <= 64 && a.k <= a.E && a.rnq >= 1 && a.rnq <= 6 &&
+         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+         a.gu.ns <= (uint32_t)kLayerNs && a.dn.ns <= (uint32_t)kLayerNs && a.H % 32 == 0 &&
+         a.I % 32 == 0 && a.gu.tiles % 4 == 0 &&
+         a.k * la.n_gu_per_slot + la.n_dn <= kLayerMaxBlocks;
+}
+
+hipError_t launch_decode_layer(const LayerArgs &la, hipStream_t s) {
+  const DecodeArgs &a = la.d;
+  if (!decode_layer_supported(la) || !la.sync || !la.hterm) return hipErrorInvalidValue;
+  const dim3 grid(a.k * la.n_gu_per_slot + la.n_dn), block(kLayerThreads);
+  const size_t lds = decode_layer_lds(la);
+  switch (a.rnq) {  // router chain length per lane, in 16-byte loads (6 for H = 2880)
+    case 1: hipLaunchKernelGGL(k_decode_layer<1>, grid, block, lds, s, la); break;
+    case 2: hipLaunchKernelGGL(k_decode_layer<2>, grid, block, lds, s, la); break;
+    case 3: hipLaunchKernelGGL(k_decode_layer<3>, grid, block, lds, s, la); break;
+    case 4: hipLaunchKernelGGL(k_decode_layer<4>, grid, block, lds, s, la); break;
+    case 5: hipLaunchKernelGGL(k_decode_layer<5>, grid, block, lds, s, la); break;
+    default: hipLaunchKernelGGL(k_decode_layer<6>, grid, block, lds, s, la); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace moe

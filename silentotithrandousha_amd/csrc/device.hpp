@@ -9,6 +9,7 @@ namespace moe {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // ------------------------------------------------------------------ scalar helpers
 
@@ -115,20 +116,21 @@ __device__ __forceinline__ float wave_max(float m) {
 
 // Canonical order: lane l accumulates k = l, l+64, ... (k < H) with fused multiply-adds; the
 // 64 partials are combined by a xor butterfly (32, 16, ..., 1); then the bias is added.
-// Device layout of the router ("lane-major"): for expert e and lane l the weights
-// W[e][l + 64 i], i = 0..KIp-1, are contiguous (KIp = ceil(H/64) rounded up to 8, zero
-// padded), so a lane reads its whole chain with KIp/8 16-byte loads. x is staged in LDS with
-// zeros past H; padded terms are fmaf(0, 0, p) = p exactly (p starts at +0 and can never
-// become -0), so the chain equals the unpadded one. NQ = KIp/8 (0: runtime loop).
+// Device layout of the router ("load-major"): lane l's chain k = l + 64 i, i = 0..KIp-1
+// (KIp = ceil(H/64) rounded up to 8, zero padded) is read with KIp/8 16-byte loads; load q of
+// expert e holds W[e][l + 64 (8q + h)], h = 0..7, at uint4 index (e * NQ + q) * 64 + l, so one
+// load instruction of a wavefront reads 1 KB of consecutive bytes. x is staged with zeros past
+// H; padded terms are fmaf(0, 0, p) = p exactly (p starts at +0 and can never become -0), so
+// the chain equals the unpadded one. NQ = KIp/8 (0: runtime loop). w_e: expert e's weights.
 template <int NQ>
-__device__ __forceinline__ float router_dot(const uint16_t *w_lane, const float *s_x, int nq,
+__device__ __forceinline__ float router_dot(const uint16_t *w_e, const float *s_x, int nq,
                                             int lane) {
   float p = 0.0f;
-  const uint4 *wq = reinterpret_cast<const uint4 *>(w_lane);
+  const uint4 *wq = reinterpret_cast<const uint4 *>(w_e) + lane;
   if (NQ > 0) {
     uint4 v[NQ > 0 ? NQ : 1];
 #pragma unroll
-    for (int q = 0; q < NQ; q++) v[q] = wq[q];
+    for (int q = 0; q < NQ; q++) v[q] = wq[q * 64];
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
       const uint32_t u[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
@@ -140,7 +142,7 @@ __device__ __forceinline__ float router_dot(const uint16_t *w_lane, const float 
     }
   } else {
     for (int q = 0; q < nq; q++) {
-      const uint4 vq = wq[q];
+      const uint4 vq = wq[q * 64];
       const uint32_t u[4] = {vq.x, vq.y, vq.z, vq.w};
       for (int h = 0; h < 8; h++) {
         const uint16_t b = (uint16_t)(u[h >> 1] >> (16 * (h & 1)));
@@ -166,9 +168,9 @@ __device__ __forceinline__ void router_load(RouterRegs<RNQ, RB> &R, const uint16
 #pragma unroll
   for (int r = 0; r < RB; r++) {
     const int e = min(e0 + r * estride, E - 1);
-    const uint4 *wq = reinterpret_cast<const uint4 *>(rw + ((size_t)e * 64 + lane) * RNQ * 8);
+    const uint4 *wq = reinterpret_cast<const uint4 *>(rw + (size_t)e * RNQ * 512) + lane;
 #pragma unroll
-    for (int q = 0; q < RNQ; q++) R.v[r][q] = wq[q];
+    for (int q = 0; q < RNQ; q++) R.v[r][q] = wq[q * 64];
   }
 }
 
@@ -271,12 +273,13 @@ __device__ __forceinline__ uint32_t rank_key(float v) {
 // keys read with v_readlane; every thread of the block calls (two barriers). s_logit[E] is
 // read. On return s_order[s] holds the expert of slot s (-1 past the kept count), s_w[s] its
 // weight and *s_sel the kept count. s_pn: kMaxTopK floats of scratch.
+// Q = ceil(E / 64) logits per lane (1 for E <= 64, the GPT-OSS-20B router).
+template <int Q = kMaxExperts / 64>
 __device__ __forceinline__ void block_topk(const TopkCfg &c, const float *s_logit, float *s_pn,
                                            int *s_order, float *s_w, int *s_sel) {
   const int E = c.E;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    constexpr int Q = kMaxExperts / 64;
     float l[Q], p[Q];
     uint32_t key[Q];
     float m = -INFINITY;
@@ -347,6 +350,132 @@ __device__ __forceinline__ void block_topk(const TopkCfg &c, const float *s_logi
   __syncthreads();
 }
 
+// block_topk for E <= 64 with the same arithmetic, done by one wavefront with logit e in lane e
+// (lanes >= E ignored): the kept probabilities are gathered in slot order into uniform
+// registers (ballot + readlane), so the adaptive count and the renormalisation need no pass
+// through LDS. Writes s_order / s_w / *s_sel; the caller synchronises.
+__device__ __forceinline__ void wave_topk64(const TopkCfg &c, float l, int lane, int *s_order,
+                                            float *s_w, int *s_sel) {
+  const int E = c.E;
+  const bool valid = lane < E;
+  const uint32_t key = rank_key(l);
+  const float m = wave_max(valid ? l : -INFINITY);
+  const float p = valid ? expf(l - m) : 0.0f;
+  const float sum = wave_sum_xor(p);
+  const float pn = sum > 0.0f ? p / sum : p;
+  int rank = 0;
+  for (int f = 0; f < E; f++) {
+    const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)key, f);
+    rank += (kf > key || (kf == key && f < lane)) ? 1 : 0;
+  }
+  const int kk = c.k < E ? c.k : E;
+  float ps[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) {  // slots 0..3 (the single-token kernels keep k <= 4)
+    const uint64_t mask = __ballot(valid && rank == s);
+    const int src = mask ? __builtin_ctzll(mask) : 0;
+    ps[s] = mask ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pn), src)) : 0.0f;
+  }
+  int sel = kk;
+  if (c.adaptive && kk > 1) {
+    const float margin = fmaxf(ps[0] - ps[1], 0.0f);
+    if (ps[0] >= c.top1_min && margin >= c.margin_min)
+      sel = 1;
+    else if (ps[0] + ps[1] >= c.top2_mass)
+      sel = 2;
+    const int mk = c.min_k < kk ? c.min_k : kk;
+    if (sel < mk) sel = mk;
+    if (sel > kk) sel = kk;
+  }
+  float top_sum = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+    if (s < sel) top_sum = top_sum + ps[s];
+  const bool ok = isfinite(top_sum) && top_sum > 0.0f;
+  if (valid && rank < sel) {
+    s_order[rank] = lane;
+    s_w[rank] = ok ? canon_nan(pn / top_sum) : 1.0f / (float)sel;
+  }
+  if (lane >= sel && lane < c.k) {
+    s_order[lane] = -1;
+    s_w[lane] = 0.0f;
+  }
+  if (lane == 0) *s_sel = sel;
+}
+
+__device__ __forceinline__ void block_topk64(const TopkCfg &c, const float *s_logit, int *s_order,
+                                             float *s_w, int *s_sel) {
+  if (threadIdx.x < 64)
+    wave_topk64(c, s_logit[min((int)threadIdx.x, c.E - 1)], (int)threadIdx.x, s_order, s_w, s_sel);
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ fp8 activation terms
+//
+// The block-scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4) takes the MXFP4 weights as they are
+// (E2M1 nibbles with their E8M0 scales) and the activation as OCP fp8 e4m3 with one E8M0 scale
+// per 32 values. An f32 activation block is sent as kTerms fp8 terms, x = sum_t q_t 2^(e_t),
+// with e_0 chosen so the block's largest magnitude scales into [128, 256) and e_t = e_0 - 4t.
+// Term t rounds the residual left by the terms before it to e4m3 (round to nearest even, 4
+// significant bits), so each term divides a value's remaining error by at least 2^4 while it
+// stays in e4m3's normal range, and the residual after the last term is below 2^-16 of the
+// value (the bf16 hi+lo split keeps 2^-17). Every residual is exact in f32 (the rounded term is
+// within a factor of two of the residual it rounds). Products of E2M1, e4m3 and power-of-two
+// scales are exact in the MFMA, which accumulates in f32.
+constexpr int kTerms = 4;
+
+// Splits the 8 consecutive values x[0..7] of a lane; the 4 lanes of an aligned quad hold one
+// 32-value block (lane % 4 = which 8). q[t] = the 8 term-t bytes (value i in byte i % 4 of
+// word i / 4); s4 byte t = E8M0 scale of term t (uniform over the quad). A non-finite value in
+// the block makes term 0 all fp8 NaN (0x7F), so every product with the block is NaN where the
+// f32 path's result would be non-finite.
+__device__ __forceinline__ void split8_fp8(const float x[8], uint2 q[kTerms], uint32_t &s4) {
+  float m = 0.0f, bad = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    m = fmaxf(m, fabsf(x[i]));
+    if (!isfinite(x[i])) bad = 1.0f;
+  }
+  m = fmaxf(m, xor_lane<1>(m));
+  m = fmaxf(m, xor_lane<2>(m));
+  bad = fmaxf(bad, xor_lane<1>(bad));
+  bad = fmaxf(bad, xor_lane<2>(bad));
+  if (bad != 0.0f) {
+    q[0] = make_uint2(0x7F7F7F7Fu, 0x7F7F7F7Fu);
+#pragma unroll
+    for (int t = 1; t < kTerms; t++) q[t] = make_uint2(0u, 0u);
+    s4 = 127u;
+    return;
+  }
+  int e0 = -127;
+  if (m > 0.0f) {
+    int E;
+    (void)frexpf(m, &E);  // m in [2^(E-1), 2^E)
+    e0 = max(E - 8, -127);
+  }
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) r[i] = x[i];
+  s4 = 0u;
+#pragma unroll
+  for (int t = 0; t < kTerms; t++) {
+    const int e = max(e0 - 4 * t, -127);
+    uint32_t w[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int p = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(r[4 * h], -e), ldexpf(r[4 * h + 1], -e), 0, false);
+      p = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(r[4 * h + 2], -e), ldexpf(r[4 * h + 3], -e), p, true);
+      w[h] = (uint32_t)p;
+      r[4 * h + 0] = r[4 * h + 0] - ldexpf(__builtin_amdgcn_cvt_f32_fp8(p, 0), e);
+      r[4 * h + 1] = r[4 * h + 1] - ldexpf(__builtin_amdgcn_cvt_f32_fp8(p, 1), e);
+      r[4 * h + 2] = r[4 * h + 2] - ldexpf(__builtin_amdgcn_cvt_f32_fp8(p, 2), e);
+      r[4 * h + 3] = r[4 * h + 3] - ldexpf(__builtin_amdgcn_cvt_f32_fp8(p, 3), e);
+    }
+    q[t] = make_uint2(w[0], w[1]);
+    s4 |= (uint32_t)(e + 127) << (8 * t);
+  }
+}
+
 // ------------------------------------------------------------------ one 16-row MXFP4 tile
 
 // Registers of one tile: every 16-byte weight chunk and scale word a lane needs.
@@ -405,6 +534,103 @@ __device__ __forceinline__ f32x4 tile_mfma(const TileRegs<NSMAX> &r, const PackD
     }
   }
   return (acc0 + acc1) + (acc2 + acc3);
+}
+
+// One block-scaled MFMA, A = E2M1, B = e4m3, scales = byte `op` of the scale words (op is a
+// constant after unrolling; the instruction needs it as an immediate).
+template <int OP>
+__device__ __forceinline__ f32x4 mfma_fp4_fp8_op(const i32x8 &A, const i32x8 &B, f32x4 c, uint32_t sa,
+                                                 uint32_t sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, c, 4, 0, OP, (int)sa, OP, (int)sb);
+}
+__device__ __forceinline__ f32x4 mfma_fp4_fp8(int op, const i32x8 &A, const i32x8 &B, f32x4 c,
+                                              uint32_t sa, uint32_t sb) {
+  switch (op) {
+    case 0: return mfma_fp4_fp8_op<0>(A, B, c, sa, sb);
+    case 1: return mfma_fp4_fp8_op<1>(A, B, c, sa, sb);
+    case 2: return mfma_fp4_fp8_op<2>(A, B, c, sa, sb);
+    default: return mfma_fp4_fp8_op<3>(A, B, c, sa, sb);
+  }
+}
+
+// Activation record in LDS or HBM for the block-scaled MFMA, for rows of up to 4 * NSMAX
+// 32-value blocks (blocks past the row are zero): term t, block b, value i at byte
+// t * kTermStride + 32 b + i; the E8M0 scale of (t, b) at byte
+// kTerms * kTermStride + (4 t + b % 4) * NSMAX + b / 4, so a lane of group g finds the scales of
+// its blocks 4s + g, s = 0..NSMAX-1, in consecutive bytes. The term stride is 64 bytes past a
+// multiple of 256, so the 4 terms read by one MFMA step fall in different LDS banks.
+template <int NSMAX>
+struct ActRecord {
+  static constexpr int kTermStride = 4 * NSMAX * 32 + 64;
+  static constexpr int kScaleOff = kTerms * kTermStride;
+  static constexpr int kBytes = kScaleOff + kTerms * 4 * NSMAX;
+  __host__ __device__ static constexpr int term(int t, int b) { return t * kTermStride + 32 * b; }
+  __host__ __device__ static constexpr int scale(int t, int b) { return kScaleOff + (4 * t + (b & 3)) * NSMAX + (b >> 2); }
+};
+
+// MFMA sweep of a loaded tile against an activation record (split8_fp8 terms) on
+// v_mfma_scale_f32_16x16x128_f8f6f4: A = the tile's raw E2M1 chunks with their E8M0 scale words
+// (lane group g holds block 4s+g, its scale in byte s%4 of word s/4; steps past the tile's are
+// zero), B column j = term j % kTerms. B lane layout (measured on gfx950): lane (column j,
+// group gb) supplies bytes 0..15 = values 16(gb&1)..16(gb&1)+15 of block 4s+(gb>>1), bytes
+// 16..31 = the same values of block 4s+2+(gb>>1), and the scale of block 4s+gb. Lanes of
+// columns >= kTerms read the same bytes as column j % kTerms (a broadcast) with scale byte 0;
+// their columns are never read. bsw: the lane's B scale words (byte i of word q = scale of
+// block 4(4q+i)+gb of its term; 0 for columns >= kTerms). Runs all NSMAX steps without
+// branches. Returns rows 4*(lane/16)+i of column lane%16.
+template <int NSMAX>
+__device__ __forceinline__ f32x4 tile_mfma_f8(const TileRegs<NSMAX> &r, const uint8_t *rec,
+                                              const uint32_t *bsw, int lane) {
+  using R = ActRecord<NSMAX>;
+  const int j = lane & 15, gb = lane >> 4;
+  const uint8_t *bt = rec + R::term(j & (kTerms - 1), gb >> 1) + 16 * (gb & 1);
+  f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+  // B of step s is read two steps ahead so the LDS latency hides behind the MFMAs
+  constexpr int PD = 2;
+  uint4 pb0[PD], pb1[PD];
+#pragma unroll
+  for (int s = 0; s < PD; s++) {
+    pb0[s] = *reinterpret_cast<const uint4 *>(bt + s * 128);
+    pb1[s] = *reinterpret_cast<const uint4 *>(bt + s * 128 + 64);
+  }
+#pragma unroll
+  for (int s = 0; s < NSMAX; s++) {
+    const uint4 b0 = pb0[s % PD], b1 = pb1[s % PD];
+    if (s + PD < NSMAX) {
+      pb0[s % PD] = *reinterpret_cast<const uint4 *>(bt + (s + PD) * 128);
+      pb1[s % PD] = *reinterpret_cast<const uint4 *>(bt + (s + PD) * 128 + 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads PD steps ahead of their MFMA
+    const uint4 a = r.raw[s];
+    const i32x8 A = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    const i32x8 B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                     (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    if (s & 1)
+      acc1 = mfma_fp4_fp8(s & 3, A, B, acc1, r.sw[s / 4], bsw[s / 4]);
+    else
+      acc0 = mfma_fp4_fp8(s & 3, A, B, acc0, r.sw[s / 4], bsw[s / 4]);
+  }
+  return acc0 + acc1;
+}
+
+// The lane's B scale words for tile_mfma_f8 from an activation record.
+template <int NSMAX>
+__device__ __forceinline__ void load_bsw(const uint8_t *rec, uint32_t *bsw, int lane) {
+  using R = ActRecord<NSMAX>;
+  const int j = lane & 15, gb = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < NSMAX / 4; q++)
+    bsw[q] = j < kTerms ? *reinterpret_cast<const uint32_t *>(rec + R::scale(j, gb) + 4 * q) : 0u;
+}
+
+// Sum of the kTerms term columns of an MFMA result: lanes with lane % 16 == 0 get
+// (t0 + t1) + (t2 + t3) for each of their 4 rows.
+__device__ __forceinline__ void sum_terms(const f32x4 &acc, float v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float u = acc[i] + xor_lane<1>(acc[i]);
+    v[i] = u + xor_lane<2>(u);
+  }
 }
 
 }  // namespace moe

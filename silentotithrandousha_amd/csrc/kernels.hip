@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
   }
   __syncthreads();
   for (int e = wv; e < E; e += nw) {
-    const float p = router_dot<KI>(a.w + ((size_t)e * 64 + lane) * nq * 8, s_x, nq, lane);
+    const float p = router_dot<KI>(a.w + (size_t)e * nq * 512, s_x, nq, lane);
     if (lane == 0) s_logit[e] = canon_nan(p + a.bias[e]);
   }
   __syncthreads();

@@ -15,7 +15,7 @@ constexpr int kMaxTopK = 16;
 enum GemvMode { GEMV_GATE_UP = 0, GEMV_DOWN = 1, GEMV_RAW = 2 };
 
 struct RouteArgs {
-  const uint16_t *w;     // lane-major router: [E][64][KIp] bf16 bits (see router_dot)
+  const uint16_t *w;     // load-major router: [E][KIp/8][64 lanes][8] bf16 bits (router_dot)
   const float *bias;     // [E]
   const float *x;        // [T, H]
   int T, E, H, k;
@@ -47,7 +47,7 @@ struct GemvArgs {
 
 // Single-token MoE layer in two launches (decode.hip).
 struct DecodeArgs {
-  const uint16_t *rw;  // lane-major router (see router_dot)
+  const uint16_t *rw;  // load-major router (see router_dot)
   const float *rb;     // [E]
   int rnq, Hr;         // 16-byte loads per router lane chain; router x length (64 * 8 * rnq)
   const uint8_t *base; // expert records of the layer
@@ -65,6 +65,24 @@ struct DecodeArgs {
   uint16_t *hsplit;    // [k, 2, I]
   int n_gu_wg_per_slot;
 };
+
+// One-launch single-token layer (decode_layer.hip): DecodeArgs plus the cross-block
+// signalling area (zeroed once at context creation; it returns to zero after every launch)
+// and the h-terms buffer (zeroed once; padding blocks stay zero).
+constexpr int kLayerMaxBlocks = 1024;
+struct LayerArgs {
+  DecodeArgs d;
+  void *sync;            // layer_sync_bytes(kLayerMaxBlocks) bytes
+  uint8_t *hterm;        // layer_hterm_bytes() bytes: per slot the fp8 terms of h + scales
+  uint32_t spin_limit;   // polls before a wait gives up
+  int n_gu_per_slot;     // filled by layer_geometry: gate_up tiles / 4 = h blocks of 32
+  int n_dn;              //                           down tiles
+};
+size_t layer_sync_bytes(int max_blocks);
+size_t layer_hterm_bytes();
+void layer_geometry(LayerArgs &la);
+bool decode_layer_supported(const LayerArgs &la);
+hipError_t launch_decode_layer(const LayerArgs &a, hipStream_t s);
 
 bool decode_supported(const DecodeArgs &a);
 hipError_t launch_decode_gate_up(const DecodeArgs &a, hipStream_t s);

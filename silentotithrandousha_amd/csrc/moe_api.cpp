@@ -73,7 +73,7 @@ struct Layer {
   size_t n_experts = 0;
   std::vector<uint8_t> loaded;  // per expert: its record has been written
   size_t n_loaded = 0;
-  DevBuf router;   // lane-major bf16 [E][64][KIp] then [E] f32
+  DevBuf router;   // load-major bf16 [E][KIp/8][64][8] then [E] f32
   size_t router_experts = 0;
 };
 
@@ -84,7 +84,10 @@ struct Work {
   int32_t *idx, *n_active, *active_ids, *active_off, *entry_src, *pos;
 };
 
-enum { K_ROUTE = 0, K_BUCKET, K_GATE_UP, K_DOWN, K_COMBINE, K_DECODE_GATE_UP, K_DECODE_DOWN, K_COUNT };
+enum {
+  K_ROUTE = 0, K_BUCKET, K_GATE_UP, K_DOWN, K_COMBINE, K_DECODE_GATE_UP, K_DECODE_DOWN,
+  K_DECODE_LAYER, K_COUNT
+};
 
 struct TimingRec {
   int kernel;
@@ -113,7 +116,12 @@ struct moe_ctx {
   size_t lm_vocab = 0;
   bool timing = false;
   bool capturing = false;
-  bool fused_decode = true;  // single-token forward through the two decode kernels
+  // single-token forwards: 0 = the batch path, 1 = two decode kernels, 2 = one launch
+  // (falls back to 1, then 0, where a shape is not supported)
+  int decode_mode = 2;
+  DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
+  DevBuf layer_h;     // h terms of the one-launch kernel (padding stays zero)
+  uint32_t spin_limit = 1u << 20;
   std::vector<TimingRec> recs;
   std::vector<hipEvent_t> pool;
   double acc_ms[K_COUNT] = {};
@@ -254,6 +262,17 @@ int run_experts(moe_ctx *c, const uint8_t *base, int max_active, int max_entries
   return MOE_OK;
 }
 
+// The one-launch kernel sets a sticky error word when one of its bounded waits ran out (its
+// outputs are NaN from then on). Reports it once and clears the signalling area.
+int check_layer_sync(moe_ctx *c) {
+  uint32_t err = 0;
+  HIP_TRY(hipMemcpy(&err, c->layer_sync.p, 4, hipMemcpyDeviceToHost));
+  if (!err) return MOE_OK;
+  HIP_TRY(hipMemset(c->layer_sync.p, 0, layer_sync_bytes(kLayerMaxBlocks)));
+  return fail(MOE_ERR_HIP, "single-token layer kernel: a cross-block wait ran out (outputs since "
+                           "the last synchronisation are NaN)");
+}
+
 // expert < 0: every expert of the layer must be preloaded; else that one expert.
 int check_layer(moe_ctx *c, size_t layer, bool need_router, long expert = -1) {
   if (layer >= c->layers.size() || !c->layers[layer].experts.p)
@@ -360,7 +379,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     return fail(MOE_ERR_INVALID, "top_k %zu outside [1, min(%d, %zu)]", k, kMaxTopK, E);
   if (T > (size_t)1 << 20) return fail(MOE_ERR_INVALID, "n_tokens %zu too large", T);
   RETURN_IF(ensure_work(c, T, k, E));
-  if (T == 1 && c->fused_decode) {
+  if (T == 1 && c->decode_mode > 0) {
     DecodeArgs da{};
     da.rw = (const uint16_t *)Ly.router.p;
     da.rb = (const float *)((const char *)Ly.router.p + al(router_bytes(c->H, E)));
@@ -391,6 +410,14 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     da.wts = c->w.wts;
     da.hsplit = c->w.hsplit;
     da.n_gu_wg_per_slot = (int)((c->L.gu.tiles + 3) / 4);
+    LayerArgs la{};
+    la.d = da;
+    la.sync = c->layer_sync.p;
+    la.hterm = (uint8_t *)c->layer_h.p;
+    la.spin_limit = c->spin_limit;
+    layer_geometry(la);
+    if (c->decode_mode == 2 && decode_layer_supported(la))
+      return timed(c, K_DECODE_LAYER, s, [&] { return launch_decode_layer(la, s); });
     if (decode_supported(da)) {
       RETURN_IF(timed(c, K_DECODE_GATE_UP, s, [&] { return launch_decode_gate_up(da, s); }));
       return timed(c, K_DECODE_DOWN, s, [&] { return launch_decode_down(da, s); });
@@ -469,6 +496,12 @@ int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ct
   if (e != hipSuccess) {
     delete c;
     return fail(MOE_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  const size_t sb = layer_sync_bytes(kLayerMaxBlocks), hb = layer_hterm_bytes();
+  if (c->layer_sync.ensure(sb) != MOE_OK || hipMemset(c->layer_sync.p, 0, sb) != hipSuccess ||
+      c->layer_h.ensure(hb) != MOE_OK || hipMemset(c->layer_h.p, 0, hb) != hipSuccess) {
+    moe_destroy(c);
+    return fail(MOE_ERR_OOM, "signalling area of %zu bytes", sb);
   }
   *out = c;
   return MOE_OK;
@@ -589,13 +622,16 @@ int moe_preload_router(moe_ctx *c, size_t layer, size_t n_experts, const uint16_
     return fail(MOE_ERR_INVALID, "n_experts %zu outside [1, %d]", n_experts, kMaxExperts);
   if (c->layers.size() <= layer) c->layers.resize(layer + 1);
   Layer &Ly = c->layers[layer];
-  // lane-major layout of the router (kernels.hip, router_dot): [E][64][KIp]
+  // load-major layout of the router (device.hpp, router_dot): [E][KIp/8][64 lanes][8]
   const size_t kip = router_kip(c->H);
   const size_t wb = router_bytes(c->H, n_experts), tot = al(wb) + n_experts * 4;
   RETURN_IF(Ly.router.ensure(tot));
   std::vector<uint16_t> lm(n_experts * 64 * kip, 0);
   for (size_t e = 0; e < n_experts; e++)
-    for (size_t k = 0; k < c->H; k++) lm[(e * 64 + k % 64) * kip + k / 64] = w[e * c->H + k];
+    for (size_t k = 0; k < c->H; k++) {
+      const size_t i = k / 64;  // position in lane k % 64's chain
+      lm[((e * (kip / 8) + i / 8) * 64 + k % 64) * 8 + i % 8] = w[e * c->H + k];
+    }
   HIP_TRY(hipMemcpy(Ly.router.p, lm.data(), wb, hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy((char *)Ly.router.p + al(wb), bias, n_experts * 4, hipMemcpyHostToDevice));
   Ly.router_experts = n_experts;
@@ -760,7 +796,7 @@ int moe_layer_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   RETURN_IF(forward_device(c, layer, c->w.x, T, k, c->w.y, c->stream));
   HIP_TRY(hipMemcpyAsync(y, c->w.y, T * c->H * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
-  return MOE_OK;
+  return check_layer_sync(c);
 }
 
 int moe_layer_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
@@ -866,13 +902,20 @@ int moe_memset_device(void *dst, int value, size_t bytes) {
 int moe_synchronize(moe_ctx *c) {
   RETURN_IF(use_dev(c));
   HIP_TRY(hipStreamSynchronize(c->stream));
-  return MOE_OK;
+  return check_layer_sync(c);
 }
 
 int moe_set_option(moe_ctx *c, int option, int64_t value) {
   if (!c) return fail(MOE_ERR_INVALID, "null context");
   switch (option) {
-    case MOE_OPT_FUSED_DECODE: c->fused_decode = value != 0; return MOE_OK;
+    case MOE_OPT_FUSED_DECODE:
+      if (value < 0 || value > 2) return fail(MOE_ERR_INVALID, "MOE_OPT_FUSED_DECODE is 0, 1 or 2");
+      c->decode_mode = (int)value;
+      return MOE_OK;
+    case MOE_OPT_SPIN_LIMIT:
+      if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");
+      c->spin_limit = (uint32_t)value;
+      return MOE_OK;
     default: return fail(MOE_ERR_INVALID, "unknown option %d", option);
   }
 }

@@ -119,8 +119,14 @@ class GpuMoeDispatcher:
         check(lib().moe_preload_expert(self._ctx, layer_idx, n_experts, expert_idx, *args))
 
     def set_fused_decode(self, on):
+        """True / 2: one launch (default); 1: two launches; False / 0: the batch path."""
         from ._ffi import MOE_OPT_FUSED_DECODE
-        check(lib().moe_set_option(self._ctx, MOE_OPT_FUSED_DECODE, int(bool(on))))
+        mode = 2 if on is True else (0 if on is False else int(on))
+        check(lib().moe_set_option(self._ctx, MOE_OPT_FUSED_DECODE, mode))
+
+    def set_spin_limit(self, polls):
+        from ._ffi import MOE_OPT_SPIN_LIMIT
+        check(lib().moe_set_option(self._ctx, MOE_OPT_SPIN_LIMIT, int(polls)))
 
     def set_adaptive_topk(self, enabled, min_k=3, top1_min_prob=0.90, top1_min_margin=0.35,
                           top2_min_mass=0.98):
