@@ -43,6 +43,21 @@
 
 namespace moe {
 
+// Timeline tracing for development builds (-DMOE_TRACE_TIMELINE): thread 0 of each block
+// records the realtime counter (100 MHz) at numbered points into moe_trace_ts[block][8],
+// read back with moe_trace_read(). Compiled out otherwise.
+#ifdef MOE_TRACE_TIMELINE
+__device__ long long moe_trace_ts[4096 * 8];
+#define MOE_TRACE(i)                                                                        \
+  do {                                                                                      \
+    if (threadIdx.x == 0) moe_trace_ts[blockIdx.x * 8 + (i)] = (long long)__builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define MOE_TRACE(i) \
+  do {               \
+  } while (0)
+#endif
+
 constexpr int kLayerWaves = 4;
 constexpr int kLayerThreads = 64 * kLayerWaves;
 constexpr int kLayerNs = 24;  // steps per tile: K <= 3072
@@ -175,6 +190,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   const int j = lane & 15, g = lane >> 4;
 
   // ---------------------------------------------------------------- router wavefronts
+  MOE_TRACE(0);
   const int gw = b * kLayerWaves + wv;
   if (gw < E) {
     float xr[XI];
@@ -216,6 +232,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
         for (int t = 0; t < kTerms; t++) s_x[Act::scale(t, bb)] = (uint8_t)(s4 >> (8 * t));
       }
     }
+    MOE_TRACE(1);
     // 2. routing
     if (wv == 0) {
       float l;
@@ -231,6 +248,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
       }
     }
     __syncthreads();
+    MOE_TRACE(2);
     const bool timeout = s_flag;
     const int sel = s_sel;
     const int slot = b / NGS;
@@ -250,6 +268,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     const f32x4 acc = tile_mfma_f8<kLayerNs>(r, s_x, bsw, lane);
     float v[4];
     sum_terms(acc, v);
+    MOE_TRACE(3);
     if (j == 0) {
       s_h32[wv * 8 + 2 * g] = swiglu(v[0] + bias.x, v[1] + bias.y, a.limit);
       s_h32[wv * 8 + 2 * g + 1] = swiglu(v[2] + bias.z, v[3] + bias.w, a.limit);
@@ -288,9 +307,11 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
       s_flag = old == (uint32_t)NGS - 1;
     }
     __syncthreads();
+    MOE_TRACE(4);
     if (s_flag) {  // the last gate_up block of this slot: its h terms are complete
       if (tid == 0) st_agent(&hdr->cnt[slot][0], 0u);
       for (int d = tid; d < la.n_dn; d += kLayerThreads) st_agent(&mailbox(la.sync, d)->h_ready[slot], 1u);
+      MOE_TRACE(5);
     }
     return;
   }
@@ -307,6 +328,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     if (lane == 0) s_flag = !ok || err0;
   }
   __syncthreads();
+  MOE_TRACE(1);
   bool timeout = s_flag;
   const int sel = timeout ? 0 : s_sel;
   const bool ok = slot < sel && slot < K;
@@ -330,6 +352,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     s_flag = timeout;
   }
   __syncthreads();
+  MOE_TRACE(2);
   timeout = s_flag;
   // 4. h records of the kept slots -> LDS, 1 KB per wavefront instruction, straight into LDS
   //    (the buffer and the LDS area extend 1 KB past the last record for the rounding)
@@ -342,6 +365,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     wait_mem();
   }
   __syncthreads();
+  MOE_TRACE(3);
   if (ok && !timeout) {
     const uint8_t *hrec = s_h + (size_t)slot * Act::kBytes;
     uint32_t bsw[kLayerNq];
@@ -367,6 +391,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
     a.y[t * 16 + tid] = canon_nan(y);
   }
+  MOE_TRACE(4);
   if (tid == 0) {
     if (timeout) st_agent(&hdr->err, 1u);
     for (int s = 0; s < 4; s++) st_agent(&my->h_ready[s], 0u);
@@ -410,3 +435,10 @@ hipError_t launch_decode_layer(const LayerArgs &la, hipStream_t s) {
 }
 
 }  // namespace moe
+
+#ifdef MOE_TRACE_TIMELINE
+extern "C" int moe_trace_read(long long *out, int n_blocks) {
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(moe::moe_trace_ts), (size_t)n_blocks * 8 * 8, 0,
+                                  hipMemcpyDeviceToHost);
+}
+#endif

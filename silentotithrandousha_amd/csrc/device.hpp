@@ -10,6 +10,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ scalar helpers
 
@@ -486,7 +487,9 @@ struct TileRegs {
 };
 
 // Issues every weight and scale load of tile t of a resident matrix (layout.hpp). Lanes of
-// missing blocks (the partial last step) and !ok tiles load nothing and hold zeros.
+// missing blocks (the partial last step) and !ok tiles load nothing and hold zeros. The weights
+// are read once per use, so they are loaded non-temporally (measured ~5% faster for the
+// single-token layer than cached loads).
 template <int NSMAX>
 __device__ __forceinline__ void tile_load(TileRegs<NSMAX> &r, const uint8_t *mat, const PackDims &d,
                                           int t, bool ok, int lane) {
@@ -499,7 +502,10 @@ __device__ __forceinline__ void tile_load(TileRegs<NSMAX> &r, const uint8_t *mat
 #pragma unroll
   for (int s = 0; s < NSMAX; s++) {
     r.raw[s] = make_uint4(0u, 0u, 0u, 0u);
-    if (ok && s < (int)d.ns && 4 * s + g < (int)d.nb) r.raw[s] = wp[s * 64 + lane];
+    if (ok && s < (int)d.ns && 4 * s + g < (int)d.nb) {
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp) + s * 64 + lane);
+      r.raw[s] = make_uint4(v.x, v.y, v.z, v.w);
+    }
   }
 }
 
