@@ -161,7 +161,7 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
     disp.synchronize()
     kt = {name: disp.get_timing(kid) for kid, name in
           enumerate(["route", "bucket", "gate_up", "down", "combine", "decode_gate_up",
-                     "decode_down", "decode_layer"])}
+                     "decode_down", "decode_layer", "split"])}
     disp.set_timing(False)
     if graph:
         check(L.moe_graph_destroy(graph))
@@ -194,7 +194,7 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
                    "graph_replay": bool(graph), "fused_decode": bool(args.fused and T == 1)},
         "roofline": {"bound": "hbm",
                      "kernel": {"decode_layer": "k_decode_layer", "decode_gate_up": "k_decode_gate_up",
-                                "gate_up": "k_expert_gemv<gate_up>"}[dom],
+                                "gate_up": "k_gemm_fp8<gate_up>"}[dom],
                      "achieved": round(gu_bytes / gu_avg_s / 1e9, 1) if gu_n else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_bytes / gu_avg_s / 1e9 / HBM_PEAK_GBS, 4) if gu_n else None,

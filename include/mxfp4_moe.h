@@ -74,8 +74,12 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * agree to the matmul tolerance; routing is identical.
  * MOE_OPT_SPIN_LIMIT: polls before a cross-block wait of the one-launch kernel gives up
  * (default 2^20); a wait that gives up makes the outputs NaN and the next moe_synchronize or
- * moe_layer_forward return MOE_ERR_HIP (which clears the condition). */
-enum moe_option { MOE_OPT_FUSED_DECODE = 1, MOE_OPT_SPIN_LIMIT = 2 };
+ * moe_layer_forward return MOE_ERR_HIP (which clears the condition).
+ * MOE_OPT_BATCH_GEMM: batches (n_tokens > 1) run through the grouped GEMM on the block-scaled
+ * MFMA (activations as fp8 terms, exact to 2^-12) when 1 (default) and experts average at
+ * least 32 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
+ * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical. */
+enum moe_option { MOE_OPT_FUSED_DECODE = 1, MOE_OPT_SPIN_LIMIT = 2, MOE_OPT_BATCH_GEMM = 3 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 
 /* ------------------------------------------------------------------ weights */
@@ -245,7 +249,8 @@ int moe_graph_destroy(void *graph_exec);
  * stream the kernels run on when enabled (no reference counterpart). */
 int moe_set_timing(moe_ctx *ctx, int enabled);
 /* kernel: 0 route, 1 bucket, 2 gate_up, 3 down, 4 combine, 5 single-token router+gate_up,
- * 6 single-token down+combine, 7 single-token layer in one launch.
+ * 6 single-token down+combine, 7 single-token layer in one launch, 8 activation split of a
+ * batch (grouped GEMM path; kernels 2 and 3 are then the grouped GEMMs).
  * Returns accumulated milliseconds
  * and launch count since the last reset; synchronises the context stream. */
 int moe_get_timing(moe_ctx *ctx, int kernel, double *ms, uint64_t *launches);

@@ -423,25 +423,15 @@ __device__ __forceinline__ void block_topk64(const TopkCfg &c, const float *s_lo
 // value (the bf16 hi+lo split keeps 2^-17). Every residual is exact in f32 (the rounded term is
 // within a factor of two of the residual it rounds). Products of E2M1, e4m3 and power-of-two
 // scales are exact in the MFMA, which accumulates in f32.
-constexpr int kTerms = 4;
-
 // Splits the 8 consecutive values x[0..7] of a lane; the 4 lanes of an aligned quad hold one
 // 32-value block (lane % 4 = which 8). q[t] = the 8 term-t bytes (value i in byte i % 4 of
 // word i / 4); s4 byte t = E8M0 scale of term t (uniform over the quad). A non-finite value in
 // the block makes term 0 all fp8 NaN (0x7F), so every product with the block is NaN where the
 // f32 path's result would be non-finite.
-__device__ __forceinline__ void split8_fp8(const float x[8], uint2 q[kTerms], uint32_t &s4) {
-  float m = 0.0f, bad = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    m = fmaxf(m, fabsf(x[i]));
-    if (!isfinite(x[i])) bad = 1.0f;
-  }
-  m = fmaxf(m, xor_lane<1>(m));
-  m = fmaxf(m, xor_lane<2>(m));
-  bad = fmaxf(bad, xor_lane<1>(bad));
-  bad = fmaxf(bad, xor_lane<2>(bad));
-  if (bad != 0.0f) {
+// The split once the block's largest magnitude m and its non-finite flag are known.
+__device__ __forceinline__ void split8_fp8_with_max(const float x[8], float m, bool bad, uint2 q[kTerms],
+                                                    uint32_t &s4) {
+  if (bad) {
     q[0] = make_uint2(0x7F7F7F7Fu, 0x7F7F7F7Fu);
 #pragma unroll
     for (int t = 1; t < kTerms; t++) q[t] = make_uint2(0u, 0u);
@@ -475,6 +465,20 @@ __device__ __forceinline__ void split8_fp8(const float x[8], uint2 q[kTerms], ui
     q[t] = make_uint2(w[0], w[1]);
     s4 |= (uint32_t)(e + 127) << (8 * t);
   }
+}
+
+__device__ __forceinline__ void split8_fp8(const float x[8], uint2 q[kTerms], uint32_t &s4) {
+  float m = 0.0f, bad = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    m = fmaxf(m, fabsf(x[i]));
+    if (!isfinite(x[i])) bad = 1.0f;
+  }
+  m = fmaxf(m, xor_lane<1>(m));
+  m = fmaxf(m, xor_lane<2>(m));
+  bad = fmaxf(bad, xor_lane<1>(bad));
+  bad = fmaxf(bad, xor_lane<2>(bad));
+  split8_fp8_with_max(x, m, bad != 0.0f, q, s4);
 }
 
 // ------------------------------------------------------------------ one 16-row MXFP4 tile
@@ -556,6 +560,17 @@ __device__ __forceinline__ f32x4 mfma_fp4_fp8(int op, const i32x8 &A, const i32x
     case 1: return mfma_fp4_fp8_op<1>(A, B, c, sa, sb);
     case 2: return mfma_fp4_fp8_op<2>(A, B, c, sa, sb);
     default: return mfma_fp4_fp8_op<3>(A, B, c, sa, sb);
+  }
+}
+
+// Same with the B scale in byte 0 of its word (the lane has shifted its own byte there).
+__device__ __forceinline__ f32x4 mfma_fp4_fp8_bs0(int op, const i32x8 &A, const i32x8 &B, f32x4 c,
+                                                  uint32_t sa, uint32_t sb) {
+  switch (op) {
+    case 0: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, c, 4, 0, 0, (int)sa, 0, (int)sb);
+    case 1: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, c, 4, 0, 1, (int)sa, 0, (int)sb);
+    case 2: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, c, 4, 0, 2, (int)sa, 0, (int)sb);
+    default: return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, c, 4, 0, 3, (int)sa, 0, (int)sb);
   }
 }
 

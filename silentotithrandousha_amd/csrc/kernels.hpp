@@ -45,6 +45,36 @@ struct GemvArgs {
   int max_entries_per_expert;
 };
 
+// fp8 terms per activation value for the block-scaled MFMA paths (device.hpp, split8_fp8).
+constexpr int kTerms = 4;
+
+// Step-major activation record of one row (token or entry) for the grouped GEMM (gemm.hip),
+// rows of up to 4 * kGemmNs 32-value blocks: K-step s holds [term t][128 bytes = blocks 4s..4s+3]
+// followed by [term t][4 scale bytes, byte i = E8M0 of block 4s+i]; blocks past the row are zero.
+constexpr int kGemmNs = 24;
+struct GemmRec {
+  static constexpr int kStep = kTerms * 128 + kTerms * 4;
+  static constexpr int kBytes = kGemmNs * kStep;
+  MOE_HD static constexpr int data(int s, int t) { return s * kStep + t * 128; }
+  MOE_HD static constexpr int scale(int s, int t) { return s * kStep + kTerms * 128 + 4 * t; }
+};
+
+struct GemmArgs {
+  const uint8_t *base;       // expert records of the layer
+  size_t stride, mat_off, bias_off;
+  PackDims d;                // weight matrix (rows x K)
+  const int32_t *n_active, *active_ids, *active_off;  // entries grouped by expert (k_bucket)
+  const int32_t *entry_src;  // B record of each entry (NULL: the entry's own)
+  const uint8_t *brec;       // B records (GemmRec)
+  void *out;                 // GATE_UP: h records (GemmRec) per entry; DOWN: f32 [entry][rows]
+  float limit;
+  int max_active;            // upper bound of *n_active
+  int max_col_tiles;         // upper bound of the column tiles (64 entries) over all experts
+  int n_row_blocks;          // set by launch_gemm_fp8 (row blocks of the launch)
+};
+hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *rec, hipStream_t s);
+hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
+
 // Single-token MoE layer in two launches (decode.hip).
 struct DecodeArgs {
   const uint16_t *rw;  // load-major router (see router_dot)

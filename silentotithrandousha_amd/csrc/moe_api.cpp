@@ -81,12 +81,13 @@ struct Layer {
 struct Work {
   float *x, *y, *logits, *wts, *o;
   uint16_t *xsplit, *hsplit;
+  uint8_t *xrec, *hrec;  // grouped GEMM activation records: tokens, entries (padding zero)
   int32_t *idx, *n_active, *active_ids, *active_off, *entry_src, *pos;
 };
 
 enum {
   K_ROUTE = 0, K_BUCKET, K_GATE_UP, K_DOWN, K_COMBINE, K_DECODE_GATE_UP, K_DECODE_DOWN,
-  K_DECODE_LAYER, K_COUNT
+  K_DECODE_LAYER, K_SPLIT, K_COUNT
 };
 
 struct TimingRec {
@@ -119,6 +120,7 @@ struct moe_ctx {
   // single-token forwards: 0 = the batch path, 1 = two decode kernels, 2 = one launch
   // (falls back to 1, then 0, where a shape is not supported)
   int decode_mode = 2;
+  int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 32 entries, 2 always, 0 never
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h terms of the one-launch kernel (padding stays zero)
   uint32_t spin_limit = 1u << 20;
@@ -208,8 +210,14 @@ int ensure_work(moe_ctx *c, size_t T, size_t k, size_t E) {
   size_t o_ao = off; off = al(off + (E + 1) * 4);
   size_t o_es = off; off = al(off + N * 4);
   size_t o_pos = off; off = al(off + N * 4);
+  size_t o_xr = off; off = al(off + T * GemmRec::kBytes);
+  size_t o_hr = off; off = al(off + N * GemmRec::kBytes);
   RETURN_IF(c->work.ensure(off));
   char *b = (char *)c->work.p;
+  // h records are written block by block; their padding past I must read as zeros
+  HIP_TRY(hipMemset(b + o_hr, 0, N * GemmRec::kBytes));
+  c->w.xrec = (uint8_t *)(b + o_xr);
+  c->w.hrec = (uint8_t *)(b + o_hr);
   c->w.x = (float *)(b + o_x);
   c->w.y = (float *)(b + o_y);
   c->w.logits = (float *)(b + o_lg);
@@ -453,7 +461,41 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
                            c->w.active_off, c->w.entry_src, c->w.pos, s);
     }));
   const int max_active = (int)std::min(E, T * k);
-  RETURN_IF(run_experts(c, (const uint8_t *)Ly.experts.p, max_active, (int)std::min(T, (size_t)1 << 30), s));
+  // the grouped GEMM pays off once experts see tens of entries (64-entry tiles); smaller
+  // batches stream each weight tile once through the GEMV kernels
+  if (c->batch_gemm && T > 1 && (c->batch_gemm == 2 || T * k >= 32 * E) && c->L.gu.ns <= (uint32_t)kGemmNs &&
+      c->L.dn.ns <= (uint32_t)kGemmNs &&
+      (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const size_t N = T * k;
+    RETURN_IF(timed(c, K_SPLIT, s, [&] { return launch_split_rows(x, T, c->H, c->w.xrec, s); }));
+    GemmArgs ga{};
+    ga.base = (const uint8_t *)Ly.experts.p;
+    ga.stride = c->L.stride;
+    ga.n_active = c->w.n_active;
+    ga.active_ids = c->w.active_ids;
+    ga.active_off = c->w.active_off;
+    ga.limit = c->clamp;
+    ga.max_active = max_active;
+    ga.max_col_tiles = (int)(max_active + (N + 63) / 64);
+    GemmArgs gu = ga;
+    gu.mat_off = c->L.gu_off;
+    gu.bias_off = c->L.gub_off;
+    gu.d = c->L.gu;
+    gu.entry_src = c->w.entry_src;
+    gu.brec = c->w.xrec;
+    gu.out = c->w.hrec;
+    RETURN_IF(timed(c, K_GATE_UP, s, [&] { return launch_gemm_fp8(GEMV_GATE_UP, gu, s); }));
+    GemmArgs dn = ga;
+    dn.mat_off = c->L.dn_off;
+    dn.bias_off = c->L.dnb_off;
+    dn.d = c->L.dn;
+    dn.entry_src = nullptr;
+    dn.brec = c->w.hrec;
+    dn.out = c->w.o;
+    RETURN_IF(timed(c, K_DOWN, s, [&] { return launch_gemm_fp8(GEMV_DOWN, dn, s); }));
+  } else {
+    RETURN_IF(run_experts(c, (const uint8_t *)Ly.experts.p, max_active, (int)std::min(T, (size_t)1 << 30), s));
+  }
   RETURN_IF(timed(c, K_COMBINE, s, [&] {
     return launch_combine(c->w.o, c->w.pos, c->w.wts, (int)T, (int)k, (int)c->H, 0, y, s);
   }));
@@ -911,6 +953,10 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
     case MOE_OPT_FUSED_DECODE:
       if (value < 0 || value > 2) return fail(MOE_ERR_INVALID, "MOE_OPT_FUSED_DECODE is 0, 1 or 2");
       c->decode_mode = (int)value;
+      return MOE_OK;
+    case MOE_OPT_BATCH_GEMM:
+      if (value < 0 || value > 2) return fail(MOE_ERR_INVALID, "MOE_OPT_BATCH_GEMM is 0, 1 or 2");
+      c->batch_gemm = (int)value;
       return MOE_OK;
     case MOE_OPT_SPIN_LIMIT:
       if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");

@@ -124,6 +124,11 @@ class GpuMoeDispatcher:
         mode = 2 if on is True else (0 if on is False else int(on))
         check(lib().moe_set_option(self._ctx, MOE_OPT_FUSED_DECODE, mode))
 
+    def set_batch_gemm(self, mode):
+        """1 / True: grouped GEMM for large batches (default); 2: for every batch; 0: never."""
+        from ._ffi import MOE_OPT_BATCH_GEMM
+        check(lib().moe_set_option(self._ctx, MOE_OPT_BATCH_GEMM, int(mode)))
+
     def set_spin_limit(self, polls):
         from ._ffi import MOE_OPT_SPIN_LIMIT
         check(lib().moe_set_option(self._ctx, MOE_OPT_SPIN_LIMIT, int(polls)))
