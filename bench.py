@@ -209,6 +209,14 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
                            "frac_mxfp4_peak": round(flops / (ms_per_step / 1e3) / 1e12 / MXFP4_PEAK_TFLOPS, 5)},
         "kernel_us": {n: round(v[0] * 1e3 / max(v[1], 1), 3) for n, v in kt.items() if v[1]},
     }
+    if not args.traffic_kib:  # calibrated PMC measurement of the same kernel and workload
+        tf = os.path.join(ROOT, "profiles", "traffic.json")
+        kname = res["roofline"]["kernel"]
+        if os.path.exists(tf):
+            rec = json.load(open(tf)).get(kname)
+            if rec and rec.get("workload") == config_name:
+                res["roofline"]["traffic"] = rec["bytes_per_launch"]
+                res["roofline"]["traffic_source"] = rec["source"]
     if mfma_bound and gu_n:
         # dense regime: the MFMA roofline against the MXFP4 peak (the arithmetic runs on the
         # bf16 MFMA with a hi+lo split of the activations, i.e. 2x these flops)
@@ -309,8 +317,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--traffic-kib", type=float, default=0.0,
-                    help="HBM KiB per launch of the dominant kernel from calibrated rocprofv3 "
-                         "--pmc FETCH_SIZE + WRITE_SIZE runs, reported as roofline.traffic")
+                    help="HBM KiB per launch of the dominant kernel (overrides the calibrated "
+                         "rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE figure in profiles/traffic.json)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
