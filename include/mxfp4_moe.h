@@ -69,7 +69,7 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
 /* Options (no reference counterpart).
  * MOE_OPT_FUSED_DECODE selects how single-token forwards run: 2 (default) one launch (router,
  * top-k, gate_up, SwiGLU, down and combine, with the down weights streaming during gate_up;
- * up to 64 experts), 1 two launches (router + gate_up; down + combine), 0 the five-kernel
+ * up to 128 experts), 1 two launches (router + gate_up; down + combine), 0 the five-kernel
  * path that batches take. Shapes a mode does not support take the next lower one. Results
  * agree to the matmul tolerance; routing is identical.
  * MOE_OPT_SPIN_LIMIT: polls before a cross-block wait of the one-launch kernel gives up

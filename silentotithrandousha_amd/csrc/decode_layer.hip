@@ -66,11 +66,13 @@ using Act = ActRecord<kLayerNs>;  // x and h records: 4 fp8 terms of up to 3072 
 
 constexpr int kReplicas = 16;
 
-struct LogitCopy {       // kCopyBytes apart
-  uint64_t logit[64];    // (1 << 32) | f32 bits of logit e, 0 when empty
+constexpr int kLayerMaxE = 128;
+
+struct LogitCopy {               // kCopyBytes apart
+  uint64_t logit[kLayerMaxE];    // (1 << 32) | f32 bits of logit e, 0 when empty
   uint32_t readers_done;
 };
-constexpr size_t kCopyBytes = 640;
+constexpr size_t kCopyBytes = 1088;
 static_assert(sizeof(LogitCopy) <= kCopyBytes, "copy layout");
 
 struct LayerMailbox {    // one per down block, 64 bytes apart
@@ -137,19 +139,26 @@ __device__ __forceinline__ float router_logit(const uint16_t *rw, const float *r
 }
 
 // Wavefront 0 of a block: wait for the E tagged logits in copy `cp`, run the top-k. Returns
-// false when the wait ran out. lane e's logit in *l.
+// false when the wait ran out. Logit 64 q + lane in l[q].
 __device__ __forceinline__ bool await_routing(LogitCopy *cp, const TopkCfg &c, uint32_t spin_limit,
-                                              int lane, float *l, int *s_order, float *s_w, int *s_sel) {
+                                              int lane, float (&l)[2], int *s_order, float *s_w, int *s_sel) {
   const int E = c.E;
-  uint64_t v = 0;
+  uint64_t v0 = 0, v1 = 0;
   for (uint32_t n = 0;; n++) {
-    v = lane < E ? ld_agent64(&cp->logit[lane]) : (1ull << 32);
-    if (__all((v >> 32) == 1ull)) break;
+    v0 = lane < E ? ld_agent64(&cp->logit[lane]) : (1ull << 32);
+    v1 = lane + 64 < E ? ld_agent64(&cp->logit[lane + 64]) : (1ull << 32);
+    if (__all((v0 >> 32) == 1ull && (v1 >> 32) == 1ull)) break;
     if (n >= spin_limit) return false;
     __builtin_amdgcn_s_sleep(1);
   }
-  *l = __uint_as_float((uint32_t)v);
-  wave_topk64(c, *l, lane, s_order, s_w, s_sel);
+  l[0] = __uint_as_float((uint32_t)v0);
+  l[1] = __uint_as_float((uint32_t)v1);
+  if (E <= 64) {
+    const float l1[1] = {l[0]};
+    wave_topk<1>(c, l1, lane, s_order, s_w, s_sel);
+  } else {
+    wave_topk<2>(c, l, lane, s_order, s_w, s_sel);
+  }
   return true;
 }
 
@@ -162,6 +171,7 @@ __device__ __forceinline__ void release_copy(LogitCopy *cp, int readers, int E, 
   old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
   if (old == (uint32_t)readers - 1) {
     if (lane < E) st_agent64(&cp->logit[lane], 0ull);
+    if (lane + 64 < E) st_agent64(&cp->logit[lane + 64], 0ull);
     if (lane == 0) st_agent(&cp->readers_done, 0u);
   }
 }
@@ -235,12 +245,13 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     MOE_TRACE(1);
     // 2. routing
     if (wv == 0) {
-      float l;
-      const bool ok = await_routing(cp, tc, la.spin_limit, lane, &l, s_order, s_w, &s_sel);
+      float l[2];
+      const bool ok = await_routing(cp, tc, la.spin_limit, lane, l, s_order, s_w, &s_sel);
       release_copy(cp, readers, E, lane);
       if (lane == 0) s_flag = !ok;
       if (b == 0 && ok) {
-        if (lane < E) a.logits[lane] = l;
+        if (lane < E) a.logits[lane] = l[0];
+        if (lane + 64 < E) a.logits[lane + 64] = l[1];
         if (lane < K) {
           a.idx[lane] = s_order[lane];
           a.wts[lane] = s_w[lane];
@@ -322,8 +333,8 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   uint8_t *s_h = reinterpret_cast<uint8_t *>(smem);  // [slot] activation records of h
   // 1. routing
   if (wv == 0) {
-    float l;
-    const bool ok = await_routing(cp, tc, la.spin_limit, lane, &l, s_order, s_w, &s_sel);
+    float l[2];
+    const bool ok = await_routing(cp, tc, la.spin_limit, lane, l, s_order, s_w, &s_sel);
     release_copy(cp, readers, E, lane);
     if (lane == 0) s_flag = !ok || err0;
   }
@@ -411,7 +422,7 @@ size_t layer_hterm_bytes() { return (size_t)4 * Act::kBytes + 1024; }
 
 bool decode_layer_supported(const LayerArgs &la) {
   const DecodeArgs &a = la.d;
-  return a.k >= 1 && a.k <= 4 && a.E >= 1 && a.E <= 64 && a.k <= a.E && a.rnq >= 1 && a.rnq <= 6 &&
+  return a.k >= 1 && a.k <= 4 && a.E >= 1 && a.E <= kLayerMaxE && a.k <= a.E && a.rnq >= 1 && a.rnq <= 6 &&
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          a.gu.ns <= (uint32_t)kLayerNs && a.dn.ns <= (uint32_t)kLayerNs && a.H % 32 == 0 &&
          a.I % 32 == 0 && a.gu.tiles % 4 == 0 &&

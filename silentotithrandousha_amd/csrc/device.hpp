@@ -351,31 +351,58 @@ __device__ __forceinline__ void block_topk(const TopkCfg &c, const float *s_logi
   __syncthreads();
 }
 
-// block_topk for E <= 64 with the same arithmetic, done by one wavefront with logit e in lane e
-// (lanes >= E ignored): the kept probabilities are gathered in slot order into uniform
-// registers (ballot + readlane), so the adaptive count and the renormalisation need no pass
-// through LDS. Writes s_order / s_w / *s_sel; the caller synchronises.
-__device__ __forceinline__ void wave_topk64(const TopkCfg &c, float l, int lane, int *s_order,
-                                            float *s_w, int *s_sel) {
+// block_topk with the same arithmetic, done by one wavefront for E <= 64 Q: logit e = 64 q + lane
+// in l[q] (entries past E ignored). The kept probabilities are gathered in slot order into
+// uniform registers (ballot + readlane), so the adaptive count and the renormalisation need no
+// pass through LDS. Writes s_order / s_w / *s_sel; the caller synchronises.
+template <int Q>
+__device__ __forceinline__ void wave_topk(const TopkCfg &c, const float (&l)[Q], int lane, int *s_order,
+                                          float *s_w, int *s_sel) {
   const int E = c.E;
-  const bool valid = lane < E;
-  const uint32_t key = rank_key(l);
-  const float m = wave_max(valid ? l : -INFINITY);
-  const float p = valid ? expf(l - m) : 0.0f;
-  const float sum = wave_sum_xor(p);
-  const float pn = sum > 0.0f ? p / sum : p;
-  int rank = 0;
-  for (int f = 0; f < E; f++) {
-    const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)key, f);
-    rank += (kf > key || (kf == key && f < lane)) ? 1 : 0;
+  bool valid[Q];
+  uint32_t key[Q];
+  float m = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    valid[q] = 64 * q + lane < E;
+    key[q] = rank_key(l[q]);
+    if (valid[q]) m = fmaxf(m, l[q]);
+  }
+  m = wave_max(m);
+  float p[Q], ls = 0.0f;
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    p[q] = valid[q] ? expf(l[q] - m) : 0.0f;
+    ls = ls + p[q];
+  }
+  const float sum = wave_sum_xor(ls);
+  float pn[Q];
+  int rank[Q];
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    pn[q] = sum > 0.0f ? p[q] / sum : p[q];
+    rank[q] = 0;
+  }
+#pragma unroll
+  for (int qf = 0; qf < Q; qf++) {
+    const int nf = min(64, E - 64 * qf);
+    for (int fl = 0; fl < nf; fl++) {
+      const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)key[qf], fl);
+      const int f = 64 * qf + fl;
+#pragma unroll
+      for (int q = 0; q < Q; q++) rank[q] += (kf > key[q] || (kf == key[q] && f < 64 * q + lane)) ? 1 : 0;
+    }
   }
   const int kk = c.k < E ? c.k : E;
   float ps[4];
 #pragma unroll
   for (int s = 0; s < 4; s++) {  // slots 0..3 (the single-token kernels keep k <= 4)
-    const uint64_t mask = __ballot(valid && rank == s);
-    const int src = mask ? __builtin_ctzll(mask) : 0;
-    ps[s] = mask ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pn), src)) : 0.0f;
+    ps[s] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+      const uint64_t mask = __ballot(valid[q] && rank[q] == s);
+      if (mask) ps[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pn[q]), __builtin_ctzll(mask)));
+    }
   }
   int sel = kk;
   if (c.adaptive && kk > 1) {
@@ -393,15 +420,24 @@ __device__ __forceinline__ void wave_topk64(const TopkCfg &c, float l, int lane,
   for (int s = 0; s < 4; s++)
     if (s < sel) top_sum = top_sum + ps[s];
   const bool ok = isfinite(top_sum) && top_sum > 0.0f;
-  if (valid && rank < sel) {
-    s_order[rank] = lane;
-    s_w[rank] = ok ? canon_nan(pn / top_sum) : 1.0f / (float)sel;
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    if (valid[q] && rank[q] < sel) {
+      s_order[rank[q]] = 64 * q + lane;
+      s_w[rank[q]] = ok ? canon_nan(pn[q] / top_sum) : 1.0f / (float)sel;
+    }
   }
   if (lane >= sel && lane < c.k) {
     s_order[lane] = -1;
     s_w[lane] = 0.0f;
   }
   if (lane == 0) *s_sel = sel;
+}
+
+__device__ __forceinline__ void wave_topk64(const TopkCfg &c, float l, int lane, int *s_order,
+                                            float *s_w, int *s_sel) {
+  const float lq[1] = {l};
+  wave_topk<1>(c, lq, lane, s_order, s_w, s_sel);
 }
 
 __device__ __forceinline__ void block_topk64(const TopkCfg &c, const float *s_logit, int *s_order,

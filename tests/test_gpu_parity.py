@@ -317,10 +317,11 @@ def test_fused_decode_repeated_calls_and_graph_replay(orc, disp20, layer20, mode
 
 
 @pytest.mark.parametrize("mode", [2, 1])
-@pytest.mark.parametrize("shape", [(64, 32, 32, 4), (64, 32, 8, 1), (320, 96, 64, 3), (1024, 512, 16, 2)])
+@pytest.mark.parametrize("shape", [(64, 32, 32, 4), (64, 32, 8, 1), (320, 96, 64, 3), (1024, 512, 16, 2),
+                                   (64, 32, 128, 4), (320, 96, 100, 3), (128, 64, 65, 2)])
 def test_fused_decode_small_shapes(orc, mode, shape):
     """Small and ragged single-token shapes (one gate_up block per slot, few down blocks, k < 4,
-    64 experts, router chains of 1..2 loads per lane) on both fused paths."""
+    64 to 128 experts, router chains of 1..2 loads per lane) on both fused paths."""
     H, I, E, k = shape
     L = syn.make_layer(H, I, E, seed=310 + H + E, scale_lo=120, scale_hi=124)
     d = GpuMoeDispatcher(H, I, 7.0)
@@ -382,7 +383,7 @@ def test_adaptive_topk_fused_and_unfused(orc):
 
 
 def test_120b_layer_decode(orc):
-    """GPT-OSS-120B shape (128 experts, top-4) at batch 1 and 8."""
+    """GPT-OSS-120B shape (128 experts, top-4) at batch 1 (every single-token path) and 8."""
     E = 128
     L = syn.make_layer(H20, I20, E, seed=330)
     d = GpuMoeDispatcher(H20, I20, 7.0)
@@ -392,7 +393,36 @@ def test_120b_layer_decode(orc):
         want, _, idx, _ = orc.moe_layer(x, L, 4)
         gidx, _ = d.router_topk(0, x, 4)
         assert np.array_equal(gidx, idx)
-        assert_rel_l2(d.layer_forward(0, x, 4), want, f"120B T={T}")
+        for mode in (MODES if T == 1 else [2]):
+            d.set_fused_decode(mode)
+            assert_rel_l2(d.layer_forward(0, x, 4), want, f"120B T={T} mode {mode}")
+    d.close()
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_single_token_ties_and_nan_across_halves(orc, mode):
+    """128 experts: tied logits on both sides of expert 64 keep the lower index first, a NaN
+    logit in the upper half ranks last; k = 3 drops the last of the tied experts, so picking
+    the wrong one changes the output."""
+    H, I, E = 64, 32, 128
+    L = syn.make_layer(H, I, E, seed=350, scale_lo=120, scale_hi=124, router=False)
+    w = np.zeros((E, H), np.float32)
+    w[:, 0] = -0.5
+    w[[3, 67, 100], 0] = 1.0
+    w[120, 0] = 1.5
+    wb = syn.bf16_bits(w)
+    wb[90, 1] = 0x7FC0  # NaN logit for expert 90
+    L["router_w"], L["router_b"] = wb, np.zeros(E, np.float32)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    d.set_fused_decode(mode)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = 2.0
+    x[0, 1] = 1.0
+    for k in (3, 4):
+        want, _, idx, _ = orc.moe_layer(x, L, k)
+        assert list(idx[0]) == [120, 3, 67, 100][:k]
+        assert_rel_l2(d.layer_forward(0, x, k), want, f"ties k={k} mode {mode}")
     d.close()
 
 
