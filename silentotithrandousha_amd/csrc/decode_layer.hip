@@ -138,11 +138,9 @@ __device__ __forceinline__ float router_logit(const uint16_t *rw, const float *r
   return canon_nan(wave_sum_xor(p) + rb[e]);
 }
 
-// Wavefront 0 of a block: wait for the E tagged logits in copy `cp`, run the top-k. Returns
-// false when the wait ran out. Logit 64 q + lane in l[q].
-__device__ __forceinline__ bool await_routing(LogitCopy *cp, const TopkCfg &c, uint32_t spin_limit,
-                                              int lane, float (&l)[2], int *s_order, float *s_w, int *s_sel) {
-  const int E = c.E;
+// Wavefront 0 of a block: wait for the E tagged logits in copy `cp`; logit 64 q + lane in l[q].
+// Returns false when the wait ran out.
+__device__ __forceinline__ bool await_logits(LogitCopy *cp, int E, uint32_t spin_limit, int lane, float (&l)[2]) {
   uint64_t v0 = 0, v1 = 0;
   for (uint32_t n = 0;; n++) {
     v0 = lane < E ? ld_agent64(&cp->logit[lane]) : (1ull << 32);
@@ -153,21 +151,55 @@ __device__ __forceinline__ bool await_routing(LogitCopy *cp, const TopkCfg &c, u
   }
   l[0] = __uint_as_float((uint32_t)v0);
   l[1] = __uint_as_float((uint32_t)v1);
-  if (E <= 64) {
-    const float l1[1] = {l[0]};
-    wave_topk<1>(c, l1, lane, s_order, s_w, s_sel);
-  } else {
-    wave_topk<2>(c, l, lane, s_order, s_w, s_sel);
-  }
   return true;
 }
 
+// The routing on the critical path: the winners -> s_order, and the kept count -> *s_sel. With
+// adaptive k the count depends on the probabilities, so the whole top-k runs here; otherwise
+// the kept count is min(k, E) and the weights follow later (route_weights), overlapping the
+// weight loads.
+__device__ __forceinline__ void route_order(const TopkCfg &c, const float (&l)[2], int lane, int (&ord)[4],
+                                            int *s_order, float *s_w, int *s_sel) {
+  if (c.E <= 64) {
+    const float l1[1] = {l[0]};
+    wave_topk_order<1>(c, l1, lane, ord);
+    if (c.adaptive) wave_topk_weights<1>(c, l1, lane, ord, true, s_order, s_w, s_sel);
+  } else {
+    wave_topk_order<2>(c, l, lane, ord);
+    if (c.adaptive) wave_topk_weights<2>(c, l, lane, ord, true, s_order, s_w, s_sel);
+  }
+  if (!c.adaptive) {
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+      if (lane == s && s < c.k) s_order[s] = ord[s];
+    if (lane == 0) *s_sel = c.k < c.E ? c.k : c.E;
+  }
+}
+
+// The slot weights -> s_w, when route_order left them for later.
+__device__ __forceinline__ void route_weights(const TopkCfg &c, const float (&l)[2], int lane, const int (&ord)[4],
+                                              int *s_order, float *s_w, int *s_sel) {
+  if (c.adaptive) return;
+  if (c.E <= 64) {
+    const float l1[1] = {l[0]};
+    wave_topk_weights<1>(c, l1, lane, ord, false, s_order, s_w, s_sel);
+  } else {
+    wave_topk_weights<2>(c, l, lane, ord, false, s_order, s_w, s_sel);
+  }
+}
+
 // Wavefront 0, after its routing read: count this block as a reader of copy `cp`; the last of
-// its `readers` clears it for the next launch.
-__device__ __forceinline__ void release_copy(LogitCopy *cp, int readers, int E, int lane) {
+// its `readers` clears it for the next launch. Two halves, so that the atomic's round trip
+// overlaps the weight loads issued between them: release_begin returns the count before ours
+// (lane 0), release_end acts on it.
+__device__ __forceinline__ uint32_t release_begin(LogitCopy *cp, int lane) {
   uint32_t old = 0;
   if (lane == 0)
     old = __hip_atomic_fetch_add(&cp->readers_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return old;
+}
+
+__device__ __forceinline__ void release_end(LogitCopy *cp, uint32_t old, int readers, int E, int lane) {
   old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
   if (old == (uint32_t)readers - 1) {
     if (lane < E) st_agent64(&cp->logit[lane], 0ull);
@@ -244,19 +276,14 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
     MOE_TRACE(1);
     // 2. routing
+    uint32_t rel = 0;
+    float l[2];
+    int ord[4];
     if (wv == 0) {
-      float l[2];
-      const bool ok = await_routing(cp, tc, la.spin_limit, lane, l, s_order, s_w, &s_sel);
-      release_copy(cp, readers, E, lane);
+      const bool ok = await_logits(cp, E, la.spin_limit, lane, l);
+      if (ok) route_order(tc, l, lane, ord, s_order, s_w, &s_sel);
+      rel = release_begin(cp, lane);
       if (lane == 0) s_flag = !ok;
-      if (b == 0 && ok) {
-        if (lane < E) a.logits[lane] = l[0];
-        if (lane + 64 < E) a.logits[lane + 64] = l[1];
-        if (lane < K) {
-          a.idx[lane] = s_order[lane];
-          a.wts[lane] = s_w[lane];
-        }
-      }
     }
     __syncthreads();
     MOE_TRACE(2);
@@ -265,6 +292,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     const int slot = b / NGS;
     if (timeout || err0 || slot >= sel) {  // uniform over the block; no barrier follows
       if (timeout && tid == 0) st_agent(&hdr->err, 1u);
+      if (wv == 0) release_end(cp, rel, readers, E, lane);
       return;
     }
     // 3. this wavefront's gate_up tile (rows 16t .. 16t+15 -> h[8t, 8t+8)); bias with it
@@ -274,11 +302,21 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     TileRegs<kLayerNs> r;
     tile_load<kLayerNs>(r, rec + a.gu_off, a.gu, t, true, lane);
     const float4 bias = reinterpret_cast<const float4 *>(rec + a.gub_off)[t * 4 + g];
+    if (b == 0 && wv == 0) {  // block 0 reports the routing (the weights overlap its tile loads)
+      route_weights(tc, l, lane, ord, s_order, s_w, &s_sel);
+      if (lane < E) a.logits[lane] = l[0];
+      if (lane + 64 < E) a.logits[lane + 64] = l[1];
+      if (lane < K) {
+        a.idx[lane] = s_order[lane];
+        a.wts[lane] = s_w[lane];
+      }
+    }
     uint32_t bsw[kLayerNq];
     load_bsw<kLayerNs>(s_x, bsw, lane);
     const f32x4 acc = tile_mfma_f8<kLayerNs>(r, s_x, bsw, lane);
     float v[4];
     sum_terms(acc, v);
+    if (wv == 0) release_end(cp, rel, readers, E, lane);
     MOE_TRACE(3);
     if (j == 0) {
       s_h32[wv * 8 + 2 * g] = swiglu(v[0] + bias.x, v[1] + bias.y, a.limit);
@@ -332,10 +370,13 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   LayerMailbox *my = mailbox(la.sync, t);
   uint8_t *s_h = reinterpret_cast<uint8_t *>(smem);  // [slot] activation records of h
   // 1. routing
+  uint32_t rel = 0;
+  float l[2];
+  int ord[4];
   if (wv == 0) {
-    float l[2];
-    const bool ok = await_routing(cp, tc, la.spin_limit, lane, l, s_order, s_w, &s_sel);
-    release_copy(cp, readers, E, lane);
+    const bool ok = await_logits(cp, E, la.spin_limit, lane, l);
+    if (ok) route_order(tc, l, lane, ord, s_order, s_w, &s_sel);
+    rel = release_begin(cp, lane);
     if (lane == 0) s_flag = !ok || err0;
   }
   __syncthreads();
@@ -348,6 +389,10 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   TileRegs<kLayerNs> r;
   tile_load<kLayerNs>(r, rec + a.dn_off, a.dn, ok ? t : 0, ok, lane);
   const float4 bias = reinterpret_cast<const float4 *>(rec + a.dnb_off)[(ok ? t : 0) * 4 + g];
+  if (wv == 0) {
+    release_end(cp, rel, readers, E, lane);
+    if (!timeout) route_weights(tc, l, lane, ord, s_order, s_w, &s_sel);  // read after the h wait's barrier
+  }
   // 3. wait for h of the kept slots
   if (tid == 0 && !timeout) {
     for (int s = 0; s < sel && !timeout; s++) {

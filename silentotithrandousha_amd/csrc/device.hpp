@@ -351,57 +351,110 @@ __device__ __forceinline__ void block_topk(const TopkCfg &c, const float *s_logi
   __syncthreads();
 }
 
-// block_topk with the same arithmetic, done by one wavefront for E <= 64 Q: logit e = 64 q + lane
-// in l[q] (entries past E ignored). The kept probabilities are gathered in slot order into
-// uniform registers (ballot + readlane), so the adaptive count and the renormalisation need no
-// pass through LDS. Writes s_order / s_w / *s_sel; the caller synchronises.
+// Maximum over the wavefront: DPP within each row of 16 lanes (quad permutes, half-row and row
+// mirrors: after the quad steps a quad is uniform, so the mirrors pair it with the other quad /
+// half), then the four row results through v_readlane. Exact for any combining order.
+__device__ __forceinline__ uint32_t row_max_dpp(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = row_max_dpp(v);
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+__device__ __forceinline__ float wave_fmax_dpp(float m) {
+  const int i = __float_as_int(m);
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false)));
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x140, 0xF, 0xF, false)));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// block_topk's result for k <= 4, computed by one wavefront with logit e = 64 q + lane in l[q]
+// (entries past E ignored), in two parts so that a caller can act on the winners before the
+// probabilities exist. wave_topk_order: the winners by k rounds of a wave arg-max over rank_key
+// (ties: the lowest index, i.e. the lowest q with a candidate, then the lowest lane), which is
+// ranks_before's order; ord[s] (uniform) for s < min(k, E), -1 after.
 template <int Q>
-__device__ __forceinline__ void wave_topk(const TopkCfg &c, const float (&l)[Q], int lane, int *s_order,
-                                          float *s_w, int *s_sel) {
+__device__ __forceinline__ void wave_topk_order(const TopkCfg &c, const float (&l)[Q], int lane, int (&ord)[4]) {
   const int E = c.E;
-  bool valid[Q];
+  bool avail[Q];
   uint32_t key[Q];
-  float m = -INFINITY;
 #pragma unroll
   for (int q = 0; q < Q; q++) {
-    valid[q] = 64 * q + lane < E;
+    avail[q] = 64 * q + lane < E;
     key[q] = rank_key(l[q]);
-    if (valid[q]) m = fmaxf(m, l[q]);
   }
-  m = wave_max(m);
+  const int kk = c.k < E ? c.k : E;
+#pragma unroll
+  for (int s = 0; s < 4; s++) {  // the single-token kernels keep k <= 4
+    ord[s] = -1;
+    if (s < kk) {
+      uint32_t best = 0;
+#pragma unroll
+      for (int q = 0; q < Q; q++)
+        if (avail[q]) best = max(best, key[q]);
+      best = wave_max_u32(best);
+      int win = -1;
+#pragma unroll
+      for (int q = 0; q < Q; q++) {
+        const uint64_t mask = __ballot(avail[q] && key[q] == best);
+        if (win < 0 && mask) win = 64 * q + __builtin_ctzll(mask);
+      }
+#pragma unroll
+      for (int q = 0; q < Q; q++)
+        if (64 * q + lane == win) avail[q] = false;
+      ord[s] = win;
+    }
+  }
+}
+
+// wave_topk_weights: the same softmax as block_topk (max, exp, the same xor-butterfly sum,
+// divide), the probabilities of the winners ord, the adaptive count and the renormalisation.
+// Writes s_w (lanes s < k), *s_sel (lane 0) and, if write_order, s_order.
+template <int Q>
+__device__ __forceinline__ void wave_topk_weights(const TopkCfg &c, const float (&l)[Q], int lane,
+                                                  const int (&ord)[4], bool write_order, int *s_order,
+                                                  float *s_w, int *s_sel) {
+  const int E = c.E;
+  float m = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < Q; q++)
+    if (64 * q + lane < E) m = fmaxf(m, l[q]);
+  m = wave_fmax_dpp(m);
   float p[Q], ls = 0.0f;
 #pragma unroll
   for (int q = 0; q < Q; q++) {
-    p[q] = valid[q] ? expf(l[q] - m) : 0.0f;
+    p[q] = 64 * q + lane < E ? expf(l[q] - m) : 0.0f;
     ls = ls + p[q];
   }
   const float sum = wave_sum_xor(ls);
   float pn[Q];
-  int rank[Q];
 #pragma unroll
-  for (int q = 0; q < Q; q++) {
-    pn[q] = sum > 0.0f ? p[q] / sum : p[q];
-    rank[q] = 0;
-  }
-#pragma unroll
-  for (int qf = 0; qf < Q; qf++) {
-    const int nf = min(64, E - 64 * qf);
-    for (int fl = 0; fl < nf; fl++) {
-      const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)key[qf], fl);
-      const int f = 64 * qf + fl;
-#pragma unroll
-      for (int q = 0; q < Q; q++) rank[q] += (kf > key[q] || (kf == key[q] && f < 64 * q + lane)) ? 1 : 0;
-    }
-  }
+  for (int q = 0; q < Q; q++) pn[q] = sum > 0.0f ? p[q] / sum : p[q];
   const int kk = c.k < E ? c.k : E;
   float ps[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) {  // slots 0..3 (the single-token kernels keep k <= 4)
+  for (int s = 0; s < 4; s++) {
     ps[s] = 0.0f;
+    if (s < kk) {
 #pragma unroll
-    for (int q = 0; q < Q; q++) {
-      const uint64_t mask = __ballot(valid[q] && rank[q] == s);
-      if (mask) ps[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pn[q]), __builtin_ctzll(mask)));
+      for (int q = 0; q < Q; q++)
+        if ((ord[s] >> 6) == q) ps[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pn[q]), ord[s] & 63));
     }
   }
   int sel = kk;
@@ -421,30 +474,13 @@ __device__ __forceinline__ void wave_topk(const TopkCfg &c, const float (&l)[Q],
     if (s < sel) top_sum = top_sum + ps[s];
   const bool ok = isfinite(top_sum) && top_sum > 0.0f;
 #pragma unroll
-  for (int q = 0; q < Q; q++) {
-    if (valid[q] && rank[q] < sel) {
-      s_order[rank[q]] = 64 * q + lane;
-      s_w[rank[q]] = ok ? canon_nan(pn[q] / top_sum) : 1.0f / (float)sel;
+  for (int s = 0; s < 4; s++) {
+    if (lane == s && s < c.k) {
+      if (write_order) s_order[s] = s < sel ? ord[s] : -1;
+      s_w[s] = s < sel ? (ok ? canon_nan(ps[s] / top_sum) : 1.0f / (float)sel) : 0.0f;
     }
   }
-  if (lane >= sel && lane < c.k) {
-    s_order[lane] = -1;
-    s_w[lane] = 0.0f;
-  }
   if (lane == 0) *s_sel = sel;
-}
-
-__device__ __forceinline__ void wave_topk64(const TopkCfg &c, float l, int lane, int *s_order,
-                                            float *s_w, int *s_sel) {
-  const float lq[1] = {l};
-  wave_topk<1>(c, lq, lane, s_order, s_w, s_sel);
-}
-
-__device__ __forceinline__ void block_topk64(const TopkCfg &c, const float *s_logit, int *s_order,
-                                             float *s_w, int *s_sel) {
-  if (threadIdx.x < 64)
-    wave_topk64(c, s_logit[min((int)threadIdx.x, c.E - 1)], (int)threadIdx.x, s_order, s_w, s_sel);
-  __syncthreads();
 }
 
 // ------------------------------------------------------------------ fp8 activation terms
