@@ -77,9 +77,11 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * moe_layer_forward return MOE_ERR_HIP (which clears the condition).
  * MOE_OPT_BATCH_GEMM: batches (n_tokens > 1) run through the grouped GEMM on the block-scaled
  * MFMA (activations as fp8 terms, exact to 2^-12) when 1 (default) and experts average at
- * least 32 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
- * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical. */
-enum moe_option { MOE_OPT_FUSED_DECODE = 1, MOE_OPT_SPIN_LIMIT = 2, MOE_OPT_BATCH_GEMM = 3 };
+ * least 4 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
+ * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical.
+ * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM for experts averaging 48+ entries: 0
+ * (default) 8 wavefronts x 64 rows, 1 4 wavefronts x 128 rows (tuning; results identical). */
+enum moe_option { MOE_OPT_FUSED_DECODE = 1, MOE_OPT_SPIN_LIMIT = 2, MOE_OPT_BATCH_GEMM = 3, MOE_OPT_GEMM_SHAPE = 4 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 
 /* ------------------------------------------------------------------ weights */

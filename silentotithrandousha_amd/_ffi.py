@@ -20,6 +20,7 @@ MOE_ERR_OOM = 5
 MOE_OPT_FUSED_DECODE = 1
 MOE_OPT_SPIN_LIMIT = 2
 MOE_OPT_BATCH_GEMM = 3
+MOE_OPT_GEMM_SHAPE = 4
 
 _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p

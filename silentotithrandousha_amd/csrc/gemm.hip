@@ -5,11 +5,12 @@
 // expert's entries as kTerms fp8 terms (split8_fp8), f32 accumulation.
 //
 //   k_split_rows   f32 rows (x) -> step-major activation records
-//   k_gemm_fp8     one block = 512 weight rows x 64 entries of one expert; each wavefront owns
-//                  128 rows (8 tiles of 16) x the 64 entries (4 column groups) x kGemmTerms
-//                  activation terms.
-//                  Per K-step of 128: the B records of the 64 entries go through registers
-//                  into a double-buffered LDS area; A tiles load straight into registers.
+//   k_gemm_fp8     one block = 64 RT weight rows x 16 CG entries of one expert; each wavefront
+//                  owns 16 RT rows (RT tiles of 16) x all the block's entries (CG column
+//                  groups) x kGemmTerms activation terms.
+//                  K-steps of 128 run through a ring of 3: the B records of the entries go
+//                  straight into LDS by LDS-DMA (global_load_lds), A tiles into registers, two
+//                  steps ahead of the MFMAs.
 //                  GATE_UP epilogue: bias, SwiGLU (gate = row 2i, up = row 2i+1) and the split
 //                  of the wavefront's 32 h values per entry into the h records; DOWN epilogue:
 //                  bias and +-65504 clamp into f32 [entry][H].
@@ -81,227 +82,309 @@ hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *r
 
 // ------------------------------------------------------------------ grouped GEMM
 
-constexpr int kGemmThreads = 256;
-constexpr int kGemmRT = 8;                       // 16-row tiles per wavefront
-constexpr int kGemmRowsPerWave = 16 * kGemmRT;
-constexpr int kGemmRows = 4 * kGemmRowsPerWave;  // weight rows per block
-constexpr int kGemmCols = 64;                    // entries per block
 // The batch path multiplies by the first kGemmTerms terms of the records (3 of 4: the
 // activation is then exact to 2^-12 of each value, well inside the 1e-3 tolerance; the fourth
 // term would add a third more MFMA work and LDS traffic for precision no caller needs).
 constexpr int kGemmTerms = 3;
 constexpr int kEntryStep = kGemmTerms * 128 + 16;   // LDS bytes of one entry's K-step
-constexpr int kBufBytes = kGemmCols * kEntryStep;   // one K-step of B for 64 entries
 static_assert(G::kStep == kTerms * 128 + 16, "a K-step of a record = term data + 16 scale bytes");
 static_assert(kEntryStep % 64 == 16, "entry stride: 16-byte aligned, spreads over the LDS banks");
 constexpr int kChunks = kEntryStep / 16;            // 16-byte chunks per entry K-step (25)
-constexpr int kChunksPerThread = (kChunks + 3) / 4;  // 4 threads per entry
 
-// MFMAs of one K-step for a wavefront: 4 row tiles x 4 column groups x kTerms terms; OP = the
-// step's A-scale byte (s % 4).
-template <int OP>
-__device__ __forceinline__ void gemm_step(f32x4 (&acc)[kGemmRT][4], const uint4 (&ar)[kGemmRT],
-                                          const uint32_t (&sw)[kGemmRT], const uint8_t *cur, int j, int g) {
+// s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
+// outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima).
+constexpr int vm_wait(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+// The same with lgkmcnt 0: also this wavefront's LDS operations complete.
+constexpr int vm_lgkm_wait(int n) { return vm_wait(n) & ~0x0F00; }
+
+// Block shape: W wavefronts x RT tiles of 16 weight rows each, x CG column groups of 16
+// entries shared by the W wavefronts. Every operand goes through LDS by LDS-DMA
+// (global_load_lds) into a ring of D K-steps: per step, the B records of the entries (kDma
+// 1 KB pieces per wavefront), and per wavefront its RT A chunks (1 KB each) and RT A-scale words
+// (256 B each).
+template <int RT, int CG, int W, int D>
+struct GemmShape {
+  static constexpr int kThreads = 64 * W;
+  static constexpr int kRows = 16 * RT * W;                  // weight rows per block
+  static constexpr int kCols = 16 * CG;                      // entries per block
+  static constexpr int kStepChunks = kCols * kChunks;        // 16-byte chunks of one K-step of B
+  static constexpr int kGroups = (kStepChunks + 63) / 64;    // 1 KB pieces holding them
+  static constexpr int kDma = (kGroups + W - 1) / W;         // B pieces per wavefront per step
+  static constexpr int kBufB = kGroups * 1024;               // LDS bytes of one step of B
+  static constexpr int kBufA = W * RT * 1024;                // A chunks of one step
+  static constexpr int kBufS = W * RT * 256;                 // A-scale words of one step
+  static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
+  static constexpr int kLds = D * kSlot + 1024;              // + 1 KB for the pieces past kGroups
+  static constexpr int kIssue = kDma + 2 * RT;               // VMEM operations per wavefront per step
+};
+
+// B operands of one column group for the wavefront's lanes (entry j, lane group g): per term the
+// 32 bytes of the MFMA B layout and the E8M0 scale of the lane's block.
+struct GemmB {
+  i32x8 v[kGemmTerms];
+  uint32_t sc[kGemmTerms];
+};
+
+__device__ __forceinline__ void gemm_read_b(GemmB &b, const uint8_t *eb, int g) {
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    __builtin_amdgcn_sched_barrier(0);  // one column group's B operands live at a time
-    const uint8_t *eb = cur + (16 * c + j) * kEntryStep;
-#pragma unroll
-    for (int t = 0; t < kGemmTerms; t++) {
-      const uint4 b0 = *reinterpret_cast<const uint4 *>(eb + t * 128 + 32 * (g >> 1) + 16 * (g & 1));
-      const uint4 b1 = *reinterpret_cast<const uint4 *>(eb + t * 128 + 64 + 32 * (g >> 1) + 16 * (g & 1));
-      const uint32_t bs = *reinterpret_cast<const uint32_t *>(eb + kGemmTerms * 128 + 4 * t) >> (8 * g);
-      const i32x8 B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-#pragma unroll
-      for (int r = 0; r < kGemmRT; r++) {
-        const i32x8 A = {(int)ar[r].x, (int)ar[r].y, (int)ar[r].z, (int)ar[r].w, 0, 0, 0, 0};
-        acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[r][c], 4, 0, OP, (int)sw[r], 0, (int)bs);
-      }
-    }
+  for (int t = 0; t < kGemmTerms; t++) {
+    const uint4 b0 = *reinterpret_cast<const uint4 *>(eb + t * 128 + 32 * (g >> 1) + 16 * (g & 1));
+    const uint4 b1 = *reinterpret_cast<const uint4 *>(eb + t * 128 + 64 + 32 * (g >> 1) + 16 * (g & 1));
+    b.v[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    b.sc[t] = *reinterpret_cast<const uint32_t *>(eb + kGemmTerms * 128 + 4 * t) >> (8 * g);
   }
 }
 
-template <int MODE>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_fp8(GemmArgs a) {
-  extern __shared__ uint4 smem[];
+// MFMAs of one K-step for a wavefront: RT row tiles x CG column groups x kGemmTerms terms, all
+// operands from the step's ring slot; sh = 8 * (s % 4) selects the step's byte of the A-scale
+// words. The B operands of column group c + 1 are read while the MFMAs of group c run. Column
+// groups past the block's entries compute on repeated entries (not stored).
+template <int RT, int CG, int W, int D>
+__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CG], const uint8_t *slot, int wv, int lane, int sh) {
+  using S = GemmShape<RT, CG, W, D>;
+  const int j = lane & 15, g = lane >> 4;
+  const uint8_t *bb = slot + j * kEntryStep, *ab = slot + S::kBufB + wv * RT * 1024,
+                *sb = slot + S::kBufB + S::kBufA + wv * RT * 256;
+  uint4 ar[RT];
+  uint32_t sw[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    ar[r] = *reinterpret_cast<const uint4 *>(ab + r * 1024 + 16 * lane);
+    sw[r] = *reinterpret_cast<const uint32_t *>(sb + r * 256 + 4 * lane) >> sh;
+  }
+  GemmB bc, bn;
+  gemm_read_b(bc, bb, g);
+#pragma unroll
+  for (int c = 0; c < CG; c++) {
+    if (c + 1 < CG) gemm_read_b(bn, bb + 16 * (c + 1) * kEntryStep, g);
+    __builtin_amdgcn_sched_barrier(0);  // the next group's reads issue before this group's MFMAs
+#pragma unroll
+    for (int t = 0; t < kGemmTerms; t++) {
+#pragma unroll
+      for (int r = 0; r < RT; r++) {
+        const i32x8 A = {(int)ar[r].x, (int)ar[r].y, (int)ar[r].z, (int)ar[r].w, 0, 0, 0, 0};
+        acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, bc.v[t], acc[r][c], 4, 0, 0, (int)sw[r], 0,
+                                                                     (int)bc.sc[t]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < CG) bc = bn;
+  }
+}
+
+template <int MODE, int RT, int CG, int W, int D>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_gemm_fp8(GemmArgs a) {
+  using S = GemmShape<RT, CG, W, D>;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem_g[];
   __shared__ int s_tile[4];  // expert record index, first entry, entry count, row block
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
 
-  // ---- tile: global column tile cl (over the experts' 64-entry tiles) and row block, row
-  //      blocks fastest, so neighbouring blocks share the entries' activation records
-  if (tid == 0) {
-    int cl = (int)blockIdx.x / a.n_row_blocks;
-    const int rb = (int)blockIdx.x - cl * a.n_row_blocks;
+  // ---- tile: global column tile cl (over the experts' kCols-entry tiles) and row block, row
+  //      blocks fastest, so neighbouring blocks share the entries' activation records.
+  //      Wavefront 0 finds the expert of tile cl: lanes read 64 experts' entry ranges at once,
+  //      a prefix sum of their tile counts places cl.
+  if (wv == 0) {
+    const int cl = (int)blockIdx.x / a.n_row_blocks;
     const int na = min(*a.n_active, a.max_active);
-    int ex = -1, beg = 0, cnt = 0;
-    for (int ai = 0; ai < na; ai++) {
-      const int o0 = a.active_off[ai], o1 = a.active_off[ai + 1];
-      const int nct = (o1 - o0 + kGemmCols - 1) / kGemmCols;
-      if (cl < nct) {
-        ex = a.active_ids[ai];
-        beg = o0 + cl * kGemmCols;
-        cnt = min(kGemmCols, o1 - beg);
+    int ex = -1, beg = 0, cnt = 0, base = 0;
+    for (int q0 = 0; q0 < na; q0 += 64) {
+      const int ai = q0 + lane;
+      int o0 = 0, o1 = 0;
+      if (ai < na) {
+        o0 = a.active_off[ai];
+        o1 = a.active_off[ai + 1];
+      }
+      const int nct = (o1 - o0 + S::kCols - 1) / S::kCols;
+      int incl = nct;  // inclusive prefix sum over the lanes
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      const int start = base + incl - nct;
+      const uint64_t hit = __ballot(ai < na && cl >= start && cl < start + nct);
+      if (hit) {
+        const int hl = __builtin_ctzll(hit);
+        if (lane == hl) {
+          ex = a.active_ids[ai];
+          beg = o0 + (cl - start) * S::kCols;
+          cnt = min(S::kCols, o1 - beg);
+        }
+        ex = __shfl(ex, hl);
+        beg = __shfl(beg, hl);
+        cnt = __shfl(cnt, hl);
         break;
       }
-      cl -= nct;
+      base += __shfl(incl, 63);
     }
-    s_tile[0] = ex;
-    s_tile[1] = beg;
-    s_tile[2] = cnt;
-    s_tile[3] = rb;
+    if (lane == 0) {
+      s_tile[0] = ex;
+      s_tile[1] = beg;
+      s_tile[2] = cnt;
+      s_tile[3] = (int)blockIdx.x - cl * a.n_row_blocks;
+    }
   }
   __syncthreads();
   const int ex = s_tile[0], beg = s_tile[1], ncol = s_tile[2];
   if (ex < 0) return;
   const int rblk = s_tile[3];
-  const int t0 = (rblk * kGemmRows + wv * kGemmRowsPerWave) / 16;  // first 16-row tile of wave
+  const int t0 = (rblk * S::kRows + wv * 16 * RT) / 16;  // first 16-row tile of the wavefront
   const uint8_t *rec = a.base + (size_t)ex * a.stride;
   const uint8_t *mat = rec + a.mat_off;
   const PackDims d = a.d;
+  uint8_t *const trash = smem_g + D * S::kSlot;
 
-  // ---- B: thread (entry e = tid / 4, part p = tid % 4) moves 16-byte chunks p, p+4, ... of
-  //      the entry's K-step as it sits in LDS: the first kGemmTerms terms' bytes, then the 16
-  //      scale bytes; padding columns repeat a valid entry
-  uint8_t *const buf0 = reinterpret_cast<uint8_t *>(smem);
-  uint8_t *const buf1 = buf0 + kBufBytes;
-  const int be = tid >> 2, bp = tid & 3;
-  const uint8_t *bsrc;
-  {
-    const int ge = beg + min(be, ncol - 1);
+  // ---- sources. B: piece i of the wavefront = 1 KB piece 4 i + wv of the step, chunk c =
+  //      64 (4 i + wv) + lane (entry c / kChunks, part c % kChunks: the first kGemmTerms terms'
+  //      16-byte pieces, then the 16 scale bytes); padding entries repeat a valid entry; pieces
+  //      past kGroups go to the trash KB. A: chunk (step, lane) of each of the wavefront's RT
+  //      tiles; tiles past the matrix read the last tile (results not stored); a lane's K-block
+  //      past the matrix reads an in-range chunk, whose scale byte is 0 (the packer zero-fills
+  //      them) while the B records hold zeros there, so it adds exact zeros. Every lane of every
+  //      DMA runs, so each wavefront issues exactly kIssue VMEM operations per step, which the
+  //      vmcnt waits count on.
+  const uint8_t *bsrc[S::kDma];
+#pragma unroll
+  for (int i = 0; i < S::kDma; i++) {
+    const int c = min(64 * (W * i + wv) + lane, S::kStepChunks - 1);
+    const int e = c / kChunks, part = c % kChunks;
+    const int ge = beg + min(e, ncol - 1);
     const int row = a.entry_src ? a.entry_src[ge] : ge;
-    bsrc = a.brec + (size_t)row * G::kBytes;
+    bsrc[i] = a.brec + (size_t)row * G::kBytes + (part < kChunks - 1 ? 16 * part : kTerms * 128);
   }
-  uint4 bst[kChunksPerThread];
-  auto load_b = [&](int s) {
-    const uint8_t *p = bsrc + (size_t)s * G::kStep;
+  const uint8_t *asrc[RT];
+  const uint8_t *ssrc[RT];
+  bool tv[RT];
+  const size_t last_chunk = (size_t)d.rows * d.nb - 1;
 #pragma unroll
-    for (int k = 0; k < kChunksPerThread; k++) {
-      const int ch = bp + 4 * k;  // chunk of the LDS entry step; the last one is the scales
-      const int off = ch < kChunks - 1 ? 16 * ch : kTerms * 128;
-      if (ch < kChunks) bst[k] = *reinterpret_cast<const uint4 *>(p + off);
-    }
-  };
-  auto store_b = [&](uint8_t *bf) {
-    uint8_t *q = bf + be * kEntryStep;
-#pragma unroll
-    for (int k = 0; k < kChunksPerThread; k++) {
-      const int ch = bp + 4 * k;
-      if (ch < kChunks) *reinterpret_cast<uint4 *>(q + 16 * ch) = bst[k];
-    }
-  };
+  for (int r = 0; r < RT; r++) {
+    tv[r] = t0 + r < (int)d.tiles;
+    const int tl = min(t0 + r, (int)d.tiles - 1);
+    asrc[r] = mat + (size_t)tl * 16 * d.nb * 16;
+    ssrc[r] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
+  }
+  const uint8_t *alast = mat + last_chunk * 16;
+#define GEMM_LOAD(step)                                                                             \
+  do {                                                                                              \
+    uint8_t *sl = smem_g + ((step) % D) * S::kSlot;                                                 \
+    _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                           \
+      uint8_t *dst = W * i + wv < S::kGroups ? sl + 1024 * (W * i + wv) : trash;                    \
+      __builtin_amdgcn_global_load_lds(                                                             \
+          reinterpret_cast<const uint32_t *>(bsrc[i] + (size_t)(step) * G::kStep),                  \
+          (__attribute__((address_space(3))) void *)dst, 16, 0, 0);                                 \
+    }                                                                                               \
+    _Pragma("unroll") for (int r = 0; r < RT; r++) {                                                \
+      const uint8_t *src = asrc[r] + (size_t)(step) * 1024 + 16 * lane;                             \
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src < alast ? src : alast), \
+          (__attribute__((address_space(3))) void *)(sl + S::kBufB + (wv * RT + r) * 1024), 16, 0, 0); \
+    }                                                                                               \
+    _Pragma("unroll") for (int r = 0; r < RT; r++)                                                  \
+      __builtin_amdgcn_global_load_lds(                                                             \
+          reinterpret_cast<const uint32_t *>(ssrc[r] + (size_t)((step) >> 2) * 256),                \
+          (__attribute__((address_space(3))) void *)(sl + S::kBufB + S::kBufA + (wv * RT + r) * 256), 4, 0, 0); \
+  } while (0)
 
-  // ---- A: kGemmRT tiles of 16 rows, one 16-byte chunk per lane per step (zeros past the matrix)
-  const uint4 *wp = reinterpret_cast<const uint4 *>(mat);
-  const uint32_t *sp = reinterpret_cast<const uint32_t *>(mat + pack_weight_bytes(d));
-  bool tv[kGemmRT];
+  f32x4 acc[RT][CG];
 #pragma unroll
-  for (int r = 0; r < kGemmRT; r++) tv[r] = t0 + r < (int)d.tiles;
-  auto load_a = [&](int s, uint4 (&ar)[kGemmRT]) {
+  for (int r = 0; r < RT; r++)
 #pragma unroll
-    for (int r = 0; r < kGemmRT; r++) {
-      const bool v = tv[r] && s < (int)d.ns && 4 * s + g < (int)d.nb;
-      const uint4 x = wp[v ? ((size_t)(t0 + r) * 16 * d.nb) + s * 64 + lane : 0];
-      ar[r] = v ? x : make_uint4(0u, 0u, 0u, 0u);
-    }
-  };
-  auto load_as = [&](int q, uint32_t (&sw)[kGemmRT]) {
-#pragma unroll
-    for (int r = 0; r < kGemmRT; r++) {
-      const bool v = tv[r] && q < (int)d.nq;
-      const uint32_t x = sp[v ? ((size_t)(t0 + r) * d.nq + q) * 64 + lane : 0];
-      sw[r] = v ? x : 0u;
-    }
-  };
+    for (int c = 0; c < CG; c++) acc[r][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  f32x4 acc[kGemmRT][4];
+  // ---- bias of the epilogue, loaded now so that its latency hides under the K loop
+  const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
+  float4 bv[RT];
 #pragma unroll
-  for (int r = 0; r < kGemmRT; r++)
-#pragma unroll
-    for (int c = 0; c < 4; c++) acc[r][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int r = 0; r < RT; r++) bv[r] = reinterpret_cast<const float4 *>(bias)[min(t0 + r, (int)d.tiles - 1) * 4 + g];
 
-  // ---- K loop: step s computes from LDS buffer s % 2 and registers while the loads of step
-  //      s + 1 (B into staging registers, A into the next register set) are in flight
+  // ---- K loop: step s computes from ring slot s % D while steps s + 1 .. s + D - 1 load. Each
+  //      step ends with this wavefront's loads of step s + 1 complete (the VMEM operations
+  //      issued after them are those of steps s + 2 .. s + D - 1) and its LDS reads done, then a
+  //      barrier: slot (s + 1) % D is whole and slot s % D is free for step s + D.
+  static_assert(D == 2 || D == 3, "ring depth");
   const int ns = (int)d.ns;
-  uint4 a_cur[kGemmRT], a_nxt[kGemmRT];
-  uint32_t sw[kGemmRT];
-  load_b(0);
-  load_a(0, a_cur);
-  load_as(0, sw);
-  store_b(buf0);
-  __syncthreads();
-  for (int s = 0; s < ns; s++) {
-    const bool more = s + 1 < ns;
-    if (more) {
-      load_b(s + 1);
-      load_a(s + 1, a_nxt);
-    }
-    const uint8_t *cur = (s & 1) ? buf1 : buf0;
-    switch (s & 3) {
-      case 0: gemm_step<0>(acc, a_cur, sw, cur, j, g); break;
-      case 1: gemm_step<1>(acc, a_cur, sw, cur, j, g); break;
-      case 2: gemm_step<2>(acc, a_cur, sw, cur, j, g); break;
-      default: gemm_step<3>(acc, a_cur, sw, cur, j, g); break;
-    }
-    if (more) {
-      store_b((s & 1) ? buf0 : buf1);
-#pragma unroll
-      for (int r = 0; r < kGemmRT; r++) a_cur[r] = a_nxt[r];
-      if ((s & 3) == 3) load_as((s + 1) / 4, sw);
-    }
-    __syncthreads();  // buffer (s+1)%2 is complete and buffer s%2 is free
+  GEMM_LOAD(0);
+  if (D == 3 && 1 < ns) {
+    GEMM_LOAD(1);
+    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kIssue));
+  } else {
+    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
   }
+  __builtin_amdgcn_s_barrier();
+  for (int s = 0; s < ns; s++) {
+    __builtin_amdgcn_sched_barrier(0);
+    const bool more = s + D - 1 < ns;
+    if (more) GEMM_LOAD(s + D - 1);
+    gemm_step<RT, CG, W, D>(acc, smem_g + (s % D) * S::kSlot, wv, lane, 8 * (s & 3));
+    if (D == 3 && more)
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kIssue));
+    else
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+    __builtin_amdgcn_s_barrier();
+  }
+#undef GEMM_LOAD
 
   // ---- epilogue
-  const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
   if (MODE == GEMV_GATE_UP) {
-    // every 4 row tiles (64 rows) of the wavefront = h block W (h values 32 W .. 32 W + 31)
+    // every 4 row tiles (64 rows) of the wavefront = h block hb (h values 32 hb .. 32 hb + 31)
+    // of its entries. The h terms are staged per entry in the (now free) ring as [4 terms x 32
+    // bytes | 4 scale bytes], then copied to the h records with 16-byte stores.
+    static_assert(RT % 4 == 0, "whole h blocks per wavefront");
+    constexpr int kStage = 144;  // bytes per entry, 16-byte aligned
+    static_assert(W * S::kCols * kStage <= D * S::kSlot, "staging fits in the ring");
     uint8_t *hout = reinterpret_cast<uint8_t *>(a.out);
+    uint8_t *stage = smem_g + wv * S::kCols * kStage;
 #pragma unroll
-    for (int hbk = 0; hbk < kGemmRT / 4; hbk++) {
+    for (int hbk = 0; hbk < RT / 4; hbk++) {
       if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
-      const int W = t0 / 4 + hbk;
-      float4 bv[4];
+      const int hb = t0 / 4 + hbk;
 #pragma unroll
-      for (int r = 0; r < 4; r++) bv[r] = reinterpret_cast<const float4 *>(bias)[(t0 + 4 * hbk + r) * 4 + g];
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
+      for (int c = 0; c < CG; c++) {
+        if (16 * c >= ncol) break;
         float hv[8];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const f32x4 &av = acc[4 * hbk + r][c];
-          hv[2 * r] = swiglu(av[0] + bv[r].x, av[1] + bv[r].y, a.limit);
-          hv[2 * r + 1] = swiglu(av[2] + bv[r].z, av[3] + bv[r].w, a.limit);
+          const float4 &b4 = bv[4 * hbk + r];
+          hv[2 * r] = swiglu(av[0] + b4.x, av[1] + b4.y, a.limit);
+          hv[2 * r + 1] = swiglu(av[2] + b4.z, av[3] + b4.w, a.limit);
         }
         uint2 q[kTerms];
         uint32_t s4;
         split8_fp8_cols(hv, q, s4);
-        const int e = 16 * c + j;
-        if (e < ncol) {
-          uint8_t *hr = hout + (size_t)(beg + e) * G::kBytes;
-          const int s = W >> 2, i = W & 3;
+        uint8_t *se = stage + (16 * c + j) * kStage;
 #pragma unroll
-          for (int t = 0; t < kTerms; t++) {
+        for (int t = 0; t < kTerms; t++) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {  // h 8r + 2g, 8r + 2g + 1 of the block = bytes 2r, 2r+1
-              const uint32_t w = r < 2 ? q[t].x : q[t].y;
-              *reinterpret_cast<uint16_t *>(hr + G::data(s, t) + 32 * i + 8 * r + 2 * g) = (uint16_t)(w >> (16 * (r & 1)));
-            }
-            if (g == 0) hr[G::scale(s, t) + i] = (uint8_t)(s4 >> (8 * t));
+          for (int r = 0; r < 4; r++) {  // h 8r + 2g, 8r + 2g + 1 of the block = bytes 2r, 2r+1
+            const uint32_t w = r < 2 ? q[t].x : q[t].y;
+            *reinterpret_cast<uint16_t *>(se + t * 32 + 8 * r + 2 * g) = (uint16_t)(w >> (16 * (r & 1)));
           }
         }
+        if (g == 0) *reinterpret_cast<uint32_t *>(se + 128) = s4;
       }
+      const int st = hb >> 2, i = hb & 3;
+      for (int p = lane; p < ncol * 8; p += 64) {
+        const int e = p >> 3, t = (p >> 1) & 3, half = p & 1;
+        *reinterpret_cast<uint4 *>(hout + (size_t)(beg + e) * G::kBytes + G::data(st, t) + 32 * i + 16 * half) =
+            *reinterpret_cast<const uint4 *>(stage + e * kStage + t * 32 + 16 * half);
+      }
+      for (int p = lane; p < ncol * kTerms; p += 64) {
+        const int e = p / kTerms, t = p % kTerms;
+        hout[(size_t)(beg + e) * G::kBytes + G::scale(st, t) + i] = stage[e * kStage + 128 + t];
+      }
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));  // staging reads done before the next h block
     }
   } else {
     float *out = reinterpret_cast<float *>(a.out);
     const int R = (int)d.rows;
 #pragma unroll
-    for (int r = 0; r < kGemmRT; r++) {
+    for (int r = 0; r < RT; r++) {
       if (!tv[r]) continue;
-      const float4 b4 = reinterpret_cast<const float4 *>(bias)[(t0 + r) * 4 + g];
+      const float4 b4 = bv[r];
       const int row = (t0 + r) * 16 + 4 * g;
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
+      for (int c = 0; c < CG; c++) {
         const int e = 16 * c + j;
         if (e >= ncol) continue;
         float4 o;
@@ -315,20 +398,40 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1,
   }
 }
 
-size_t gemm_lds_bytes() { return (size_t)2 * kBufBytes; }
-
-hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &args, hipStream_t s) {
-  GemmArgs a = args;
-  a.n_row_blocks = (int)((a.d.rows + kGemmRows - 1) / kGemmRows);
-  if (a.d.ns > (uint32_t)kGemmNs || (mode == GEMV_GATE_UP && a.d.rows % 64)) return hipErrorInvalidValue;
-  const size_t blocks = (size_t)a.n_row_blocks * a.max_col_tiles;
+template <int MODE, int RT, int CG, int W, int D>
+static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
+  using S = GemmShape<RT, CG, W, D>;
+  static_assert(S::kLds <= 160 * 1024, "LDS");
+  static bool attr = false;  // the ring needs more than the default 64 KB of dynamic LDS
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_fp8<MODE, RT, CG, W, D>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  a.n_row_blocks = (int)((a.d.rows + S::kRows - 1) / S::kRows);
+  const size_t col_tiles = (size_t)a.max_active + (a.n_entries + S::kCols - 1) / S::kCols;
+  const size_t blocks = (size_t)a.n_row_blocks * col_tiles;
   if (!blocks) return hipSuccess;
-  const size_t lds = gemm_lds_bytes();
-  if (mode == GEMV_GATE_UP)
-    hipLaunchKernelGGL(k_gemm_fp8<GEMV_GATE_UP>, dim3((unsigned)blocks), dim3(kGemmThreads), lds, s, a);
-  else
-    hipLaunchKernelGGL(k_gemm_fp8<GEMV_DOWN>, dim3((unsigned)blocks), dim3(kGemmThreads), lds, s, a);
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CG, W, D>), dim3((unsigned)blocks), dim3(S::kThreads), S::kLds, s, a);
   return hipGetLastError();
+}
+
+// Column tile width from the mean entries per active expert (the per-expert counts live on the
+// device): 64 entries once experts average 48 or more (8 wavefronts, two per SIMD, so that one
+// wavefront's LDS reads overlap the other's MFMAs), down to 16 for a few per expert.
+template <int MODE>
+static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
+  const size_t active = std::max<size_t>(1, std::min<size_t>((size_t)a.max_active, a.n_entries));
+  const size_t mean = a.n_entries / active;
+  if (mean >= 48) return a.shape == 1 ? launch_gemm_shape<MODE, 8, 4, 4, 2>(a, s) : launch_gemm_shape<MODE, 4, 4, 8, 2>(a, s);
+  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 4, 3>(a, s);
+  return launch_gemm_shape<MODE, 4, 1, 4, 3>(a, s);
+}
+
+hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s) {
+  if (a.d.ns > (uint32_t)kGemmNs || (mode == GEMV_GATE_UP && a.d.rows % 64)) return hipErrorInvalidValue;
+  return mode == GEMV_GATE_UP ? launch_gemm_mode<GEMV_GATE_UP>(a, s) : launch_gemm_mode<GEMV_DOWN>(a, s);
 }
 
 }  // namespace moe

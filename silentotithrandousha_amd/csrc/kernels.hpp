@@ -69,7 +69,8 @@ struct GemmArgs {
   void *out;                 // GATE_UP: h records (GemmRec) per entry; DOWN: f32 [entry][rows]
   float limit;
   int max_active;            // upper bound of *n_active
-  int max_col_tiles;         // upper bound of the column tiles (64 entries) over all experts
+  size_t n_entries;          // entries over all experts (sets the column tiles)
+  int shape;                 // block shape override for tuning (0: by the mean entries per expert)
   int n_row_blocks;          // set by launch_gemm_fp8 (row blocks of the launch)
 };
 hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *rec, hipStream_t s);

@@ -120,7 +120,8 @@ struct moe_ctx {
   // single-token forwards: 0 = the batch path, 1 = two decode kernels, 2 = one launch
   // (falls back to 1, then 0, where a shape is not supported)
   int decode_mode = 2;
-  int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 32 entries, 2 always, 0 never
+  int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 4 entries, 2 always, 0 never
+  int gemm_shape = 0;  // grouped GEMM block shape override (tuning)
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h terms of the one-launch kernel (padding stays zero)
   uint32_t spin_limit = 1u << 20;
@@ -461,9 +462,9 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
                            c->w.active_off, c->w.entry_src, c->w.pos, s);
     }));
   const int max_active = (int)std::min(E, T * k);
-  // the grouped GEMM pays off once experts see tens of entries (64-entry tiles); smaller
-  // batches stream each weight tile once through the GEMV kernels
-  if (c->batch_gemm && T > 1 && (c->batch_gemm == 2 || T * k >= 32 * E) && c->L.gu.ns <= (uint32_t)kGemmNs &&
+  // the grouped GEMM (16- to 64-entry column tiles) pays off once experts average a few
+  // entries; smaller batches stream each weight tile through the GEMV kernels
+  if (c->batch_gemm && T > 1 && (c->batch_gemm == 2 || T * k >= 4 * E) && c->L.gu.ns <= (uint32_t)kGemmNs &&
       c->L.dn.ns <= (uint32_t)kGemmNs &&
       (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
     const size_t N = T * k;
@@ -476,7 +477,8 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     ga.active_off = c->w.active_off;
     ga.limit = c->clamp;
     ga.max_active = max_active;
-    ga.max_col_tiles = (int)(max_active + (N + 63) / 64);
+    ga.n_entries = N;
+    ga.shape = c->gemm_shape;
     GemmArgs gu = ga;
     gu.mat_off = c->L.gu_off;
     gu.bias_off = c->L.gub_off;
@@ -957,6 +959,10 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
     case MOE_OPT_BATCH_GEMM:
       if (value < 0 || value > 2) return fail(MOE_ERR_INVALID, "MOE_OPT_BATCH_GEMM is 0, 1 or 2");
       c->batch_gemm = (int)value;
+      return MOE_OK;
+    case MOE_OPT_GEMM_SHAPE:
+      if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0 or 1");
+      c->gemm_shape = (int)value;
       return MOE_OK;
     case MOE_OPT_SPIN_LIMIT:
       if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");

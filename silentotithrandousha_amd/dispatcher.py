@@ -129,6 +129,11 @@ class GpuMoeDispatcher:
         from ._ffi import MOE_OPT_BATCH_GEMM
         check(lib().moe_set_option(self._ctx, MOE_OPT_BATCH_GEMM, int(mode)))
 
+    def set_gemm_shape(self, shape):
+        """Grouped GEMM block shape for large batches (0 default, 1 alternative; tuning only)."""
+        from ._ffi import MOE_OPT_GEMM_SHAPE
+        check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_SHAPE, int(shape)))
+
     def set_spin_limit(self, polls):
         from ._ffi import MOE_OPT_SPIN_LIMIT
         check(lib().moe_set_option(self._ctx, MOE_OPT_SPIN_LIMIT, int(polls)))

@@ -451,11 +451,13 @@ def test_tiny_layer_fixture(fused):
 
 # ---------------------------------------------------------------- grouped GEMM (batches)
 
-@pytest.mark.parametrize("shape", [(512, 512, 16, 4, 300), (256, 128, 8, 2, 2), (1024, 512, 32, 4, 129)])
+@pytest.mark.parametrize("shape", [(512, 512, 16, 4, 300), (256, 128, 8, 2, 2), (1024, 512, 32, 4, 129),
+                                   (256, 256, 8, 4, 64)])
 def test_batch_gemm_matches_oracle_and_gemv(orc, shape):
-    """Batches through the grouped GEMM (block-scaled fp4 x fp8 MFMA, 4 activation terms) vs the
+    """Batches through the grouped GEMM (block-scaled fp4 x fp8 MFMA, 3 activation terms) vs the
     fp32 oracle (1e-3) and vs the per-tile GEMV path (bf16 hi+lo activations, 2e-4): uneven
-    expert loads, partial column tiles, partial row blocks."""
+    expert loads, partial column tiles, partial row blocks; 64-, 32- and 16-entry column tiles
+    (mean entries per expert 75, 32, 16 and 1)."""
     H, I, E, k, T = shape
     L = syn.make_layer(H, I, E, seed=400 + T, scale_lo=120, scale_hi=126, router_sigma=0.1)
     d = GpuMoeDispatcher(H, I, 7.0)
@@ -470,6 +472,25 @@ def test_batch_gemm_matches_oracle_and_gemv(orc, shape):
     d.set_batch_gemm(0)
     ref = d.layer_forward(0, x, k)
     assert rel_l2(got, ref) < 2e-4
+    d.close()
+
+
+def test_batch_gemm_block_shapes_identical(orc):
+    """The two block shapes for large batches (8 wavefronts x 64 rows, 4 x 128) accumulate every
+    output in the same K and term order: identical results."""
+    H, I, E, k, T = 512, 512, 16, 4, 300
+    L = syn.make_layer(H, I, E, seed=410, scale_lo=120, scale_hi=126, router_sigma=0.1)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    x = syn.hidden(T, H, seed=411)
+    d.set_batch_gemm(2)
+    outs = []
+    for shape in (0, 1):
+        d.set_gemm_shape(shape)
+        outs.append(d.layer_forward(0, x, k))
+    d.set_gemm_shape(0)
+    assert np.array_equal(outs[0], outs[1])
+    assert_rel_l2(outs[1], orc.moe_layer(x, L, k)[0], "gemm shape 1")
     d.close()
 
 
