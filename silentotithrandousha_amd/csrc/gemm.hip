@@ -97,6 +97,20 @@ constexpr int vm_wait(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
 // The same with lgkmcnt 0: also this wavefront's LDS operations complete.
 constexpr int vm_lgkm_wait(int n) { return vm_wait(n) & ~0x0F00; }
 
+// LDS-DMA of 16 (dwordx4) or 4 (dword) bytes per lane: lane l's bytes land at LDS address
+// lds + l * size (lds uniform over the wavefront). Written as inline assembly so that the compiler does not see these LDS writes:
+// it would otherwise make later LDS reads wait for every DMA in flight (it cannot always tell
+// the ring slots apart). The kernel orders them itself: vmcnt waits counted per step, then a
+// barrier, with compiler fences around it.
+__device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void *g, const void *lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
 // Block shape: W wavefronts x RT tiles of 16 weight rows each, x CG column groups of 16
 // entries shared by the W wavefronts. Every operand goes through LDS by LDS-DMA
 // (global_load_lds) into a ring of D K-steps: per step, the B records of the entries (kDma
@@ -110,11 +124,11 @@ struct GemmShape {
   static constexpr int kStepChunks = kCols * kChunks;        // 16-byte chunks of one K-step of B
   static constexpr int kGroups = (kStepChunks + 63) / 64;    // 1 KB pieces holding them
   static constexpr int kDma = (kGroups + W - 1) / W;         // B pieces per wavefront per step
-  static constexpr int kBufB = kGroups * 1024;               // LDS bytes of one step of B
+  static constexpr int kBufB = kDma * W * 1024;              // one step of B (+ the pieces past kGroups)
   static constexpr int kBufA = W * RT * 1024;                // A chunks of one step
   static constexpr int kBufS = W * RT * 256;                 // A-scale words of one step
   static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
-  static constexpr int kLds = D * kSlot + 1024;              // + 1 KB for the pieces past kGroups
+  static constexpr int kLds = D * kSlot;
   static constexpr int kIssue = kDma + 2 * RT;               // VMEM operations per wavefront per step
 };
 
@@ -175,7 +189,11 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CG], const uint8_t *s
 template <int MODE, int RT, int CG, int W, int D>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_gemm_fp8(GemmArgs a) {
   using S = GemmShape<RT, CG, W, D>;
-  extern __shared__ __attribute__((aligned(1024))) uint8_t smem_g[];
+  // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
+  // alias the reads of another, so those reads do not wait for it
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r0[S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r1[S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
   __shared__ int s_tile[4];  // expert record index, first entry, entry count, row block
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -233,12 +251,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   const uint8_t *rec = a.base + (size_t)ex * a.stride;
   const uint8_t *mat = rec + a.mat_off;
   const PackDims d = a.d;
-  uint8_t *const trash = smem_g + D * S::kSlot;
 
   // ---- sources. B: piece i of the wavefront = 1 KB piece 4 i + wv of the step, chunk c =
   //      64 (4 i + wv) + lane (entry c / kChunks, part c % kChunks: the first kGemmTerms terms'
   //      16-byte pieces, then the 16 scale bytes); padding entries repeat a valid entry; pieces
-  //      past kGroups go to the trash KB. A: chunk (step, lane) of each of the wavefront's RT
+  //      past kGroups land in the unused tail of the slot's B area. A: chunk (step, lane) of each of the wavefront's RT
   //      tiles; tiles past the matrix read the last tile (results not stored); a lane's K-block
   //      past the matrix reads an in-range chunk, whose scale byte is 0 (the packer zero-fills
   //      them) while the B records hold zeros there, so it adds exact zeros. Every lane of every
@@ -265,24 +282,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     ssrc[r] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
   }
   const uint8_t *alast = mat + last_chunk * 16;
-#define GEMM_LOAD(step)                                                                             \
+#define GEMM_LOAD(step, sl)                                                                         \
   do {                                                                                              \
-    uint8_t *sl = smem_g + ((step) % D) * S::kSlot;                                                 \
     _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                           \
-      uint8_t *dst = W * i + wv < S::kGroups ? sl + 1024 * (W * i + wv) : trash;                    \
-      __builtin_amdgcn_global_load_lds(                                                             \
-          reinterpret_cast<const uint32_t *>(bsrc[i] + (size_t)(step) * G::kStep),                  \
-          (__attribute__((address_space(3))) void *)dst, 16, 0, 0);                                 \
+      lds_dma16(bsrc[i] + (size_t)(step) * G::kStep, (sl) + 1024 * (W * i + wv));                  \
     }                                                                                               \
     _Pragma("unroll") for (int r = 0; r < RT; r++) {                                                \
       const uint8_t *src = asrc[r] + (size_t)(step) * 1024 + 16 * lane;                             \
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src < alast ? src : alast), \
-          (__attribute__((address_space(3))) void *)(sl + S::kBufB + (wv * RT + r) * 1024), 16, 0, 0); \
+      lds_dma16(src < alast ? src : alast, (sl) + S::kBufB + (wv * RT + r) * 1024);                 \
     }                                                                                               \
     _Pragma("unroll") for (int r = 0; r < RT; r++)                                                  \
-      __builtin_amdgcn_global_load_lds(                                                             \
-          reinterpret_cast<const uint32_t *>(ssrc[r] + (size_t)((step) >> 2) * 256),                \
-          (__attribute__((address_space(3))) void *)(sl + S::kBufB + S::kBufA + (wv * RT + r) * 256), 4, 0, 0); \
+      lds_dma4(ssrc[r] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (wv * RT + r) * 256); \
   } while (0)
 
   f32x4 acc[RT][CG];
@@ -297,31 +307,44 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 #pragma unroll
   for (int r = 0; r < RT; r++) bv[r] = reinterpret_cast<const float4 *>(bias)[min(t0 + r, (int)d.tiles - 1) * 4 + g];
 
-  // ---- K loop: step s computes from ring slot s % D while steps s + 1 .. s + D - 1 load. Each
-  //      step ends with this wavefront's loads of step s + 1 complete (the VMEM operations
-  //      issued after them are those of steps s + 2 .. s + D - 1) and its LDS reads done, then a
-  //      barrier: slot (s + 1) % D is whole and slot s % D is free for step s + D.
+  // ---- K loop, unrolled by D so that each step names its ring slots: step s computes from
+  //      slot s % D while steps s + 1 .. s + D - 1 load. Every step issues one step's loads
+  //      (past the last step: a repeat of step ns - 1 into the free slot), so the VMEM count is
+  //      the same at every step and the wait needs no branch: each step ends with this
+  //      wavefront's loads of step s + 1 complete (issued after them: D - 2 steps' loads) and
+  //      its LDS reads done, then a barrier: slot (s + 1) % D is whole, slot s % D is free.
   static_assert(D == 2 || D == 3, "ring depth");
   const int ns = (int)d.ns;
-  GEMM_LOAD(0);
-  if (D == 3 && 1 < ns) {
-    GEMM_LOAD(1);
-    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kIssue));
-  } else {
-    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
-  }
+#define GEMM_STEP(st, cur, nxt)                                                                     \
+  do {                                                                                              \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    GEMM_LOAD(min((st) + D - 1, ns - 1), nxt);                                                      \
+    gemm_step<RT, CG, W, D>(acc, cur, wv, lane, 8 * ((st) & 3));                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));                                  \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
+    __builtin_amdgcn_s_barrier();                                                                   \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
+  } while (0)
+  GEMM_LOAD(0, s_r0);
+  if (D == 3) GEMM_LOAD(min(1, ns - 1), s_r1);
+  __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
-  for (int s = 0; s < ns; s++) {
-    __builtin_amdgcn_sched_barrier(0);
-    const bool more = s + D - 1 < ns;
-    if (more) GEMM_LOAD(s + D - 1);
-    gemm_step<RT, CG, W, D>(acc, smem_g + (s % D) * S::kSlot, wv, lane, 8 * (s & 3));
-    if (D == 3 && more)
-      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kIssue));
-    else
-      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
-    __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (D == 2) {
+    for (int s = 0; s < ns; s += 2) {
+      GEMM_STEP(s, s_r0, s_r1);
+      if (s + 1 < ns) GEMM_STEP(s + 1, s_r1, s_r0);
+    }
+  } else {
+    for (int s = 0; s < ns; s += 3) {
+      GEMM_STEP(s, s_r0, s_r2);
+      if (s + 1 < ns) GEMM_STEP(s + 1, s_r1, s_r0);
+      if (s + 2 < ns) GEMM_STEP(s + 2, s_r2, s_r1);
+    }
   }
+#undef GEMM_STEP
 #undef GEMM_LOAD
 
   // ---- epilogue
@@ -331,9 +354,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     // bytes | 4 scale bytes], then copied to the h records with 16-byte stores.
     static_assert(RT % 4 == 0, "whole h blocks per wavefront");
     constexpr int kStage = 144;  // bytes per entry, 16-byte aligned
-    static_assert(W * S::kCols * kStage <= D * S::kSlot, "staging fits in the ring");
+    static_assert(W <= 8 && 4 * S::kCols * kStage <= S::kSlot, "staging fits in two ring slots");
     uint8_t *hout = reinterpret_cast<uint8_t *>(a.out);
-    uint8_t *stage = smem_g + wv * S::kCols * kStage;
+    uint8_t *stage = (wv < 4 ? s_r0 : s_r1) + (wv & 3) * S::kCols * kStage;
 #pragma unroll
     for (int hbk = 0; hbk < RT / 4; hbk++) {
       if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
@@ -401,19 +424,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 template <int MODE, int RT, int CG, int W, int D>
 static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   using S = GemmShape<RT, CG, W, D>;
-  static_assert(S::kLds <= 160 * 1024, "LDS");
-  static bool attr = false;  // the ring needs more than the default 64 KB of dynamic LDS
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_fp8<MODE, RT, CG, W, D>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
   a.n_row_blocks = (int)((a.d.rows + S::kRows - 1) / S::kRows);
   const size_t col_tiles = (size_t)a.max_active + (a.n_entries + S::kCols - 1) / S::kCols;
   const size_t blocks = (size_t)a.n_row_blocks * col_tiles;
   if (!blocks) return hipSuccess;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CG, W, D>), dim3((unsigned)blocks), dim3(S::kThreads), S::kLds, s, a);
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CG, W, D>), dim3((unsigned)blocks), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
