@@ -23,73 +23,121 @@ namespace moe {
 
 using G = GemmRec;  // step-major activation record (kernels.hpp)
 
-// Quad of lanes 16 apart (lane, lane+16, lane+32, lane+48) holding one 32-value block: the
-// split of split8_fp8 with the block reductions across lane bits 4 and 5.
-__device__ __forceinline__ void split8_fp8_cols(const float x[8], uint2 q[kTerms], uint32_t &s4) {
-  float m = 0.0f, bad = 0.0f;
+// ------------------------------------------------------------------ fp6 activation terms
+
+// E2M3 (fp6: sign, 2 exponent bits with bias 1, 3 mantissa bits; no Inf/NaN, largest 7.5) code
+// of t, rounded to nearest even and saturated at 7.5; q = the value of the code. The grid is
+// 1/8 below 2, 1/4 in [2, 4), 1/2 in [4, 8): n = rint(|t| / grid) counts grid steps exactly,
+// and the code is n, n + 8 or n + 16 in the three ranges (n = 16 at a range's top is the next
+// range's first code).
+__device__ __forceinline__ uint32_t e2m3_rne(float t, float &q) {
+  const float a = fabsf(t);
+  const bool r0 = a < 2.0f, r1 = a < 4.0f;
+  const float inv = r0 ? 8.0f : (r1 ? 4.0f : 2.0f);
+  float n = rintf(a * inv);
+  if (!r1) n = fminf(n, 15.0f);
+  const uint32_t code = (uint32_t)n + (r0 ? 0u : (r1 ? 8u : 16u));
+  const float m = n * (r0 ? 0.125f : (r1 ? 0.25f : 0.5f));
+  q = t < 0.0f ? -m : m;
+  return code | (t < 0.0f ? 0x20u : 0u);
+}
+
+// Split of 16 values of a 32-value block (block max |x| = m, bad = some value of the block is
+// not finite) into kGemmTerms E2M3 terms: term t has scale 2^(E - 2 - 5t) where m = f 2^E,
+// f in [1/2, 1) (so term 0 holds the block in [-4, 4)), and takes the exact residual of the
+// terms before it (the activation is then exact to about 2^-13 of the block maximum). Codes of
+// value u at bits 6u of d[t][0..2]; sb byte t = the E8M0 scale of term t (0xFF, NaN, for a bad
+// block: the products come out NaN, as the f32 arithmetic would).
+__device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool bad, uint32_t (&d)[kGemmTerms][3],
+                                            uint32_t &sb) {
+  int E = 0;
+  if (m > 0.0f && isfinite(m)) frexpf(m, &E);
+  float r[16];
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    m = fmaxf(m, fabsf(x[i]));
-    if (!isfinite(x[i])) bad = 1.0f;
+  for (int i = 0; i < 16; i++) r[i] = bad ? 0.0f : x[i];
+  sb = 0;
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    const int se = max(E - 2 - 5 * t, -127);
+    sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
+    uint64_t lo = 0, hi = 0;  // 96 bits: values 0..9 in lo (bits 0..59), 10..15 in hi (60..95)
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float q;
+      const uint32_t c = e2m3_rne(__builtin_amdgcn_ldexpf(r[i], -se), q);
+      r[i] = r[i] - __builtin_amdgcn_ldexpf(q, se);
+      if (i < 10)
+        lo |= (uint64_t)c << (6 * i);
+      else
+        hi |= (uint64_t)c << (6 * (i - 10));
+    }
+    d[t][0] = (uint32_t)lo;
+    d[t][1] = (uint32_t)(lo >> 32) | (uint32_t)(hi << 28);
+    d[t][2] = (uint32_t)(hi >> 4);
   }
-  m = fmaxf(m, xor_lane<16>(m));
-  m = fmaxf(m, xor_lane<32>(m));
-  bad = fmaxf(bad, xor_lane<16>(bad));
-  bad = fmaxf(bad, xor_lane<32>(bad));
-  split8_fp8_with_max(x, m, bad != 0.0f, q, s4);
 }
 
 // ------------------------------------------------------------------ activation records
 
-// grid (ceil(4 ns / 64), rows), 256 threads: thread quad q of block x handles 32-block
-// b = 64 x + q of row `row` (values past K are zeros, blocks up to 4 * kGemmNs written).
+// grid (1, rows), 256 threads: thread p < 8 kGemmNs handles half p & 1 of 32-block p >> 1 of
+// row `row` (values past K are zeros, blocks up to 4 * kGemmNs written); the two halves of a
+// block are neighbouring lanes.
 __global__ __launch_bounds__(256) void k_split_rows(const float *src, int K, uint8_t *rec) {
-  const int row = blockIdx.y, tid = threadIdx.x;
-  const int b = blockIdx.x * 64 + (tid >> 2), part = tid & 3;
-  if (blockIdx.x * 64 >= 4 * kGemmNs) return;
-  float v[8];
-  const int k0 = 32 * b + 8 * part;
-  if (b < 4 * kGemmNs && k0 < K) {
-    const float4 a0 = *reinterpret_cast<const float4 *>(src + (size_t)row * K + k0);
-    const float4 a1 = *reinterpret_cast<const float4 *>(src + (size_t)row * K + k0 + 4);
-    v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-    v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-  } else {
+  const int row = blockIdx.y, p = threadIdx.x;
+  const int b = p >> 1, h = p & 1;
+  const int k0 = 32 * b + 16 * h;
+  float v[16];
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+  for (int q = 0; q < 4; q++) {
+    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (p < 8 * kGemmNs && k0 + 4 * q < K) a = *reinterpret_cast<const float4 *>(src + (size_t)row * K + k0 + 4 * q);
+    v[4 * q] = a.x;
+    v[4 * q + 1] = a.y;
+    v[4 * q + 2] = a.z;
+    v[4 * q + 3] = a.w;
   }
-  uint2 q[kTerms];
-  uint32_t s4;
-  split8_fp8(v, q, s4);
-  if (b >= 4 * kGemmNs) return;
+  float m = 0.0f, bad = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    m = fmaxf(m, fabsf(v[i]));
+    if (!isfinite(v[i])) bad = 1.0f;
+  }
+  m = fmaxf(m, xor_lane<1>(m));
+  bad = fmaxf(bad, xor_lane<1>(bad));
+  uint32_t d[kGemmTerms][3], sb;
+  split16_fp6(v, m, bad != 0.0f, d, sb);
+  if (p >= 8 * kGemmNs) return;
   uint8_t *r = rec + (size_t)row * G::kBytes;
-  const int s = b >> 2, i = b & 3;
+  const int st = b >> 2, i = b & 3;
 #pragma unroll
-  for (int t = 0; t < kTerms; t++) *reinterpret_cast<uint2 *>(r + G::data(s, t) + 32 * i + 8 * part) = q[t];
-  if (part == 0) {
+  for (int t = 0; t < kGemmTerms; t++) {
+    uint32_t *dst = reinterpret_cast<uint32_t *>(r + G::half(st, t, i, h));
+    dst[0] = d[t][0];
+    dst[1] = d[t][1];
+    dst[2] = d[t][2];
+  }
+  if (h == 0) {
 #pragma unroll
-    for (int t = 0; t < kTerms; t++) r[G::scale(s, t) + i] = (uint8_t)(s4 >> (8 * t));
+    for (int t = 0; t < kGemmTerms; t++) r[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
   }
 }
 
 hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *rec, hipStream_t s) {
+  static_assert(8 * kGemmNs <= 256, "one thread per half block");
   if (K % 8 || K > (size_t)kGemmNs * 128) return hipErrorInvalidValue;
   if (!rows) return hipSuccess;
-  hipLaunchKernelGGL(k_split_rows, dim3((4 * kGemmNs + 63) / 64, (unsigned)rows), dim3(256), 0, s, src,
-                     (int)K, rec);
+  hipLaunchKernelGGL(k_split_rows, dim3(1, (unsigned)rows), dim3(256), 0, s, src, (int)K, rec);
   return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ grouped GEMM
 
-// The batch path multiplies by the first kGemmTerms terms of the records (3 of 4: the
-// activation is then exact to 2^-12 of each value, well inside the 1e-3 tolerance; the fourth
-// term would add a third more MFMA work and LDS traffic for precision no caller needs).
-constexpr int kGemmTerms = 3;
-constexpr int kEntryStep = kGemmTerms * 128 + 16;   // LDS bytes of one entry's K-step
-static_assert(G::kStep == kTerms * 128 + 16, "a K-step of a record = term data + 16 scale bytes");
-static_assert(kEntryStep % 64 == 16, "entry stride: 16-byte aligned, spreads over the LDS banks");
-constexpr int kChunks = kEntryStep / 16;            // 16-byte chunks per entry K-step (25)
+// The batch path's activations are kGemmTerms E2M3 terms (exact to about 2^-13 of each block's
+// maximum, well inside the 1e-3 tolerance): the fp4 x fp6 MFMA issues in 16 cycles where fp4 x
+// fp8 takes 32, and a K-step of a record is 304 bytes instead of 400 for three fp8 terms.
+constexpr int kEntryStep = G::kStep;                // LDS bytes of one entry's K-step (a record step)
+static_assert(kEntryStep % 16 == 0, "entry stride: 16-byte aligned");
+constexpr int kChunks = kEntryStep / 16;            // 16-byte chunks per entry K-step (19)
 
 // s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
 // outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima).
@@ -111,25 +159,29 @@ __device__ __forceinline__ void lds_dma4(const void *g, const void *lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
-// Block shape: W wavefronts x RT tiles of 16 weight rows each, x CG column groups of 16
-// entries shared by the W wavefronts. Every operand goes through LDS by LDS-DMA
-// (global_load_lds) into a ring of D K-steps: per step, the B records of the entries (kDma
-// 1 KB pieces per wavefront), and per wavefront its RT A chunks (1 KB each) and RT A-scale words
-// (256 B each).
-template <int RT, int CG, int W, int D>
+// Block shape: WR x WC wavefronts; wavefront (wr, wc) owns RT tiles of 16 weight rows (row
+// group wr) x CGW column groups of 16 entries (entry group wc). Every operand goes through LDS by
+// LDS-DMA (global_load_lds) into a ring of D K-steps: per step, the B records of the block's
+// entries (kDma 1 KB pieces per wavefront), the block's WR * RT A chunks (1 KB each) and A-scale
+// words (256 B each), kDmaA of each per wavefront.
+template <int RT, int CGW, int WR, int WC, int D>
 struct GemmShape {
+  static constexpr int W = WR * WC;
   static constexpr int kThreads = 64 * W;
-  static constexpr int kRows = 16 * RT * W;                  // weight rows per block
-  static constexpr int kCols = 16 * CG;                      // entries per block
+  static constexpr int kRows = 16 * RT * WR;                 // weight rows per block
+  static constexpr int kCols = 16 * CGW * WC;                // entries per block
   static constexpr int kStepChunks = kCols * kChunks;        // 16-byte chunks of one K-step of B
   static constexpr int kGroups = (kStepChunks + 63) / 64;    // 1 KB pieces holding them
   static constexpr int kDma = (kGroups + W - 1) / W;         // B pieces per wavefront per step
+  static constexpr int kTilesA = WR * RT;                    // A tiles of the block
+  static constexpr int kDmaA = kTilesA / W;                  // A tiles (and scale words) per wavefront
+  static_assert(kTilesA % W == 0, "A tiles shared evenly");
   static constexpr int kBufB = kDma * W * 1024;              // one step of B (+ the pieces past kGroups)
-  static constexpr int kBufA = W * RT * 1024;                // A chunks of one step
-  static constexpr int kBufS = W * RT * 256;                 // A-scale words of one step
+  static constexpr int kBufA = kTilesA * 1024;               // A chunks of one step
+  static constexpr int kBufS = kTilesA * 256;                // A-scale words of one step
   static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
   static constexpr int kLds = D * kSlot;
-  static constexpr int kIssue = kDma + 2 * RT;               // VMEM operations per wavefront per step
+  static constexpr int kIssue = kDma + 2 * kDmaA;            // VMEM operations per wavefront per step
 };
 
 // B operands of one column group for the wavefront's lanes (entry j, lane group g): per term the
@@ -142,10 +194,10 @@ struct GemmB {
 __device__ __forceinline__ void gemm_read_b(GemmB &b, const uint8_t *eb, int g) {
 #pragma unroll
   for (int t = 0; t < kGemmTerms; t++) {
-    const uint4 b0 = *reinterpret_cast<const uint4 *>(eb + t * 128 + 32 * (g >> 1) + 16 * (g & 1));
-    const uint4 b1 = *reinterpret_cast<const uint4 *>(eb + t * 128 + 64 + 32 * (g >> 1) + 16 * (g & 1));
-    b.v[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-    b.sc[t] = *reinterpret_cast<const uint32_t *>(eb + kGemmTerms * 128 + 4 * t) >> (8 * g);
+    const uint2 *q = reinterpret_cast<const uint2 *>(eb + t * G::kTermBytes + 24 * g);
+    const uint2 d0 = q[0], d1 = q[1], d2 = q[2];
+    b.v[t] = i32x8{(int)d0.x, (int)d0.y, (int)d1.x, (int)d1.y, (int)d2.x, (int)d2.y, 0, 0};
+    b.sc[t] = *reinterpret_cast<const uint32_t *>(eb + kGemmTerms * G::kTermBytes + 4 * t) >> (8 * g);
   }
 }
 
@@ -153,12 +205,14 @@ __device__ __forceinline__ void gemm_read_b(GemmB &b, const uint8_t *eb, int g) 
 // operands from the step's ring slot; sh = 8 * (s % 4) selects the step's byte of the A-scale
 // words. The B operands of column group c + 1 are read while the MFMAs of group c run. Column
 // groups past the block's entries compute on repeated entries (not stored).
-template <int RT, int CG, int W, int D>
-__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CG], const uint8_t *slot, int wv, int lane, int sh) {
-  using S = GemmShape<RT, CG, W, D>;
+template <int RT, int CGW, int WR, int WC, int D>
+__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *slot, int wr, int wc, int lane,
+                                          int sh) {
+  using S = GemmShape<RT, CGW, WR, WC, D>;
+  constexpr int CG = CGW;
   const int j = lane & 15, g = lane >> 4;
-  const uint8_t *bb = slot + j * kEntryStep, *ab = slot + S::kBufB + wv * RT * 1024,
-                *sb = slot + S::kBufB + S::kBufA + wv * RT * 256;
+  const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024,
+                *sb = slot + S::kBufB + S::kBufA + wr * RT * 256;
   uint4 ar[RT];
   uint32_t sw[RT];
 #pragma unroll
@@ -177,7 +231,8 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CG], const uint8_t *s
 #pragma unroll
       for (int r = 0; r < RT; r++) {
         const i32x8 A = {(int)ar[r].x, (int)ar[r].y, (int)ar[r].z, (int)ar[r].w, 0, 0, 0, 0};
-        acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, bc.v[t], acc[r][c], 4, 0, 0, (int)sw[r], 0,
+        // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
+        acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, bc.v[t], acc[r][c], 4, 2, 0, (int)sw[r], 0,
                                                                      (int)bc.sc[t]);
       }
     }
@@ -186,16 +241,19 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CG], const uint8_t *s
   }
 }
 
-template <int MODE, int RT, int CG, int W, int D>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_gemm_fp8(GemmArgs a) {
-  using S = GemmShape<RT, CG, W, D>;
+template <int MODE, int RT, int CGW, int WR, int WC, int D>
+__global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
+  using S = GemmShape<RT, CGW, WR, WC, D>;
+  constexpr int W = S::W, CG = CGW;
   // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
   // alias the reads of another, so those reads do not wait for it
   __shared__ __attribute__((aligned(1024))) uint8_t s_r0[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r1[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
+  __shared__ __attribute__((aligned(16))) float s_bias[W * RT * 16];  // per wavefront: its rows' bias
   __shared__ int s_tile[4];  // expert record index, first entry, entry count, row block
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wr = wv % WR, wc = wv / WR;
   const int j = lane & 15, g = lane >> 4;
 
   // ---- tile: global column tile cl (over the experts' kCols-entry tiles) and row block, row
@@ -247,20 +305,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   const int ex = s_tile[0], beg = s_tile[1], ncol = s_tile[2];
   if (ex < 0) return;
   const int rblk = s_tile[3];
-  const int t0 = (rblk * S::kRows + wv * 16 * RT) / 16;  // first 16-row tile of the wavefront
+  const int tb = rblk * S::kRows / 16;  // first 16-row tile of the block
+  const int t0 = tb + wr * RT;           // first 16-row tile of the wavefront
   const uint8_t *rec = a.base + (size_t)ex * a.stride;
   const uint8_t *mat = rec + a.mat_off;
   const PackDims d = a.d;
 
-  // ---- sources. B: piece i of the wavefront = 1 KB piece 4 i + wv of the step, chunk c =
-  //      64 (4 i + wv) + lane (entry c / kChunks, part c % kChunks: the first kGemmTerms terms'
-  //      16-byte pieces, then the 16 scale bytes); padding entries repeat a valid entry; pieces
-  //      past kGroups land in the unused tail of the slot's B area. A: chunk (step, lane) of each of the wavefront's RT
-  //      tiles; tiles past the matrix read the last tile (results not stored); a lane's K-block
-  //      past the matrix reads an in-range chunk, whose scale byte is 0 (the packer zero-fills
-  //      them) while the B records hold zeros there, so it adds exact zeros. Every lane of every
-  //      DMA runs, so each wavefront issues exactly kIssue VMEM operations per step, which the
-  //      vmcnt waits count on.
+  // ---- sources. B: piece i of the wavefront = 1 KB piece W i + wv of the step, chunk c =
+  //      64 (W i + wv) + lane (entry c / kChunks, 16-byte part c % kChunks of the record
+  //      step); padding entries repeat a valid entry; pieces past kGroups land in the unused
+  //      tail of the slot's B area. A: the block's WR RT tiles, tile W i + wv by this
+  //      wavefront, chunk (step, lane) of each; tiles past the matrix read the last tile
+  //      (results not stored); a lane's K-block past the matrix reads an in-range chunk, whose
+  //      scale byte is 0 (the packer zero-fills them) while the B records hold zeros there, so
+  //      it adds exact zeros. Every lane of every DMA runs, so each wavefront issues exactly
+  //      kIssue VMEM operations per step, which the vmcnt waits count on.
   const uint8_t *bsrc[S::kDma];
 #pragma unroll
   for (int i = 0; i < S::kDma; i++) {
@@ -268,31 +327,32 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     const int e = c / kChunks, part = c % kChunks;
     const int ge = beg + min(e, ncol - 1);
     const int row = a.entry_src ? a.entry_src[ge] : ge;
-    bsrc[i] = a.brec + (size_t)row * G::kBytes + (part < kChunks - 1 ? 16 * part : kTerms * 128);
+    bsrc[i] = a.brec + (size_t)row * G::kBytes + 16 * part;
   }
-  const uint8_t *asrc[RT];
-  const uint8_t *ssrc[RT];
-  bool tv[RT];
+  const uint8_t *asrc[S::kDmaA];  // the wavefront's share of the block's A tiles: W i + wv
+  const uint8_t *ssrc[S::kDmaA];
   const size_t last_chunk = (size_t)d.rows * d.nb - 1;
 #pragma unroll
-  for (int r = 0; r < RT; r++) {
-    tv[r] = t0 + r < (int)d.tiles;
-    const int tl = min(t0 + r, (int)d.tiles - 1);
-    asrc[r] = mat + (size_t)tl * 16 * d.nb * 16;
-    ssrc[r] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
+  for (int i = 0; i < S::kDmaA; i++) {
+    const int tl = min(tb + W * i + wv, (int)d.tiles - 1);
+    asrc[i] = mat + (size_t)tl * 16 * d.nb * 16;
+    ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
   }
+  bool tv[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) tv[r] = t0 + r < (int)d.tiles;
   const uint8_t *alast = mat + last_chunk * 16;
 #define GEMM_LOAD(step, sl)                                                                         \
   do {                                                                                              \
     _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                           \
       lds_dma16(bsrc[i] + (size_t)(step) * G::kStep, (sl) + 1024 * (W * i + wv));                  \
     }                                                                                               \
-    _Pragma("unroll") for (int r = 0; r < RT; r++) {                                                \
-      const uint8_t *src = asrc[r] + (size_t)(step) * 1024 + 16 * lane;                             \
-      lds_dma16(src < alast ? src : alast, (sl) + S::kBufB + (wv * RT + r) * 1024);                 \
+    _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++) {                                          \
+      const uint8_t *src = asrc[i] + (size_t)(step) * 1024 + 16 * lane;                             \
+      lds_dma16(src < alast ? src : alast, (sl) + S::kBufB + (W * i + wv) * 1024);                  \
     }                                                                                               \
-    _Pragma("unroll") for (int r = 0; r < RT; r++)                                                  \
-      lds_dma4(ssrc[r] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (wv * RT + r) * 256); \
+    _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                            \
+      lds_dma4(ssrc[i] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (W * i + wv) * 256); \
   } while (0)
 
   f32x4 acc[RT][CG];
@@ -301,11 +361,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 #pragma unroll
     for (int c = 0; c < CG; c++) acc[r][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // ---- bias of the epilogue, loaded now so that its latency hides under the K loop
-  const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
-  float4 bv[RT];
+  // ---- bias of the wavefront's rows into LDS by DMA before the K loop (complete at the first
+  //      wait), read in the epilogue
+  {
+    const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
 #pragma unroll
-  for (int r = 0; r < RT; r++) bv[r] = reinterpret_cast<const float4 *>(bias)[min(t0 + r, (int)d.tiles - 1) * 4 + g];
+    for (int k = 0; k < RT / 4; k++)
+      lds_dma4(bias + min(t0 * 16 + 64 * k + lane, (int)d.rows - 1), s_bias + (wv * RT + 4 * k) * 16);
+  }
 
   // ---- K loop, unrolled by D so that each step names its ring slots: step s computes from
   //      slot s % D while steps s + 1 .. s + D - 1 load. Every step issues one step's loads
@@ -319,7 +382,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   do {                                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     GEMM_LOAD(min((st) + D - 1, ns - 1), nxt);                                                      \
-    gemm_step<RT, CG, W, D>(acc, cur, wv, lane, 8 * ((st) & 3));                                    \
+    gemm_step<RT, CGW, WR, WC, D>(acc, cur, wr, wc, lane, 8 * ((st) & 3));                          \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));                                  \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
@@ -348,53 +411,75 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 #undef GEMM_LOAD
 
   // ---- epilogue
+  float4 bv[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) bv[r] = *reinterpret_cast<const float4 *>(s_bias + (wv * RT + r) * 16 + 4 * g);
   if (MODE == GEMV_GATE_UP) {
     // every 4 row tiles (64 rows) of the wavefront = h block hb (h values 32 hb .. 32 hb + 31)
-    // of its entries. The h terms are staged per entry in the (now free) ring as [4 terms x 32
-    // bytes | 4 scale bytes], then copied to the h records with 16-byte stores.
+    // of its entries. The SwiGLU values are staged in the (now free) ring as f32 [entry][32];
+    // then lane 2 e + h takes half h of entry e's block: the kGemmTerms E2M3 terms of its 16
+    // values (block maximum shared with the neighbouring lane) go to the h record.
     static_assert(RT % 4 == 0, "whole h blocks per wavefront");
-    constexpr int kStage = 144;  // bytes per entry, 16-byte aligned
-    static_assert(W <= 8 && 4 * S::kCols * kStage <= S::kSlot, "staging fits in two ring slots");
+    constexpr int kWaveCols = 16 * CGW;  // entries of the wavefront
+    static_assert(kWaveCols <= 32 || kWaveCols == 64, "one or two passes of 64 lanes");
+    static_assert(W <= 8 && 4 * kWaveCols * 128 <= S::kSlot, "staging fits in two ring slots");
     uint8_t *hout = reinterpret_cast<uint8_t *>(a.out);
-    uint8_t *stage = (wv < 4 ? s_r0 : s_r1) + (wv & 3) * S::kCols * kStage;
+    float *stage = reinterpret_cast<float *>((wv < 4 ? s_r0 : s_r1) + (wv & 3) * kWaveCols * 128);
+    const int e0 = kWaveCols * wc;                                     // first entry of the wavefront
+    const int nloc = max(0, min(kWaveCols, ncol - e0));                // its entries in the tile
 #pragma unroll
     for (int hbk = 0; hbk < RT / 4; hbk++) {
       if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
       const int hb = t0 / 4 + hbk;
 #pragma unroll
       for (int c = 0; c < CG; c++) {
-        if (16 * c >= ncol) break;
-        float hv[8];
+        if (16 * c >= nloc) break;
+        float *se = stage + (16 * c + j) * 32;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
+        for (int r = 0; r < 4; r++) {  // h values 8r + 2g, 8r + 2g + 1 of the block
           const f32x4 &av = acc[4 * hbk + r][c];
           const float4 &b4 = bv[4 * hbk + r];
-          hv[2 * r] = swiglu(av[0] + b4.x, av[1] + b4.y, a.limit);
-          hv[2 * r + 1] = swiglu(av[2] + b4.z, av[3] + b4.w, a.limit);
+          *reinterpret_cast<float2 *>(se + 8 * r + 2 * g) =
+              make_float2(swiglu(av[0] + b4.x, av[1] + b4.y, a.limit), swiglu(av[2] + b4.z, av[3] + b4.w, a.limit));
         }
-        uint2 q[kTerms];
-        uint32_t s4;
-        split8_fp8_cols(hv, q, s4);
-        uint8_t *se = stage + (16 * c + j) * kStage;
-#pragma unroll
-        for (int t = 0; t < kTerms; t++) {
-#pragma unroll
-          for (int r = 0; r < 4; r++) {  // h 8r + 2g, 8r + 2g + 1 of the block = bytes 2r, 2r+1
-            const uint32_t w = r < 2 ? q[t].x : q[t].y;
-            *reinterpret_cast<uint16_t *>(se + t * 32 + 8 * r + 2 * g) = (uint16_t)(w >> (16 * (r & 1)));
-          }
-        }
-        if (g == 0) *reinterpret_cast<uint32_t *>(se + 128) = s4;
       }
       const int st = hb >> 2, i = hb & 3;
-      for (int p = lane; p < ncol * 8; p += 64) {
-        const int e = p >> 3, t = (p >> 1) & 3, half = p & 1;
-        *reinterpret_cast<uint4 *>(hout + (size_t)(beg + e) * G::kBytes + G::data(st, t) + 32 * i + 16 * half) =
-            *reinterpret_cast<const uint4 *>(stage + e * kStage + t * 32 + 16 * half);
-      }
-      for (int p = lane; p < ncol * kTerms; p += 64) {
-        const int e = p / kTerms, t = p % kTerms;
-        hout[(size_t)(beg + e) * G::kBytes + G::scale(st, t) + i] = stage[e * kStage + 128 + t];
+#pragma unroll
+      for (int pass = 0; pass < (kWaveCols + 31) / 32; pass++) {
+        const int e = 32 * pass + (lane >> 1), h = lane & 1;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float4 x = *reinterpret_cast<const float4 *>(stage + min(e, kWaveCols - 1) * 32 + 16 * h + 4 * q);
+          v[4 * q] = x.x;
+          v[4 * q + 1] = x.y;
+          v[4 * q + 2] = x.z;
+          v[4 * q + 3] = x.w;
+        }
+        float m = 0.0f, bad = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+          m = fmaxf(m, fabsf(v[k]));
+          if (!isfinite(v[k])) bad = 1.0f;
+        }
+        m = fmaxf(m, xor_lane<1>(m));
+        bad = fmaxf(bad, xor_lane<1>(bad));
+        uint32_t dq[kGemmTerms][3], sb;
+        split16_fp6(v, m, bad != 0.0f, dq, sb);
+        if (e < nloc) {
+          uint8_t *hr = hout + (size_t)(beg + e0 + e) * G::kBytes;
+#pragma unroll
+          for (int t = 0; t < kGemmTerms; t++) {
+            uint32_t *dst = reinterpret_cast<uint32_t *>(hr + G::half(st, t, i, h));
+            dst[0] = dq[t][0];
+            dst[1] = dq[t][1];
+            dst[2] = dq[t][2];
+          }
+          if (h == 0) {
+#pragma unroll
+            for (int t = 0; t < kGemmTerms; t++) hr[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+          }
+        }
       }
       __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));  // staging reads done before the next h block
     }
@@ -408,7 +493,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
       const int row = (t0 + r) * 16 + 4 * g;
 #pragma unroll
       for (int c = 0; c < CG; c++) {
-        const int e = 16 * c + j;
+        const int e = 16 * (CGW * wc + c) + j;
         if (e >= ncol) continue;
         float4 o;
         o.x = canon_nan(rclamp(acc[r][c][0] + b4.x, -65504.0f, 65504.0f));
@@ -421,15 +506,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   }
 }
 
-template <int MODE, int RT, int CG, int W, int D>
+template <int MODE, int RT, int CGW, int WR, int WC, int D>
 static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
-  using S = GemmShape<RT, CG, W, D>;
+  using S = GemmShape<RT, CGW, WR, WC, D>;
   static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
   a.n_row_blocks = (int)((a.d.rows + S::kRows - 1) / S::kRows);
   const size_t col_tiles = (size_t)a.max_active + (a.n_entries + S::kCols - 1) / S::kCols;
   const size_t blocks = (size_t)a.n_row_blocks * col_tiles;
   if (!blocks) return hipSuccess;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CG, W, D>), dim3((unsigned)blocks), dim3(S::kThreads), 0, s, a);
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D>), dim3((unsigned)blocks), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -440,9 +525,10 @@ template <int MODE>
 static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   const size_t active = std::max<size_t>(1, std::min<size_t>((size_t)a.max_active, a.n_entries));
   const size_t mean = a.n_entries / active;
-  if (mean >= 48) return a.shape == 1 ? launch_gemm_shape<MODE, 8, 4, 4, 2>(a, s) : launch_gemm_shape<MODE, 4, 4, 8, 2>(a, s);
-  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 4, 3>(a, s);
-  return launch_gemm_shape<MODE, 4, 1, 4, 3>(a, s);
+  if (mean >= 48)
+    return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2>(a, s);
+  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3>(a, s);
+  return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
 }
 
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s) {

@@ -48,15 +48,22 @@ struct GemvArgs {
 // fp8 terms per activation value for the block-scaled MFMA paths (device.hpp, split8_fp8).
 constexpr int kTerms = 4;
 
-// Step-major activation record of one row (token or entry) for the grouped GEMM (gemm.hip),
-// rows of up to 4 * kGemmNs 32-value blocks: K-step s holds [term t][128 bytes = blocks 4s..4s+3]
-// followed by [term t][4 scale bytes, byte i = E8M0 of block 4s+i]; blocks past the row are zero.
+// Step-major activation record of one row (token or entry) for the grouped GEMM (gemm.hip):
+// kGemmTerms fp6 (E2M3) terms per value, rows of up to 4 * kGemmNs 32-value blocks. K-step s
+// holds, per term t, 96 bytes in MFMA B-operand order: block 4s + b at 24 b, value u of the block
+// at bits 6u (the 6 dwords lane group b of the fp6 MFMA operand takes: K = 32 b + u); then
+// [term t][4 scale bytes, byte i = E8M0 of block 4s+i] (12 bytes) and 4 pad bytes. Blocks past
+// the row are zero.
 constexpr int kGemmNs = 24;
+constexpr int kGemmTerms = 3;
 struct GemmRec {
-  static constexpr int kStep = kTerms * 128 + kTerms * 4;
+  static constexpr int kTermBytes = 96;
+  static constexpr int kStep = kGemmTerms * kTermBytes + 16;
   static constexpr int kBytes = kGemmNs * kStep;
-  MOE_HD static constexpr int data(int s, int t) { return s * kStep + t * 128; }
-  MOE_HD static constexpr int scale(int s, int t) { return s * kStep + kTerms * 128 + 4 * t; }
+  MOE_HD static constexpr int data(int s, int t) { return s * kStep + t * kTermBytes; }
+  // byte offset of the 12-byte half h (values 16h .. 16h + 15) of block b (0..3) of step s, term t
+  MOE_HD static constexpr int half(int s, int t, int b, int h) { return data(s, t) + 24 * b + 12 * h; }
+  MOE_HD static constexpr int scale(int s, int t) { return s * kStep + kGemmTerms * kTermBytes + 4 * t; }
 };
 
 struct GemmArgs {
