@@ -252,17 +252,78 @@ def run_matvec_bench(args):
     for i in range(args.warmup):
         mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
     disp.synchronize()
+    # the copies back to back in one HIP graph (a matvec is ~0.6 us of HBM traffic, below the
+    # cost of a host launch), replayed for the timed region
+    graph = None
+    if args.graph:
+        check(L.moe_graph_begin(disp.ctx))
+        for i in range(copies):
+            mxfp4_matvec(disp, packed[i], R, C, x, y)
+        g = ctypes.c_void_p()
+        check(L.moe_graph_end(disp.ctx, ctypes.byref(g)))
+        graph = g.value
+        check(L.moe_graph_launch(disp.ctx, graph))
+        disp.synchronize()
+    reps = max(1, args.steps // copies) if graph else 0
+    steps = reps * copies if graph else args.steps
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
+    if graph:
+        for _ in range(reps):
+            check(L.moe_graph_launch(disp.ctx, graph))
+    else:
+        for i in range(steps):
+            mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
     disp.synchronize()
     el = time.perf_counter() - t0
+    if graph:
+        check(L.moe_graph_destroy(graph))
     byts = R * nb * 17 + C * 4 + R * 4
-    return {"metric": "MXFP4 matvec 2880x2880 GB/s", "value": round(byts * args.steps / el / 1e9, 1),
-            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "ms_per_step": round(el * 1e3 / args.steps, 6), "higher_is_better": True,
+    gbs = byts * steps / el / 1e9
+    return {"metric": "MXFP4 matvec 2880x2880 GB/s", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+            "ms_per_step": round(el * 1e3 / steps, 6), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "config1 matvec 2880x2880", "copies": copies}}
+            "config": {"workload": "config1 matvec 2880x2880", "copies": copies,
+                       "graph_replay": bool(graph)},
+            "roofline": {"bound": "hbm", "kernel": "split + k_expert_gemv (per matvec, graph replay)",
+                         "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes_per_launch": byts}}
+
+
+def run_lm_head_bench(args, H, V):
+    """The next row after the MoE path: dispatch_lm_head (moe_dispatch.rs:624-683), logits[V] =
+    W[V, H] x in f32 with the reference's f32 weights (201 088 x 2880 = 2.32 GB), device-resident
+    input and logits."""
+    from silentotithrandousha_amd import DeviceBuffer
+    rng = np.random.default_rng(9)
+    log(f"lm head: {V} x {H} f32 ({V * H * 4 / 1e9:.2f} GB)")
+    w = rng.standard_normal((V, H), dtype=np.float32)
+    w *= np.float32(0.02)
+    disp = GpuMoeDispatcher(H, H, 7.0)
+    disp.init_lm_head(w, V)
+    del w
+    x = DeviceBuffer.from_array(rng.standard_normal(H, dtype=np.float32))
+    y = DeviceBuffer(V * 4)
+    for _ in range(args.warmup):
+        disp.dispatch_lm_head_device(x, V, y)
+    disp.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        disp.dispatch_lm_head_device(x, V, y)
+    disp.synchronize()
+    el = time.perf_counter() - t0
+    byts = V * H * 4 + H * 4 + V * 4
+    gbs = byts * args.steps / el / 1e9
+    disp.close()
+    return {"metric": "LM head f32 GEMV 201088x2880 GB/s", "value": round(gbs, 1), "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(el * 1e3 / args.steps, 6), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (weights N(0,0.02), x N(0,1))",
+            "config": {"workload": "lm head (next row) 201088x2880 f32", "vocab": V, "hidden": H},
+            "roofline": {"bound": "hbm", "kernel": "k_lm_head", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes_per_launch": byts}}
 
 
 def copy_calibration(mib):
@@ -311,7 +372,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None, help="default: per workload")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode1",
-                    choices=["decode1", "decode64", "prefill", "matvec", "decode1_120b", "prefill_120b"])
+                    choices=["decode1", "decode64", "prefill", "matvec", "decode1_120b", "prefill_120b", "lm_head"])
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-graph", dest="graph", action="store_false")
     ap.add_argument("--no-fused", dest="fused", action="store_false",
@@ -328,7 +389,8 @@ def main():
                     help="run one device copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
     dsteps, dwarm = {"decode1": (4800, 480), "decode1_120b": (4800, 480), "matvec": (4800, 480),
-                     "decode64": (960, 96), "prefill": (8, 2), "prefill_120b": (48, 8)}[args.workload]
+                     "decode64": (960, 96), "prefill": (8, 2), "prefill_120b": (48, 8),
+                     "lm_head": (40, 4)}[args.workload]
     args.steps = dsteps if args.steps is None else args.steps
     args.warmup = dwarm if args.warmup is None else args.warmup
     if args.gpus != 1:
@@ -339,6 +401,8 @@ def main():
     H = I = 2880
     if args.workload == "matvec":
         res = run_matvec_bench(args)
+    elif args.workload == "lm_head":
+        res = run_lm_head_bench(args, H, 201088)
     elif args.workload == "decode1":
         res = run_layer_bench(args, H, I, 32, 4, 1, args.layers, "config2 gpt-oss-20b moe layer decode b=1", "decode1")
     elif args.workload == "decode64":

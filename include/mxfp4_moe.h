@@ -173,6 +173,10 @@ int moe_init_lm_head(moe_ctx *ctx, const float *weights, size_t vocab_size);
 /* GpuMoeDispatcher::dispatch_lm_head — moe_dispatch.rs:624-683. logits[vocab] = W input.
  * Returns MOE_ERR_STATE where the reference panics ("call init_lm_head first"). */
 int moe_dispatch_lm_head(moe_ctx *ctx, const float *input, size_t vocab_size, float *logits);
+/* The same with device pointers, enqueued on `stream` (NULL = the context's stream); no
+ * synchronisation (no reference counterpart: the device-resident form of dispatch_lm_head). */
+int moe_dispatch_lm_head_device(moe_ctx *ctx, const float *input, size_t vocab_size, float *logits,
+                                void *stream);
 
 /* ------------------------------------------------------------------ path-level entry points */
 

@@ -24,59 +24,144 @@ namespace moe {
 // ------------------------------------------------------------------ router + top-k
 
 constexpr int kRouteThreads = 1024;
+constexpr int kRouteTokens = 8;  // tokens per block for large batches: the router weights load once per block
 
-template <int KI>
+// Router + top-k for TB tokens per block (block b: tokens TB b .. TB b + TB - 1). x of the tokens
+// is staged in LDS (zero padded to the router chains' length; with xsplit != NULL its bf16
+// hi + lo split is written for the GEMV path); wavefront w computes experts w, w + 16, ... for
+// every token of the block from one load of the expert's weights (router_dot's canonical order
+// per token); then wavefront w runs the top-k of token w (wave_topk_order/weights, k <= 4,
+// E <= 128: block_topk's arithmetic), or for larger k the block runs block_topk per token.
+template <int KI, int TB>
 __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
-  __shared__ float s_logit[kMaxExperts];
+  __shared__ float s_logit[TB][kMaxExperts];
   __shared__ float s_p[kMaxExperts];
-  __shared__ int s_order[kMaxTopK];
-  const int t = blockIdx.x;
+  __shared__ int s_order[TB][kMaxTopK];
+  __shared__ float s_w[TB][kMaxTopK];
+  __shared__ int s_sel[TB];
+  const int t0 = blockIdx.x * TB;
+  const int nt = min(TB, a.T - t0);
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int nw = kRouteThreads / 64;
   const int H = a.H, E = a.E;
   const int nq = ((H + 63) / 64 + 7) / 8;  // uint4 per lane chain
   const int Hp = nq * 8 * 64;
-  const float *x = a.x + (size_t)t * H;
-  extern __shared__ float s_x[];  // Hp floats
-  uint16_t *xs = a.xsplit + (size_t)t * 2 * H;
-  for (int k = threadIdx.x; k < Hp; k += kRouteThreads) {
-    const float v = k < H ? x[k] : 0.0f;
-    s_x[k] = v;
-    if (k < H) {
-      uint16_t hi, lo;
-      split_bf16(v, hi, lo);
-      xs[k] = hi;
-      xs[H + k] = lo;
+  extern __shared__ float s_x[];  // TB * Hp floats
+  for (int tb = 0; tb < nt; tb++) {
+    const float *x = a.x + (size_t)(t0 + tb) * H;
+    uint16_t *xs = a.xsplit ? a.xsplit + (size_t)(t0 + tb) * 2 * H : nullptr;
+    for (int k = threadIdx.x; k < Hp; k += kRouteThreads) {
+      const float v = k < H ? x[k] : 0.0f;
+      s_x[tb * Hp + k] = v;
+      if (xs && k < H) {
+        uint16_t hi, lo;
+        split_bf16(v, hi, lo);
+        xs[k] = hi;
+        xs[H + k] = lo;
+      }
     }
   }
   __syncthreads();
   for (int e = wv; e < E; e += nw) {
-    const float p = router_dot<KI>(a.w + (size_t)e * nq * 512, s_x, nq, lane);
-    if (lane == 0) s_logit[e] = canon_nan(p + a.bias[e]);
+    const uint16_t *w_e = a.w + (size_t)e * nq * 512;
+    if (KI > 0) {
+      uint4 v[KI > 0 ? KI : 1];
+      const uint4 *wq = reinterpret_cast<const uint4 *>(w_e) + lane;
+#pragma unroll
+      for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
+#pragma unroll
+      for (int tb = 0; tb < TB; tb++) {
+        if (tb < nt) {
+          const float *xt = s_x + tb * Hp;
+          float p = 0.0f;
+#pragma unroll
+          for (int q = 0; q < KI; q++) {
+            const uint32_t u[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+              const uint16_t bw = (uint16_t)(u[h >> 1] >> (16 * (h & 1)));
+              p = __builtin_fmaf(bf16_to_f32(bw), xt[lane + 64 * (8 * q + h)], p);
+            }
+          }
+          p = wave_sum_xor(p);
+          if (lane == 0) s_logit[tb][e] = canon_nan(p + a.bias[e]);
+        }
+      }
+    } else {
+      for (int tb = 0; tb < nt; tb++) {
+        const float p = router_dot<0>(w_e, s_x + tb * Hp, nq, lane);
+        if (lane == 0) s_logit[tb][e] = canon_nan(p + a.bias[e]);
+      }
+    }
   }
   __syncthreads();
 
-  for (int e = threadIdx.x; e < E; e += kRouteThreads) a.logits[(size_t)t * E + e] = s_logit[e];
-  __shared__ float s_w[kMaxTopK];
-  __shared__ int s_sel;
   const TopkCfg c{E, a.k, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
-  block_topk(c, s_logit, s_p, s_order, s_w, &s_sel);
-  if (threadIdx.x < a.k) {
-    const size_t o = (size_t)t * a.k + threadIdx.x;
-    a.idx[o] = s_order[threadIdx.x];
-    a.wts[o] = s_w[threadIdx.x];
+  const bool per_wave = a.k <= 4 && E <= 128;
+  if (per_wave) {
+    static_assert(TB <= kRouteThreads / 64, "a wavefront per token");
+    if (wv < nt) {
+      const int tb = wv, t = t0 + tb;
+      float l[2];
+      l[0] = lane < E ? s_logit[tb][lane] : 0.0f;
+      l[1] = lane + 64 < E ? s_logit[tb][lane + 64] : 0.0f;
+      if (lane < E) a.logits[(size_t)t * E + lane] = l[0];
+      if (lane + 64 < E) a.logits[(size_t)t * E + lane + 64] = l[1];
+      int ord[4];
+      if (E <= 64) {
+        const float l1[1] = {l[0]};
+        wave_topk_order<1>(c, l1, lane, ord);
+        wave_topk_weights<1>(c, l1, lane, ord, true, s_order[tb], s_w[tb], &s_sel[tb]);
+      } else {
+        wave_topk_order<2>(c, l, lane, ord);
+        wave_topk_weights<2>(c, l, lane, ord, true, s_order[tb], s_w[tb], &s_sel[tb]);
+      }
+      if (lane < a.k) {
+        const size_t o = (size_t)t * a.k + lane;
+        a.idx[o] = s_order[tb][lane];
+        a.wts[o] = s_w[tb][lane];
+      }
+    }
+  } else {
+    for (int tb = 0; tb < nt; tb++) {
+      const int t = t0 + tb;
+      for (int e = threadIdx.x; e < E; e += kRouteThreads) a.logits[(size_t)t * E + e] = s_logit[tb][e];
+      block_topk(c, s_logit[tb], s_p, s_order[tb], s_w[tb], &s_sel[tb]);
+      if (threadIdx.x < a.k) {
+        const size_t o = (size_t)t * a.k + threadIdx.x;
+        a.idx[o] = s_order[tb][threadIdx.x];
+        a.wts[o] = s_w[tb][threadIdx.x];
+      }
+    }
   }
-  if (a.fuse_bucket && threadIdx.x == 0) {  // single token: the expert list is the slot list
-    const int sel = s_sel;
+  if (a.fuse_bucket && threadIdx.x == 0) {  // single token (TB = 1): the expert list is the slot list
+    const int sel = s_sel[0];
     *a.n_active = sel;
-    for (int s = 0; s < sel; s++) {
-      a.active_ids[s] = s_order[s];
-      a.active_off[s] = s;
-      a.entry_src[s] = 0;
+    for (int s2 = 0; s2 < sel; s2++) {
+      a.active_ids[s2] = s_order[0][s2];
+      a.active_off[s2] = s2;
+      a.entry_src[s2] = 0;
     }
     a.active_off[sel] = sel;
-    for (int s = 0; s < a.k; s++) a.pos[s] = s < sel ? s : -1;
+    for (int s2 = 0; s2 < a.k; s2++) a.pos[s2] = s2 < sel ? s2 : -1;
+  }
+}
+
+template <int KI>
+static void launch_route_ki(const RouteArgs &a, int nq, hipStream_t s) {
+  const size_t hp = (size_t)nq * 8 * 64 * sizeof(float);
+  if (a.T >= 2048 && kRouteTokens * hp <= 144 * 1024) {
+    static bool attr = false;  // TB tokens of x may exceed the default 64 KB of dynamic LDS
+    if (!attr) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_route<KI, kRouteTokens>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kRouteTokens * hp));
+      attr = true;
+    }
+    hipLaunchKernelGGL((k_route<KI, kRouteTokens>), dim3((unsigned)((a.T + kRouteTokens - 1) / kRouteTokens)),
+                       dim3(kRouteThreads), kRouteTokens * hp, s, a);
+  } else {
+    hipLaunchKernelGGL((k_route<KI, 1>), dim3((unsigned)a.T), dim3(kRouteThreads), hp, s, a);
   }
 }
 
@@ -87,12 +172,11 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
   const int nq = ((a.H + 63) / 64 + 7) / 8;
   const size_t lds = (size_t)nq * 8 * 64 * sizeof(float);
   if (lds > 65536) return hipErrorInvalidValue;
-  const dim3 g(a.T), b(kRouteThreads);
   switch (nq) {  // 2880 -> 45 chain terms -> 6 loads per lane
-    case 1: hipLaunchKernelGGL(k_route<1>, g, b, lds, s, a); break;
-    case 2: hipLaunchKernelGGL(k_route<2>, g, b, lds, s, a); break;
-    case 6: hipLaunchKernelGGL(k_route<6>, g, b, lds, s, a); break;
-    default: hipLaunchKernelGGL(k_route<0>, g, b, lds, s, a); break;
+    case 1: launch_route_ki<1>(a, nq, s); break;
+    case 2: launch_route_ki<2>(a, nq, s); break;
+    case 6: launch_route_ki<6>(a, nq, s); break;
+    default: launch_route_ki<0>(a, nq, s); break;
   }
   return hipGetLastError();
 }

@@ -112,7 +112,8 @@ struct moe_ctx {
   Work w{};
   DevBuf scratch_experts;  // dispatch_expert / batched: experts uploaded per call
   DevBuf stage;            // checkpoint-layout staging for uploads
-  DevBuf mv_split;         // matvec x split
+  DevBuf mv_split;         // matvec: [one-entry expert list | x split]
+  void *mv_list_at = nullptr;  // mv_split.p when its list was written
   DevBuf lm_w, lm_x, lm_y;
   size_t lm_vocab = 0;
   bool timing = false;
@@ -448,7 +449,13 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
   ra.logits = c->w.logits;
   ra.idx = c->w.idx;
   ra.wts = c->w.wts;
-  ra.xsplit = c->w.xsplit;
+  // the grouped GEMM (16- to 64-entry column tiles) pays off once experts average a few
+  // entries; smaller batches stream each weight tile through the GEMV kernels, which read the
+  // bf16 hi + lo split of x that the router writes
+  const bool use_gemm = c->batch_gemm && T > 1 && (c->batch_gemm == 2 || T * k >= 4 * E) &&
+                        c->L.gu.ns <= (uint32_t)kGemmNs && c->L.dn.ns <= (uint32_t)kGemmNs &&
+                        (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  ra.xsplit = use_gemm ? nullptr : c->w.xsplit;
   ra.fuse_bucket = T == 1;
   ra.n_active = c->w.n_active;
   ra.active_ids = c->w.active_ids;
@@ -462,11 +469,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
                            c->w.active_off, c->w.entry_src, c->w.pos, s);
     }));
   const int max_active = (int)std::min(E, T * k);
-  // the grouped GEMM (16- to 64-entry column tiles) pays off once experts average a few
-  // entries; smaller batches stream each weight tile through the GEMV kernels
-  if (c->batch_gemm && T > 1 && (c->batch_gemm == 2 || T * k >= 4 * E) && c->L.gu.ns <= (uint32_t)kGemmNs &&
-      c->L.dn.ns <= (uint32_t)kGemmNs &&
-      (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+  if (use_gemm) {
     const size_t N = T * k;
     RETURN_IF(timed(c, K_SPLIT, s, [&] { return launch_split_rows(x, T, c->H, c->w.xrec, s); }));
     GemmArgs ga{};
@@ -792,6 +795,16 @@ int moe_dispatch_lm_head(moe_ctx *c, const float *input, size_t vocab, float *lo
   return MOE_OK;
 }
 
+int moe_dispatch_lm_head_device(moe_ctx *c, const float *input, size_t vocab, float *logits, void *stream) {
+  RETURN_IF(use_dev(c));
+  if (!c->lm_vocab) return fail(MOE_ERR_STATE, "call init_lm_head first");
+  if (!input || !logits) return fail(MOE_ERR_INVALID, "null input or logits");
+  if (vocab > c->lm_vocab)
+    return fail(MOE_ERR_INVALID, "vocab_size %zu exceeds the initialised %zu", vocab, c->lm_vocab);
+  HIP_TRY(launch_lm_head((const float *)c->lm_w.p, input, vocab, c->H, logits, pick(c, stream)));
+  return MOE_OK;
+}
+
 int moe_router_topk(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k, int32_t *idx,
                     float *weights, float *logits) {
   RETURN_IF(use_dev(c));
@@ -819,7 +832,7 @@ int moe_router_topk(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k
   ra.logits = c->w.logits;
   ra.idx = c->w.idx;
   ra.wts = c->w.wts;
-  ra.xsplit = c->w.xsplit;
+  ra.xsplit = nullptr;
   ra.fuse_bucket = 0;
   HIP_TRY(launch_route(ra, c->stream));
   HIP_TRY(hipMemcpyAsync(idx, c->w.idx, T * k * 4, hipMemcpyDeviceToHost, c->stream));
@@ -892,12 +905,17 @@ int moe_mxfp4_matvec_device(moe_ctx *c, const uint8_t *packed, size_t rows, size
     return fail(MOE_ERR_INVALID, "rows %zu must be a multiple of 16 and cols %zu of 32", rows, cols);
   hipStream_t s = pick(c, stream);
   RETURN_IF(ensure_work(c, 1, 1, 1));
-  RETURN_IF(c->mv_split.ensure(al(cols * 2 * 2) + 256));
-  uint16_t *xs = (uint16_t *)c->mv_split.p;
-  int32_t *lists = (int32_t *)((char *)c->mv_split.p + al(cols * 2 * 2));
-  // n_active, active_ids[0], active_off[0..1], entry_src[0]
-  static const int32_t list[5] = {1, 0, 0, 1, 0};
-  HIP_TRY(hipMemcpyAsync(lists, list, sizeof(list), hipMemcpyHostToDevice, s));
+  const size_t cap0 = c->mv_split.cap;
+  RETURN_IF(c->mv_split.ensure(256 + al(cols * 2 * 2)));
+  if (c->mv_split.cap != cap0) c->mv_list_at = nullptr;  // a new allocation holds no list
+  int32_t *lists = (int32_t *)c->mv_split.p;
+  uint16_t *xs = (uint16_t *)((char *)c->mv_split.p + 256);
+  if (c->mv_list_at != c->mv_split.p) {  // once per buffer: the one-entry expert list
+    // n_active, active_ids[0], active_off[0..1], entry_src[0]
+    static const int32_t list[5] = {1, 0, 0, 1, 0};
+    HIP_TRY(hipMemcpyAsync(lists, list, sizeof(list), hipMemcpyHostToDevice, s));
+    c->mv_list_at = c->mv_split.p;
+  }
   HIP_TRY(launch_split(x, 1, cols, xs, s));
   GemvArgs a{};
   a.base = packed;

@@ -20,6 +20,11 @@ def _c(a, dt):
     return np.ascontiguousarray(a, dtype=dt)
 
 
+def _dp(b):
+    """Device pointer of a DeviceBuffer (or an int address)."""
+    return ctypes.c_void_p(b.ptr if hasattr(b, "ptr") else int(b))
+
+
 class DeviceBuffer:
     """A device allocation made through moe_device_alloc (freed on close / GC)."""
 
@@ -195,6 +200,10 @@ class GpuMoeDispatcher:
         y = np.empty(vocab_size, np.float32)
         check(lib().moe_dispatch_lm_head(self._ctx, _p(_c(x, np.float32)), vocab_size, _p(y)))
         return y
+
+    def dispatch_lm_head_device(self, x_dev, vocab_size, logits_dev, stream=None):
+        """Device pointers (DeviceBuffer or int), enqueued without synchronisation."""
+        check(lib().moe_dispatch_lm_head_device(self._ctx, _dp(x_dev), vocab_size, _dp(logits_dev), stream))
 
     # ---- path level
     def router_topk(self, layer, x, top_k, want_logits=False, n_experts=None):

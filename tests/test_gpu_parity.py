@@ -161,6 +161,33 @@ def test_matvec_edge_scales(orc):
     d.close()
 
 
+# ---------------------------------------------------------------- LM head
+
+def test_lm_head_host_and_device():
+    """dispatch_lm_head (moe_dispatch.rs:624-683): logits = W x in f32, against a float64 dot
+    (the kernel sums 64 lane-strided fused partial sums then a xor butterfly; tolerance 1e-5
+    relative L2), and the device-pointer form gives the same bits; a vocab past the initialised
+    one is refused."""
+    from silentotithrandousha_amd import DeviceBuffer
+    from silentotithrandousha_amd._ffi import MoeError
+    H, V = 2880, 1000
+    rng = np.random.default_rng(60)
+    w = (rng.standard_normal((V, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    d = GpuMoeDispatcher(H, H, 7.0)
+    d.init_lm_head(w, V)
+    got = d.dispatch_lm_head(x, V)
+    want = w.astype(np.float64) @ x.astype(np.float64)
+    assert rel_l2(got, want) < 1e-5
+    xd, yd = DeviceBuffer.from_array(x), DeviceBuffer(V * 4)
+    d.dispatch_lm_head_device(xd, V - 7, yd)
+    d.synchronize()
+    assert np.array_equal(yd.download(np.float32, (V,))[:V - 7], got[:V - 7])
+    with pytest.raises(MoeError):
+        d.dispatch_lm_head(x, V + 1)
+    d.close()
+
+
 # ---------------------------------------------------------------- router + top-k
 
 def test_router_logits_and_topk_bit_exact(orc, disp20, layer20):
