@@ -9,8 +9,8 @@
 //   [k*NGS, +H/16)    down blocks: one 16-row output tile, wavefront = slot; bias, clamp and the
 //                     slot-ordered combine into y.
 // Router: wavefront w of the grid (w < E) computes logit w in the canonical order (same
-// arithmetic as k_route) and writes it, tagged, into kReplicas copies of the logit vector;
-// block b reads copy b % kReplicas and runs the top-k itself (identical arithmetic everywhere,
+// arithmetic as k_route) and writes it, tagged, into nrep = min(kReplicas, blocks) copies of the
+// logit vector; block b reads copy b % nrep and runs the top-k itself (identical arithmetic everywhere,
 // so every block selects the same experts and weights). Block 0 also writes the logits,
 // indices and weights.
 // Matmuls: v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as stored (no decode
@@ -22,20 +22,24 @@
 // (logits, h terms, flags) is written with agent-scope relaxed atomic stores (write-through)
 // and read with agent-scope loads that bypass the L2 (relaxed atomic loads, or LDS-direct
 // loads with the same cache policy); a writer waits for its stores to complete (s_waitcnt)
-// before it raises the flag that publishes them. No address is polled by more than
-// ceil(blocks / kReplicas) blocks.
+// before it raises the flag that publishes them.
 //   * logits: every block adds 1 to its copy's counter after reading the copy; the block that
-//     brings it to the copy's reader count clears the copy and the counter;
-//   * h of slot s: every gate_up block of slot s adds 1 to counter s after its h stores are
-//     complete; the block that brings it to NGS resets it to 0 and raises h_ready[s] in every
-//     down block's mailbox; a down block clears its mailbox when done.
-// So counters, copies and mailboxes are zero again when the kernel ends and the next launch
-// (or graph replay) starts clean. The blocks that wait on gate_up blocks have higher indices, and
-// workgroups are dispatched in index order, so waiting blocks never hold back the blocks they
-// wait for; the router wavefronts are in the lowest blocks. Every wait is bounded by
-// `spin_limit` polls; a wait that runs out sets the sticky error word, the block writes NaN to
-// its outputs, and later launches return NaN at once until the host clears the error (it
-// reports it at its next synchronisation).
+//     brings it to the copy's reader count clears the copy and the counter and advances the
+//     copy's launch number (epoch). Every copy advances exactly once per launch, so all copies
+//     hold the same epoch when a launch starts, and a block reads its copy's epoch before its
+//     own count can let the copy advance;
+//   * h block i of slot s: once its h terms are complete, the gate_up block stores epoch + 1
+//     into flag (s, i) of each of kFlagReplicas replicas; down wavefront s waits until the NGS
+//     flags of slot s in its replica read epoch + 1. Flags are never cleared: a flag from an
+//     earlier launch holds a smaller number.
+// So no atomic and no second hop sits between the last h store and the down blocks. Copies and
+// counters are zero again when the kernel ends. The blocks that wait on gate_up blocks have
+// higher indices, and workgroups are dispatched in index order, so waiting blocks never hold
+// back the blocks they wait for; the router wavefronts are in the lowest blocks. Every wait is
+// bounded by `spin_limit` polls; a wait that runs out sets the sticky error word, the block
+// writes NaN to its outputs, and later launches return NaN at once until the host clears the
+// error (it reports it at its next synchronisation and zeroes the signalling area, epochs
+// included).
 #include <algorithm>
 
 #include "device.hpp"
@@ -71,23 +75,25 @@ constexpr int kLayerMaxE = 128;
 struct LogitCopy {               // kCopyBytes apart
   uint64_t logit[kLayerMaxE];    // (1 << 32) | f32 bits of logit e, 0 when empty
   uint32_t readers_done;
+  uint32_t epoch;                // launches completed
 };
 constexpr size_t kCopyBytes = 1088;
 static_assert(sizeof(LogitCopy) <= kCopyBytes, "copy layout");
 
-struct LayerMailbox {    // one per down block, 64 bytes apart
-  uint32_t h_ready[4];   // slot s's h terms are complete
-};
+constexpr int kFlagReplicas = 4;
+constexpr int kMaxHBlocks = 128;  // h blocks of 32 per slot (K <= 3072 -> 96)
 
 struct LayerSyncHdr {
   uint32_t err;          // sticky: a bounded wait ran out
   uint32_t pad0[63];
-  uint32_t cnt[4][64];   // gate_up blocks done per slot (256 bytes apart)
+  uint32_t hflag[kFlagReplicas][4][kMaxHBlocks];  // epoch + 1: h block i of slot s is published
 };
 
-size_t layer_sync_bytes(int max_blocks) {
-  return sizeof(LayerSyncHdr) + kReplicas * kCopyBytes + (size_t)max_blocks * 64;
-}
+size_t layer_sync_bytes() { return sizeof(LayerSyncHdr) + kReplicas * kCopyBytes; }
+
+// h records of the slots, in HBM and in a down block's LDS: Act::kBytes apart (a multiple of 16,
+// so a record is whole 16-byte lane pieces of LDS-direct loads).
+static_assert(Act::kBytes % 16 == 0, "h record size");
 
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -112,10 +118,6 @@ __device__ __forceinline__ LogitCopy *logit_copy(void *sync, int r) {
   return reinterpret_cast<LogitCopy *>(reinterpret_cast<uint8_t *>(sync) + sizeof(LayerSyncHdr) +
                                        (size_t)r * kCopyBytes);
 }
-__device__ __forceinline__ LayerMailbox *mailbox(void *sync, int d) {
-  return reinterpret_cast<LayerMailbox *>(reinterpret_cast<uint8_t *>(sync) + sizeof(LayerSyncHdr) +
-                                          kReplicas * kCopyBytes + (size_t)d * 64);
-}
 
 // Logit of expert e in the canonical order (router_compute's arithmetic for one expert);
 // every lane returns it. xr[i] = x[lane + 64 i], zero past H.
@@ -138,20 +140,30 @@ __device__ __forceinline__ float router_logit(const uint16_t *rw, const float *r
   return canon_nan(wave_sum_xor(p) + rb[e]);
 }
 
-// Wavefront 0 of a block: wait for the E tagged logits in copy `cp`; logit 64 q + lane in l[q].
-// Returns false when the wait ran out.
-__device__ __forceinline__ bool await_logits(LogitCopy *cp, int E, uint32_t spin_limit, int lane, float (&l)[2]) {
+// Wavefront 0 of a block: wait for the E tagged logits in copy `cp`; logit 64 q + lane in l[q],
+// the copy's epoch in *ep (read in the same polls, and complete before this returns, so before
+// the block's count on the copy is issued). Returns false when the wait ran out.
+__device__ __forceinline__ bool await_logits(LogitCopy *cp, int E, uint32_t spin_limit, int lane, float (&l)[2],
+                                             uint32_t *ep) {
   uint64_t v0 = 0, v1 = 0;
+  uint32_t e = 0;
+  bool ok = true;
   for (uint32_t n = 0;; n++) {
+    e = ld_agent(&cp->epoch);
     v0 = lane < E ? ld_agent64(&cp->logit[lane]) : (1ull << 32);
     v1 = lane + 64 < E ? ld_agent64(&cp->logit[lane + 64]) : (1ull << 32);
     if (__all((v0 >> 32) == 1ull && (v1 >> 32) == 1ull)) break;
-    if (n >= spin_limit) return false;
+    if (n >= spin_limit) {
+      ok = false;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
+  *ep = (uint32_t)__builtin_amdgcn_readfirstlane((int)e);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   l[0] = __uint_as_float((uint32_t)v0);
   l[1] = __uint_as_float((uint32_t)v1);
-  return true;
+  return ok;
 }
 
 // The routing on the critical path: the winners -> s_order, and the kept count -> *s_sel. With
@@ -189,9 +201,9 @@ __device__ __forceinline__ void route_weights(const TopkCfg &c, const float (&l)
 }
 
 // Wavefront 0, after its routing read: count this block as a reader of copy `cp`; the last of
-// its `readers` clears it for the next launch. Two halves, so that the atomic's round trip
-// overlaps the weight loads issued between them: release_begin returns the count before ours
-// (lane 0), release_end acts on it.
+// its `readers` clears it and advances its epoch for the next launch. Two halves, so that the
+// atomic's round trip overlaps the weight loads issued between them: release_begin returns the
+// count before ours (lane 0), release_end acts on it.
 __device__ __forceinline__ uint32_t release_begin(LogitCopy *cp, int lane) {
   uint32_t old = 0;
   if (lane == 0)
@@ -199,12 +211,17 @@ __device__ __forceinline__ uint32_t release_begin(LogitCopy *cp, int lane) {
   return old;
 }
 
-__device__ __forceinline__ void release_end(LogitCopy *cp, uint32_t old, int readers, int E, int lane) {
+// With fewer blocks than kReplicas only copies 0 .. nrep-1 are written and read; the last
+// reader of copy r also advances the epochs of the unused copies r + nrep, r + 2 nrep, ...
+__device__ __forceinline__ void release_end(void *sync, int r, int nrep, uint32_t old, int readers, int E,
+                                            uint32_t ep, int lane) {
   old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
   if (old == (uint32_t)readers - 1) {
+    LogitCopy *cp = logit_copy(sync, r);
     if (lane < E) st_agent64(&cp->logit[lane], 0ull);
     if (lane + 64 < E) st_agent64(&cp->logit[lane + 64], 0ull);
     if (lane == 0) st_agent(&cp->readers_done, 0u);
+    if (lane < kReplicas && lane % nrep == r) st_agent(&logit_copy(sync, lane)->epoch, ep + 1);
   }
 }
 
@@ -215,6 +232,8 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   __shared__ float s_w[kMaxTopK];
   __shared__ int s_sel;
   __shared__ int s_flag;
+  __shared__ uint32_t s_ep;
+  __shared__ int s_wfail[4];
   __shared__ float s_h32[32];
   __shared__ float s_o[4][16];
 
@@ -224,8 +243,10 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   const int NGS = la.n_gu_per_slot;
   const int n_gu = K * NGS, n_blk = n_gu + la.n_dn;
   LayerSyncHdr *hdr = reinterpret_cast<LayerSyncHdr *>(la.sync);
-  LogitCopy *cp = logit_copy(la.sync, b % kReplicas);
-  const int readers = n_blk / kReplicas + ((b % kReplicas) < (n_blk % kReplicas) ? 1 : 0);
+  const int nrep = n_blk < kReplicas ? n_blk : kReplicas;  // logit copies in use
+  const int rc = b % nrep;
+  LogitCopy *cp = logit_copy(la.sync, rc);
+  const int readers = n_blk / nrep + (rc < n_blk % nrep ? 1 : 0);
   const uint32_t err0 = ld_agent(&hdr->err);  // tested late: the load overlaps the router
   const TopkCfg tc{E, K, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
   constexpr int XI = 8 * RNQ;  // x values per lane of the router chain
@@ -243,7 +264,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
       if (lane + 64 * i >= H) xr[i] = 0.0f;
     for (int e = gw; e < E; e += n_blk * kLayerWaves) {
       const float lg = router_logit<RNQ>(a.rw, a.rb, xr, e, lane);
-      if (lane < kReplicas) st_agent64(&logit_copy(la.sync, lane)->logit[e], (1ull << 32) | __float_as_uint(lg));
+      if (lane < nrep) st_agent64(&logit_copy(la.sync, lane)->logit[e], (1ull << 32) | __float_as_uint(lg));
     }
   }
 
@@ -276,11 +297,11 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
     MOE_TRACE(1);
     // 2. routing
-    uint32_t rel = 0;
+    uint32_t rel = 0, ep = 0;
     float l[2];
     int ord[4];
     if (wv == 0) {
-      const bool ok = await_logits(cp, E, la.spin_limit, lane, l);
+      const bool ok = await_logits(cp, E, la.spin_limit, lane, l, &ep);
       if (ok) route_order(tc, l, lane, ord, s_order, s_w, &s_sel);
       rel = release_begin(cp, lane);
       if (lane == 0) s_flag = !ok;
@@ -292,7 +313,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     const int slot = b / NGS;
     if (timeout || err0 || slot >= sel) {  // uniform over the block; no barrier follows
       if (timeout && tid == 0) st_agent(&hdr->err, 1u);
-      if (wv == 0) release_end(cp, rel, readers, E, lane);
+      if (wv == 0) release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
       return;
     }
     // 3. this wavefront's gate_up tile (rows 16t .. 16t+15 -> h[8t, 8t+8)); bias with it
@@ -316,7 +337,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     const f32x4 acc = tile_mfma_f8<kLayerNs>(r, s_x, bsw, lane);
     float v[4];
     sum_terms(acc, v);
-    if (wv == 0) release_end(cp, rel, readers, E, lane);
+    if (wv == 0) release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
     MOE_TRACE(3);
     if (j == 0) {
       s_h32[wv * 8 + 2 * g] = swiglu(v[0] + bias.x, v[1] + bias.y, a.limit);
@@ -324,7 +345,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
     __syncthreads();
     // 4. h[32 hb, 32 hb + 32) as kTerms fp8 terms -> this slot's h record (lanes 0..3 of
-    //    wavefront 0 hold 8 values each)
+    //    wavefront 0 hold 8 values each); once the stores are complete, the flags
     if (wv == 0) {
       if (lane < 4) {
         float hv[8];
@@ -348,40 +369,31 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
         }
       }
       wait_mem();
-    }
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(&hdr->cnt[slot][0], 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      s_flag = old == (uint32_t)NGS - 1;
-    }
-    __syncthreads();
-    MOE_TRACE(4);
-    if (s_flag) {  // the last gate_up block of this slot: its h terms are complete
-      if (tid == 0) st_agent(&hdr->cnt[slot][0], 0u);
-      for (int d = tid; d < la.n_dn; d += kLayerThreads) st_agent(&mailbox(la.sync, d)->h_ready[slot], 1u);
-      MOE_TRACE(5);
+      if (lane < kFlagReplicas) st_agent(&hdr->hflag[lane][slot][hb], ep + 1);
+      MOE_TRACE(4);
     }
     return;
   }
 
   // ================================================================== down block
   const int t = b - n_gu, slot = wv;
-  LayerMailbox *my = mailbox(la.sync, t);
   uint8_t *s_h = reinterpret_cast<uint8_t *>(smem);  // [slot] activation records of h
   // 1. routing
-  uint32_t rel = 0;
+  uint32_t rel = 0, ep = 0;
   float l[2];
   int ord[4];
   if (wv == 0) {
-    const bool ok = await_logits(cp, E, la.spin_limit, lane, l);
+    const bool ok = await_logits(cp, E, la.spin_limit, lane, l, &ep);
     if (ok) route_order(tc, l, lane, ord, s_order, s_w, &s_sel);
     rel = release_begin(cp, lane);
-    if (lane == 0) s_flag = !ok || err0;
+    if (lane == 0) {
+      s_flag = !ok || err0;
+      s_ep = ep;
+    }
   }
   __syncthreads();
   MOE_TRACE(1);
-  bool timeout = s_flag;
+  const bool timeout = s_flag;
   const int sel = timeout ? 0 : s_sel;
   const bool ok = slot < sel && slot < K;
   const uint8_t *rec = a.base + (size_t)(ok ? s_order[slot] : 0) * a.stride;
@@ -390,39 +402,46 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   tile_load<kLayerNs>(r, rec + a.dn_off, a.dn, ok ? t : 0, ok, lane);
   const float4 bias = reinterpret_cast<const float4 *>(rec + a.dnb_off)[(ok ? t : 0) * 4 + g];
   if (wv == 0) {
-    release_end(cp, rel, readers, E, lane);
-    if (!timeout) route_weights(tc, l, lane, ord, s_order, s_w, &s_sel);  // read after the h wait's barrier
+    release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
+    if (!timeout) route_weights(tc, l, lane, ord, s_order, s_w, &s_sel);  // read after the combine's barrier
   }
-  // 3. wait for h of the kept slots
-  if (tid == 0 && !timeout) {
-    for (int s = 0; s < sel && !timeout; s++) {
-      for (uint32_t n = 0;; n++) {
-        if (ld_agent(&my->h_ready[s])) break;
-        if (n >= la.spin_limit) {
-          timeout = true;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
+  // 3. wavefront `slot`: wait for the NGS h blocks of its slot, then bring the slot's h record
+  //    into LDS, 1 KB per instruction, straight into LDS (the last instruction only on the lanes
+  //    inside the record, so no byte of a neighbour's record is written)
+  bool wfail = false;
+  if (ok) {
+    const uint32_t want = s_ep + 1;
+    const uint32_t *f = hdr->hflag[t % kFlagReplicas][slot];
+    for (uint32_t n = 0;; n++) {
+      const bool d0 = lane >= NGS || ld_agent(f + lane) == want;
+      const bool d1 = lane + 64 >= NGS || ld_agent(f + lane + 64) == want;
+      if (__all(d0 && d1)) break;
+      if (n >= la.spin_limit) {
+        wfail = true;
+        break;
       }
+      __builtin_amdgcn_s_sleep(1);
     }
-    s_flag = timeout;
+    MOE_TRACE(2);
+    if (!wfail) {
+      const uint8_t *src = la.hterm + (size_t)slot * Act::kBytes;
+      uint8_t *dst = s_h + (size_t)slot * Act::kBytes;
+#pragma unroll
+      for (int cix = 0; cix < Act::kBytes / 1024; cix++)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src + (size_t)cix * 1024) + lane,
+                                         (__attribute__((address_space(3))) void *)(dst + (size_t)cix * 1024),
+                                         16, 0, 16);
+      constexpr int kTail = Act::kBytes % 1024;
+      if (kTail && 16 * lane < kTail)
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const uint4 *>(src + (size_t)(Act::kBytes - kTail)) + lane,
+            (__attribute__((address_space(3))) void *)(dst + (size_t)(Act::kBytes - kTail)), 16, 0, 16);
+      wait_mem();
+    }
+    MOE_TRACE(3);
   }
-  __syncthreads();
-  MOE_TRACE(2);
-  timeout = s_flag;
-  // 4. h records of the kept slots -> LDS, 1 KB per wavefront instruction, straight into LDS
-  //    (the buffer and the LDS area extend 1 KB past the last record for the rounding)
-  if (!timeout) {
-    const int nchunk = (sel * Act::kBytes + 1023) / 1024;
-    for (int cix = wv; cix < nchunk; cix += kLayerWaves)
-      __builtin_amdgcn_global_load_lds(
-          reinterpret_cast<const uint4 *>(la.hterm + (size_t)cix * 1024) + lane,
-          (__attribute__((address_space(3))) void *)(s_h + (size_t)cix * 1024), 16, 0, 16);
-    wait_mem();
-  }
-  __syncthreads();
-  MOE_TRACE(3);
-  if (ok && !timeout) {
+  if (lane == 0) s_wfail[wv] = wfail;
+  if (ok && !wfail) {
     const uint8_t *hrec = s_h + (size_t)slot * Act::kBytes;
     uint32_t bsw[kLayerNq];
     load_bsw<kLayerNs>(hrec, bsw, lane);
@@ -437,9 +456,10 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
   }
   __syncthreads();
+  const bool failed = timeout || s_wfail[0] || s_wfail[1] || s_wfail[2] || s_wfail[3];
   if (tid < 16) {  // session.rs:974-980: y = 0; y += w_s * out_s in slot order
     float y = 0.0f;
-    if (timeout) {
+    if (failed) {
       y = __uint_as_float(0x7FC00000u);
     } else {
       for (int s = 0; s < 4 && s < K; s++)
@@ -448,13 +468,10 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     a.y[t * 16 + tid] = canon_nan(y);
   }
   MOE_TRACE(4);
-  if (tid == 0) {
-    if (timeout) st_agent(&hdr->err, 1u);
-    for (int s = 0; s < 4; s++) st_agent(&my->h_ready[s], 0u);
-  }
+  if (tid == 0 && failed) st_agent(&hdr->err, 1u);
 }
 
-size_t decode_layer_lds(const LayerArgs &) { return (size_t)4 * Act::kBytes + 1024; }
+size_t decode_layer_lds(const LayerArgs &) { return (size_t)4 * Act::kBytes; }
 
 // Derived geometry of the one-launch kernel for la.d (the host fills la.d, sync, hterm and
 // spin_limit).
@@ -463,14 +480,14 @@ void layer_geometry(LayerArgs &la) {
   la.n_dn = (int)la.d.dn.tiles;
 }
 
-size_t layer_hterm_bytes() { return (size_t)4 * Act::kBytes + 1024; }
+size_t layer_hterm_bytes() { return (size_t)4 * Act::kBytes; }
 
 bool decode_layer_supported(const LayerArgs &la) {
   const DecodeArgs &a = la.d;
   return a.k >= 1 && a.k <= 4 && a.E >= 1 && a.E <= kLayerMaxE && a.k <= a.E && a.rnq >= 1 && a.rnq <= 6 &&
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          a.gu.ns <= (uint32_t)kLayerNs && a.dn.ns <= (uint32_t)kLayerNs && a.H % 32 == 0 &&
-         a.I % 32 == 0 && a.gu.tiles % 4 == 0 &&
+         a.I % 32 == 0 && a.gu.tiles % 4 == 0 && a.gu.tiles / 4 <= (uint32_t)kMaxHBlocks &&
          a.k * la.n_gu_per_slot + la.n_dn <= kLayerMaxBlocks;
 }
 

@@ -105,18 +105,19 @@ struct DecodeArgs {
 };
 
 // One-launch single-token layer (decode_layer.hip): DecodeArgs plus the cross-block
-// signalling area (zeroed once at context creation; it returns to zero after every launch)
-// and the h-terms buffer (zeroed once; padding blocks stay zero).
+// signalling area (zeroed once at context creation and after a reported error; its logit copies
+// return to zero after every launch, its launch numbers and h flags only advance) and the
+// h-terms buffer (zeroed once; padding blocks stay zero).
 constexpr int kLayerMaxBlocks = 1024;
 struct LayerArgs {
   DecodeArgs d;
-  void *sync;            // layer_sync_bytes(kLayerMaxBlocks) bytes
+  void *sync;            // layer_sync_bytes() bytes
   uint8_t *hterm;        // layer_hterm_bytes() bytes: per slot the fp8 terms of h + scales
   uint32_t spin_limit;   // polls before a wait gives up
   int n_gu_per_slot;     // filled by layer_geometry: gate_up tiles / 4 = h blocks of 32
   int n_dn;              //                           down tiles
 };
-size_t layer_sync_bytes(int max_blocks);
+size_t layer_sync_bytes();
 size_t layer_hterm_bytes();
 void layer_geometry(LayerArgs &la);
 bool decode_layer_supported(const LayerArgs &la);

@@ -278,7 +278,7 @@ int check_layer_sync(moe_ctx *c) {
   uint32_t err = 0;
   HIP_TRY(hipMemcpy(&err, c->layer_sync.p, 4, hipMemcpyDeviceToHost));
   if (!err) return MOE_OK;
-  HIP_TRY(hipMemset(c->layer_sync.p, 0, layer_sync_bytes(kLayerMaxBlocks)));
+  HIP_TRY(hipMemset(c->layer_sync.p, 0, layer_sync_bytes()));
   return fail(MOE_ERR_HIP, "single-token layer kernel: a cross-block wait ran out (outputs since "
                            "the last synchronisation are NaN)");
 }
@@ -544,7 +544,7 @@ int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ct
     delete c;
     return fail(MOE_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
   }
-  const size_t sb = layer_sync_bytes(kLayerMaxBlocks), hb = layer_hterm_bytes();
+  const size_t sb = layer_sync_bytes(), hb = layer_hterm_bytes();
   if (c->layer_sync.ensure(sb) != MOE_OK || hipMemset(c->layer_sync.p, 0, sb) != hipSuccess ||
       c->layer_h.ensure(hb) != MOE_OK || hipMemset(c->layer_h.p, 0, hb) != hipSuccess) {
     moe_destroy(c);

@@ -453,6 +453,24 @@ def test_single_token_ties_and_nan_across_halves(orc, mode):
     d.close()
 
 
+def test_one_launch_tiny_grids_in_sequence(orc):
+    """A layer so small that the one-launch kernel has fewer blocks than logit copies (k gate_up
+    blocks + 4 down blocks): consecutive tokens with different routings and k in one context
+    must each match the oracle, so no copy or flag left by one launch is taken for the next's."""
+    H, I, E = 64, 32, 40
+    L = syn.make_layer(H, I, E, seed=360, scale_lo=120, scale_hi=124)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    d.set_fused_decode(2)
+    for i, k in enumerate((1, 4, 2, 3, 4, 1, 4)):
+        x = syn.hidden(1, H, seed=900 + i)
+        want, _, idx, _ = orc.moe_layer(x, L, k)
+        gidx, _ = d.router_topk(0, x, k)
+        assert np.array_equal(gidx, idx)
+        assert_rel_l2(d.layer_forward(0, x, k), want, f"call {i} k={k}")
+    d.close()
+
+
 # ---------------------------------------------------------------- committed fixture
 
 @pytest.mark.parametrize("fused", [2, 1, 0])
