@@ -3,14 +3,15 @@
 // weight stream overlapping the gate_up phase.
 //
 // Blocks of 4 wavefronts (3 per CU, so all blocks of the GPT-OSS shape are resident at once),
-// two roles by block index:
-//   [0, k*NGS)        gate_up blocks: block (slot s, i) streams the 4 gate_up tiles (64 rows)
-//                     of slot s's expert that produce h[32i, 32i+32), one tile per wavefront.
-//   [k*NGS, +H/16)    down blocks: one 16-row output tile, wavefront = slot; bias, clamp and the
+// three roles by block index:
+//   [0, n_rt)         router blocks (n_rt = ceil(E / 4)): wavefront w computes logit w;
+//   then k*NGS        gate_up blocks: block (slot s, i) streams the 4 gate_up tiles (64 rows)
+//                     of slot s's expert that produce h[32i, 32i+32), one tile per wavefront;
+//   then H/16         down blocks: one 16-row output tile, wavefront = slot; bias, clamp and the
 //                     slot-ordered combine into y.
-// Router: wavefront w of the grid (w < E) computes logit w in the canonical order (same
-// arithmetic as k_route) and writes it, tagged, into nrep = min(kReplicas, blocks) copies of the
-// logit vector; block b reads copy b % nrep and runs the top-k itself (identical arithmetic everywhere,
+// Router: each logit in the canonical order (same arithmetic as k_route), written, tagged, into
+// nrep = min(kReplicas, readers) copies of the logit vector; reader block b (counted from the
+// first gate_up block) reads copy b % nrep and runs the top-k itself (identical arithmetic everywhere,
 // so every block selects the same experts and weights). Block 0 also writes the logits,
 // indices and weights.
 // Matmuls: v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as stored (no decode
@@ -238,35 +239,40 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   __shared__ float s_o[4][16];
 
   const DecodeArgs &a = la.d;
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int H = a.H, E = a.E, K = a.k;
   const int NGS = la.n_gu_per_slot;
-  const int n_gu = K * NGS, n_blk = n_gu + la.n_dn;
-  LayerSyncHdr *hdr = reinterpret_cast<LayerSyncHdr *>(la.sync);
-  const int nrep = n_blk < kReplicas ? n_blk : kReplicas;  // logit copies in use
-  const int rc = b % nrep;
-  LogitCopy *cp = logit_copy(la.sync, rc);
-  const int readers = n_blk / nrep + (rc < n_blk % nrep ? 1 : 0);
-  const uint32_t err0 = ld_agent(&hdr->err);  // tested late: the load overlaps the router
-  const TopkCfg tc{E, K, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
+  const int n_gu = K * NGS, n_rd = n_gu + la.n_dn;         // blocks that read the routing
+  const int nrep = n_rd < kReplicas ? n_rd : kReplicas;    // logit copies in use
   constexpr int XI = 8 * RNQ;  // x values per lane of the router chain
-  const int j = lane & 15, g = lane >> 4;
 
-  // ---------------------------------------------------------------- router wavefronts
-  MOE_TRACE(0);
-  const int gw = b * kLayerWaves + wv;
-  if (gw < E) {
-    float xr[XI];
+  // ---------------------------------------------------------------- router blocks
+  // Wavefront w of the first n_rt = ceil(E / 4) blocks computes logit w and leaves; the blocks
+  // that wait for the routing come after them.
+  if ((int)blockIdx.x < la.n_rt) {
+    const int e = (int)blockIdx.x * kLayerWaves + wv;
+    if (e < E) {
+      float xr[XI];
 #pragma unroll
-    for (int i = 0; i < XI; i++) xr[i] = a.x[min(lane + 64 * i, H - 1)];
+      for (int i = 0; i < XI; i++) xr[i] = a.x[min(lane + 64 * i, H - 1)];
 #pragma unroll
-    for (int i = 0; i < XI; i++)
-      if (lane + 64 * i >= H) xr[i] = 0.0f;
-    for (int e = gw; e < E; e += n_blk * kLayerWaves) {
+      for (int i = 0; i < XI; i++)
+        if (lane + 64 * i >= H) xr[i] = 0.0f;
       const float lg = router_logit<RNQ>(a.rw, a.rb, xr, e, lane);
       if (lane < nrep) st_agent64(&logit_copy(la.sync, lane)->logit[e], (1ull << 32) | __float_as_uint(lg));
     }
+    return;
   }
+
+  const int b = (int)blockIdx.x - la.n_rt;  // gate_up blocks [0, n_gu), then down blocks
+  LayerSyncHdr *hdr = reinterpret_cast<LayerSyncHdr *>(la.sync);
+  const int rc = b % nrep;
+  LogitCopy *cp = logit_copy(la.sync, rc);
+  const int readers = n_rd / nrep + (rc < n_rd % nrep ? 1 : 0);
+  const uint32_t err0 = ld_agent(&hdr->err);  // tested late: the load overlaps the routing wait
+  const TopkCfg tc{E, K, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
+  const int j = lane & 15, g = lane >> 4;
+  MOE_TRACE(0);
 
   if (b < n_gu) {
     // ================================================================ gate_up block
@@ -344,6 +350,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
       s_h32[wv * 8 + 2 * g + 1] = swiglu(v[2] + bias.z, v[3] + bias.w, a.limit);
     }
     __syncthreads();
+    MOE_TRACE(5);
     // 4. h[32 hb, 32 hb + 32) as kTerms fp8 terms -> this slot's h record (lanes 0..3 of
     //    wavefront 0 hold 8 values each); once the stores are complete, the flags
     if (wv == 0) {
@@ -369,6 +376,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
         }
       }
       wait_mem();
+      MOE_TRACE(6);
       if (lane < kFlagReplicas) st_agent(&hdr->hflag[lane][slot][hb], ep + 1);
       MOE_TRACE(4);
     }
@@ -456,6 +464,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
   }
   __syncthreads();
+  MOE_TRACE(5);
   const bool failed = timeout || s_wfail[0] || s_wfail[1] || s_wfail[2] || s_wfail[3];
   if (tid < 16) {  // session.rs:974-980: y = 0; y += w_s * out_s in slot order
     float y = 0.0f;
@@ -478,6 +487,7 @@ size_t decode_layer_lds(const LayerArgs &) { return (size_t)4 * Act::kBytes; }
 void layer_geometry(LayerArgs &la) {
   la.n_gu_per_slot = (int)(la.d.gu.tiles / 4);
   la.n_dn = (int)la.d.dn.tiles;
+  la.n_rt = (la.d.E + kLayerWaves - 1) / kLayerWaves;
 }
 
 size_t layer_hterm_bytes() { return (size_t)4 * Act::kBytes; }
@@ -488,13 +498,14 @@ bool decode_layer_supported(const LayerArgs &la) {
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          a.gu.ns <= (uint32_t)kLayerNs && a.dn.ns <= (uint32_t)kLayerNs && a.H % 32 == 0 &&
          a.I % 32 == 0 && a.gu.tiles % 4 == 0 && a.gu.tiles / 4 <= (uint32_t)kMaxHBlocks &&
-         a.k * la.n_gu_per_slot + la.n_dn <= kLayerMaxBlocks;
+         la.n_rt == (a.E + kLayerWaves - 1) / kLayerWaves &&
+         la.n_rt + a.k * la.n_gu_per_slot + la.n_dn <= kLayerMaxBlocks;
 }
 
 hipError_t launch_decode_layer(const LayerArgs &la, hipStream_t s) {
   const DecodeArgs &a = la.d;
   if (!decode_layer_supported(la) || !la.sync || !la.hterm) return hipErrorInvalidValue;
-  const dim3 grid(a.k * la.n_gu_per_slot + la.n_dn), block(kLayerThreads);
+  const dim3 grid(la.n_rt + a.k * la.n_gu_per_slot + la.n_dn), block(kLayerThreads);
   const size_t lds = decode_layer_lds(la);
   switch (a.rnq) {  // router chain length per lane, in 16-byte loads (6 for H = 2880)
     case 1: hipLaunchKernelGGL(k_decode_layer<1>, grid, block, lds, s, la); break;

@@ -116,6 +116,7 @@ struct LayerArgs {
   uint32_t spin_limit;   // polls before a wait gives up
   int n_gu_per_slot;     // filled by layer_geometry: gate_up tiles / 4 = h blocks of 32
   int n_dn;              //                           down tiles
+  int n_rt;              //                           router blocks, ceil(E / 4)
 };
 size_t layer_sync_bytes();
 size_t layer_hterm_bytes();
