@@ -2,46 +2,50 @@
 // Session::decode_step_inner (session.rs:818-980) for one token, with the down projection's
 // weight stream overlapping the gate_up phase.
 //
-// Blocks of 4 wavefronts (3 per CU, so all blocks of the GPT-OSS shape are resident at once),
-// three roles by block index:
+// Blocks of 4 wavefronts, sized so the grid is two blocks per CU and every CU streams about the
+// same weight bytes (a CU's share of the HBM stream, not its block count, sets when it is done):
 //   [0, n_rt)         router blocks (n_rt = ceil(E / 4)): wavefront w computes logit w;
-//   then k*NGS        gate_up blocks: block (slot s, i) streams the 4 gate_up tiles (64 rows)
-//                     of slot s's expert that produce h[32i, 32i+32), one tile per wavefront;
+//   then n_gu         gate_up blocks: block b streams gate_up tiles 4b .. 4b+3 (16 rows each, one
+//                     per wavefront, one chunk of 32 h values of one slot), and X of them (spread
+//                     evenly) one more tile, split by K over the 4 wavefronts; the tiles are
+//                     numbered slot-major over the k * TPS tiles of the chosen experts;
 //   then H/16         down blocks: one 16-row output tile, wavefront = slot; bias, clamp and the
 //                     slot-ordered combine into y.
 // Router: each logit in the canonical order (same arithmetic as k_route), written, tagged, into
 // nrep = min(kReplicas, readers) copies of the logit vector; reader block b (counted from the
-// first gate_up block) reads copy b % nrep and runs the top-k itself (identical arithmetic everywhere,
-// so every block selects the same experts and weights). Block 0 also writes the logits,
-// indices and weights.
+// first gate_up block) reads copy b % nrep and runs the top-k itself (identical arithmetic
+// everywhere, so every block selects the same experts and weights). Gate_up block 0 also writes
+// the logits, indices and weights.
 // Matmuls: v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as stored (no decode
-// instructions) and the activation as kTerms fp8 terms with E8M0 scales (split8_fp8):
-// x is split by every gate_up block into LDS; each gate_up block splits its 32 h values and
-// publishes them; down blocks copy the h terms of the kept slots into LDS.
+// instructions). x enters as kTerms fp8 terms with per-block E8M0 scales (split8_fp8, split by
+// every gate_up block into LDS). h is bounded (|h| <= max(limit, 1/4) * (limit + 1)), so each
+// gate_up tile splits its 8 values into kTerms fp8 terms with fixed exponents (split2_fp8_fixed)
+// without waiting for the rest of the 32-value block, and its block stores the 32-byte pieces of
+// its tiles as whole lines of the slot's tile-major h record; down blocks copy the records of
+// the kept slots into LDS.
 //
 // Cross-block signalling without fences over the L2: every value read by another block
-// (logits, h terms, flags) is written with agent-scope relaxed atomic stores (write-through)
+// (logits, h records, flags) is written with agent-scope relaxed atomic stores (write-through)
 // and read with agent-scope loads that bypass the L2 (relaxed atomic loads, or LDS-direct
 // loads with the same cache policy); a writer waits for its stores to complete (s_waitcnt)
 // before it raises the flag that publishes them.
 //   * logits: every block adds 1 to its copy's counter after reading the copy; the block that
 //     brings it to the copy's reader count clears the copy and the counter and advances the
-//     copy's launch number (epoch). Every copy advances exactly once per launch, so all copies
-//     hold the same epoch when a launch starts, and a block reads its copy's epoch before its
-//     own count can let the copy advance;
-//   * h block i of slot s: once its h terms are complete, the gate_up block stores epoch + 1
-//     into flag (s, i) of each of kFlagReplicas replicas; down wavefront s waits until the NGS
-//     flags of slot s in its replica read epoch + 1. Flags are never cleared: a flag from an
-//     earlier launch holds a smaller number.
-// So no atomic and no second hop sits between the last h store and the down blocks. Copies and
-// counters are zero again when the kernel ends. The blocks that wait on gate_up blocks have
+//     copy's launch number (epoch) and those of the unused copies it stands for. Every copy
+//     advances exactly once per launch, so all copies hold the same epoch when a launch starts,
+//     and a block reads its copy's epoch before its own count can let the copy advance;
+//   * h: once every h store of a gate_up block is complete, it stores epoch + 1 into its flag in
+//     each of kFlagReplicas replicas; wavefront 0 of a down block waits until all n_gu flags of
+//     its replica read epoch + 1. Flags are never cleared: a flag from an earlier launch holds a
+//     smaller number.
+// Copies and counters are zero again when the kernel ends. The blocks that wait on others have
 // higher indices, and workgroups are dispatched in index order, so waiting blocks never hold
-// back the blocks they wait for; the router wavefronts are in the lowest blocks. Every wait is
-// bounded by `spin_limit` polls; a wait that runs out sets the sticky error word, the block
-// writes NaN to its outputs, and later launches return NaN at once until the host clears the
-// error (it reports it at its next synchronisation and zeroes the signalling area, epochs
-// included).
+// back the blocks they wait for. Every wait is bounded by `spin_limit` polls; a wait that runs
+// out sets the sticky error word, the block writes NaN to its outputs, and later launches return
+// NaN at once until the host clears the error (it reports it at its next synchronisation and
+// zeroes the signalling area, epochs included).
 #include <algorithm>
+#include <cmath>
 
 #include "device.hpp"
 #include "kernels.hpp"
@@ -49,15 +53,25 @@
 namespace moe {
 
 // Timeline tracing for development builds (-DMOE_TRACE_TIMELINE): thread 0 of each block
-// records the realtime counter (100 MHz) at numbered points into moe_trace_ts[block][8],
+// records the realtime counter (100 MHz) at numbered points into moe_trace_ts[block][16],
 // read back with moe_trace_read(). Compiled out otherwise.
 #ifdef MOE_TRACE_TIMELINE
-__device__ long long moe_trace_ts[4096 * 8];
+__device__ long long moe_trace_ts[4096 * 16];
 #define MOE_TRACE(i)                                                                        \
   do {                                                                                      \
-    if (threadIdx.x == 0) moe_trace_ts[blockIdx.x * 8 + (i)] = (long long)__builtin_amdgcn_s_memrealtime(); \
+    if (threadIdx.x == 0) moe_trace_ts[blockIdx.x * 16 + (i)] = (long long)__builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+// slot 7: where the block runs, XCC_ID << 16 | HW_ID bits 8..15 (CU, shader array, engine)
+#define MOE_TRACE_WHERE()                                                                         \
+  do {                                                                                            \
+    if (threadIdx.x == 0)                                                                         \
+      moe_trace_ts[blockIdx.x * 16 + 7] = ((long long)__builtin_amdgcn_s_getreg((15 << 11) | 20) << 16) | \
+                                         ((__builtin_amdgcn_s_getreg((31 << 11) | 4) >> 8) & 0xFF); \
   } while (0)
 #else
+#define MOE_TRACE_WHERE() \
+  do {                    \
+  } while (0)
 #define MOE_TRACE(i) \
   do {               \
   } while (0)
@@ -81,20 +95,93 @@ struct LogitCopy {               // kCopyBytes apart
 constexpr size_t kCopyBytes = 1088;
 static_assert(sizeof(LogitCopy) <= kCopyBytes, "copy layout");
 
-constexpr int kFlagReplicas = 4;
-constexpr int kMaxHBlocks = 128;  // h blocks of 32 per slot (K <= 3072 -> 96)
+constexpr int kFlagReplicas = 16;
+constexpr int kLayerMaxK = 32 * 4 * kLayerNs;      // 3072: longest K of a tile
+constexpr int kLayerMaxTps = 2 * kLayerMaxK / 16;  // gate_up tiles per slot (I <= 3072 -> 384)
+constexpr int kLayerMaxGu = kLayerMaxTps;          // gate_up blocks (4 slots x 384 tiles / 4)
+static_assert(kLayerMaxGu % 64 == 0, "flag poll shape");
 
 struct LayerSyncHdr {
   uint32_t err;          // sticky: a bounded wait ran out
   uint32_t pad0[63];
-  uint32_t hflag[kFlagReplicas][4][kMaxHBlocks];  // epoch + 1: h block i of slot s is published
+  uint32_t gflag[kFlagReplicas][kLayerMaxGu];  // epoch + 1: gate_up block i has published its h
 };
 
 size_t layer_sync_bytes() { return sizeof(LayerSyncHdr) + kReplicas * kCopyBytes; }
 
-// h records of the slots, in HBM and in a down block's LDS: Act::kBytes apart (a multiple of 16,
-// so a record is whole 16-byte lane pieces of LDS-direct loads).
-static_assert(Act::kBytes % 16 == 0, "h record size");
+constexpr int kLayerMaxHexp = 5;
+
+// h record of a slot (HBM, and a down block's LDS): tile-major, gate_up tile t's 8 values
+// h[8t, 8t+8) at 32 t, term j of them at 32 t + 8 j (value i at byte i), kTerms = 4 fp8 terms
+// with the fixed exponents hexp - 4j; values past I are zero. 12 KB for K <= 3072.
+constexpr int kHRecBytes = kLayerMaxK / 8 * 32;
+static_assert(kTerms == 4, "h record piece = 4 terms x 8 bytes");
+
+// MFMA sweep of a loaded down tile against an h record in LDS: the B operand of tile_mfma_f8 from
+// the tile-major layout. Lane (column j = term j % 4, group gb) takes, for step s, values
+// 16(gb&1) .. +15 of block 4s + (gb>>1) (two 8-value pieces, 32 bytes apart) and the same values
+// of block 4s + 2 + (gb>>1) (256 bytes further); sb = the lane's B scale byte in every byte
+// (term j's fixed scale, 0 for columns >= kTerms).
+template <int NSMAX>
+__device__ __forceinline__ f32x4 tile_mfma_h(const TileRegs<NSMAX> &r, const uint8_t *rec, uint32_t sb, int lane) {
+  const int j = lane & 15, gb = lane >> 4;
+  const uint8_t *bt = rec + 128 * (gb >> 1) + 64 * (gb & 1) + 8 * (j & (kTerms - 1));
+  f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+  constexpr int PD = 2;  // B of step s is read two steps ahead
+  uint2 pb[PD][4];
+#pragma unroll
+  for (int s = 0; s < PD; s++) {
+    pb[s][0] = *reinterpret_cast<const uint2 *>(bt + 512 * s);
+    pb[s][1] = *reinterpret_cast<const uint2 *>(bt + 512 * s + 32);
+    pb[s][2] = *reinterpret_cast<const uint2 *>(bt + 512 * s + 256);
+    pb[s][3] = *reinterpret_cast<const uint2 *>(bt + 512 * s + 288);
+  }
+#pragma unroll
+  for (int s = 0; s < NSMAX; s++) {
+    const uint2 b0 = pb[s % PD][0], b1 = pb[s % PD][1], b2 = pb[s % PD][2], b3 = pb[s % PD][3];
+    if (s + PD < NSMAX) {
+      pb[s % PD][0] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD));
+      pb[s % PD][1] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD) + 32);
+      pb[s % PD][2] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD) + 256);
+      pb[s % PD][3] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD) + 288);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4 a = r.raw[s];
+    const i32x8 A = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    const i32x8 B = {(int)b0.x, (int)b0.y, (int)b1.x, (int)b1.y, (int)b2.x, (int)b2.y, (int)b3.x, (int)b3.y};
+    if (s & 1)
+      acc1 = mfma_fp4_fp8(s & 3, A, B, acc1, r.sw[s / 4], sb);
+    else
+      acc0 = mfma_fp4_fp8(s & 3, A, B, acc0, r.sw[s / 4], sb);
+  }
+  return acc0 + acc1;
+}
+
+// tile_mfma_f8 over steps [s0, s0 + NS) of a tile whose chunks for those steps are in raw[] (zeros
+// past the tile) and whose scale words are all in sw[]; rec, bsw as for tile_mfma_f8. One
+// accumulator: the extra tile's quarter is short.
+template <int NSMAX, int NS, int s0>
+__device__ __forceinline__ f32x4 tile_mfma_f8_steps(const uint4 (&raw)[NS], const uint32_t *sw,
+                                                    const uint8_t *rec, const uint32_t *bsw, int lane) {
+  using R = ActRecord<NSMAX>;
+  const int j = lane & 15, gb = lane >> 4;
+  const uint8_t *bt = rec + R::term(j & (kTerms - 1), gb >> 1) + 16 * (gb & 1);
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k = 0; k < NS; k++) {
+    const int s = s0 + k;
+    if (s < NSMAX) {
+      const uint4 b0 = *reinterpret_cast<const uint4 *>(bt + s * 128);
+      const uint4 b1 = *reinterpret_cast<const uint4 *>(bt + s * 128 + 64);
+      const uint4 a = raw[k];
+      const i32x8 A = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+      const i32x8 B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                       (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+      acc = mfma_fp4_fp8(s & 3, A, B, acc, sw[s / 4], bsw[s / 4]);
+    }
+  }
+  return acc;
+}
 
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -227,23 +314,24 @@ __device__ __forceinline__ void release_end(void *sync, int r, int nrep, uint32_
 }
 
 template <int RNQ>
-__global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_decode_layer(LayerArgs la) {
+__global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2, 3))) void k_decode_layer(LayerArgs la) {
   extern __shared__ uint4 smem[];
   __shared__ int s_order[kMaxTopK];
   __shared__ float s_w[kMaxTopK];
   __shared__ int s_sel;
   __shared__ int s_flag;
   __shared__ uint32_t s_ep;
-  __shared__ int s_wfail[4];
-  __shared__ float s_h32[32];
+  __shared__ int s_wfail[1];
   __shared__ float s_o[4][16];
+  __shared__ __align__(16) uint8_t s_hp[32 * (kLayerWaves + 1)];  // h record pieces of a gate_up block's tiles
+  __shared__ __align__(16) float s_xp[kLayerWaves][16];             // the extra tile's partial sums
 
   const DecodeArgs &a = la.d;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int H = a.H, E = a.E, K = a.k;
-  const int NGS = la.n_gu_per_slot;
-  const int n_gu = K * NGS, n_rd = n_gu + la.n_dn;         // blocks that read the routing
-  const int nrep = n_rd < kReplicas ? n_rd : kReplicas;    // logit copies in use
+  const int TPS = la.n_tps;                                 // gate_up tiles per slot
+  const int n_gu = la.n_gu, n_rd = n_gu + la.n_dn;          // blocks that read the routing
+  const int nrep = n_rd < kReplicas ? n_rd : kReplicas;     // logit copies in use
   constexpr int XI = 8 * RNQ;  // x values per lane of the router chain
 
   // ---------------------------------------------------------------- router blocks
@@ -273,6 +361,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   const TopkCfg tc{E, K, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
   const int j = lane & 15, g = lane >> 4;
   MOE_TRACE(0);
+  MOE_TRACE_WHERE();
 
   if (b < n_gu) {
     // ================================================================ gate_up block
@@ -310,25 +399,55 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
       const bool ok = await_logits(cp, E, la.spin_limit, lane, l, &ep);
       if (ok) route_order(tc, l, lane, ord, s_order, s_w, &s_sel);
       rel = release_begin(cp, lane);
-      if (lane == 0) s_flag = !ok;
+      if (lane == 0) {
+        s_flag = !ok;
+        s_ep = ep;
+      }
     }
     __syncthreads();
     MOE_TRACE(2);
     const bool timeout = s_flag;
     const int sel = s_sel;
-    const int slot = b / NGS;
-    if (timeout || err0 || slot >= sel) {  // uniform over the block; no barrier follows
+    if (timeout || err0) {  // uniform over the block; no barrier follows
       if (timeout && tid == 0) st_agent(&hdr->err, 1u);
       if (wv == 0) release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
       return;
     }
-    // 3. this wavefront's gate_up tile (rows 16t .. 16t+15 -> h[8t, 8t+8)); bias with it
-    const int hb = b - slot * NGS;
-    const int t = hb * 4 + wv;
-    const uint8_t *rec = a.base + (size_t)s_order[slot] * a.stride;
+    ep = s_ep;
+    // 3. this wavefront's gate_up tile: tile 4b + wv; and for X of the blocks (spread evenly)
+    //    one of the X = k * TPS - 4 * n_gu tiles past the first 4 * n_gu (X <= n_gu), split by K
+    //    over the 4 wavefronts (steps [6 wv, 6 wv + 6)), so its bytes stream with the others.
+    //    Tile u is row tile u % TPS (rows 16 t .. 16 t + 15 -> h[8t, 8t+8)) of slot u / TPS;
+    //    tiles of dropped slots are skipped (uniformly over the block: 4b .. 4b+3 share a slot).
+    const int n_tiles = K * TPS, W = 4 * n_gu, X = n_tiles > W ? n_tiles - W : 0;
+    const int e_lo = (int)((long long)b * X / n_gu), e_hi = (int)((long long)(b + 1) * X / n_gu);
+    const int u0 = 4 * b + wv, ux = e_hi > e_lo ? W + e_lo : n_tiles;
+    const int slot0 = u0 / TPS, tt0 = u0 - slot0 * TPS, slotx = ux / TPS, ttx = ux - slotx * TPS;
+    const bool act0 = u0 < n_tiles && slot0 < sel, actx = ux < n_tiles && slotx < sel;
+    const uint8_t *rec0 = a.base + (size_t)(act0 ? s_order[slot0] : s_order[0]) * a.stride;
+    const uint8_t *recx = a.base + (size_t)(actx ? s_order[slotx] : s_order[0]) * a.stride;
     TileRegs<kLayerNs> r;
-    tile_load<kLayerNs>(r, rec + a.gu_off, a.gu, t, true, lane);
-    const float4 bias = reinterpret_cast<const float4 *>(rec + a.gub_off)[t * 4 + g];
+    tile_load<kLayerNs>(r, rec0 + a.gu_off, a.gu, tt0, act0, lane);
+    const float4 bias0 = act0 ? reinterpret_cast<const float4 *>(rec0 + a.gub_off)[tt0 * 4 + g] : make_float4(0.f, 0.f, 0.f, 0.f);
+    constexpr int kXs = (kLayerNs + kLayerWaves - 1) / kLayerWaves;  // extra-tile steps per wavefront
+    uint4 xraw[kXs];
+    uint32_t xsw[kLayerNq];
+    {
+      const int ns = (int)a.gu.ns, nb = (int)a.gu.nb;
+      const uint4 *wp = reinterpret_cast<const uint4 *>(recx + a.gu_off) + (size_t)ttx * 16 * nb;
+      const uint32_t *sp = reinterpret_cast<const uint32_t *>(recx + a.gu_off + pack_weight_bytes(a.gu)) + (size_t)ttx * a.gu.nq * 64;
+#pragma unroll
+      for (int k = 0; k < kXs; k++) {
+        const int st = kXs * wv + k;
+        xraw[k] = make_uint4(0u, 0u, 0u, 0u);
+        if (actx && st < ns && 4 * st + g < nb) {
+          const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp) + st * 64 + lane);
+          xraw[k] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kLayerNq; q++) xsw[q] = actx && q < (int)a.gu.nq ? sp[q * 64 + lane] : 0u;
+    }
     if (b == 0 && wv == 0) {  // block 0 reports the routing (the weights overlap its tile loads)
       route_weights(tc, l, lane, ord, s_order, s_w, &s_sel);
       if (lane < E) a.logits[lane] = l[0];
@@ -340,46 +459,69 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
     }
     uint32_t bsw[kLayerNq];
     load_bsw<kLayerNs>(s_x, bsw, lane);
-    const f32x4 acc = tile_mfma_f8<kLayerNs>(r, s_x, bsw, lane);
-    float v[4];
-    sum_terms(acc, v);
-    if (wv == 0) release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
-    MOE_TRACE(3);
-    if (j == 0) {
-      s_h32[wv * 8 + 2 * g] = swiglu(v[0] + bias.x, v[1] + bias.y, a.limit);
-      s_h32[wv * 8 + 2 * g + 1] = swiglu(v[2] + bias.z, v[3] + bias.w, a.limit);
+    // 4. the tile: MFMA sweep, bias, SwiGLU; lanes j == 0 hold h[8t + 2g], h[8t + 2g + 1], split
+    //    them into the fixed-exponent fp8 terms: the tile's 32-byte piece of the h record, staged
+    //    in LDS. The extra tile: each wavefront's partial sums to LDS.
+    if (act0) {
+      const f32x4 acc = tile_mfma_f8<kLayerNs>(r, s_x, bsw, lane);
+      float v[4];
+      sum_terms(acc, v);
+      if (wv == 0) release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
+      if (j == 0) {
+        const float h0 = swiglu(v[0] + bias0.x, v[1] + bias0.y, a.limit);
+        const float h1 = swiglu(v[2] + bias0.z, v[3] + bias0.w, a.limit);
+        const uint64_t q = split2_fp8_fixed(h0, h1, la.hexp);
+#pragma unroll
+        for (int te = 0; te < kTerms; te++)
+          *reinterpret_cast<uint16_t *>(s_hp + 32 * wv + 8 * te + 2 * g) = (uint16_t)(q >> (16 * te));
+      }
+    } else if (wv == 0) {
+      release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
     }
+    if (actx) {
+      f32x4 acc;
+      switch (wv) {  // the step range as a constant, so every scale word index is static
+        case 0: acc = tile_mfma_f8_steps<kLayerNs, kXs, 0>(xraw, xsw, s_x, bsw, lane); break;
+        case 1: acc = tile_mfma_f8_steps<kLayerNs, kXs, kXs>(xraw, xsw, s_x, bsw, lane); break;
+        case 2: acc = tile_mfma_f8_steps<kLayerNs, kXs, 2 * kXs>(xraw, xsw, s_x, bsw, lane); break;
+        default: acc = tile_mfma_f8_steps<kLayerNs, kXs, 3 * kXs>(xraw, xsw, s_x, bsw, lane); break;
+      }
+      float v[4];
+      sum_terms(acc, v);
+      if (j == 0) *reinterpret_cast<float4 *>(&s_xp[wv][4 * g]) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    MOE_TRACE(3);
     __syncthreads();
     MOE_TRACE(5);
-    // 4. h[32 hb, 32 hb + 32) as kTerms fp8 terms -> this slot's h record (lanes 0..3 of
-    //    wavefront 0 hold 8 values each); once the stores are complete, the flags
-    if (wv == 0) {
-      if (lane < 4) {
-        float hv[8];
+    // 5. the block's 4 consecutive tiles are 128 contiguous bytes of one slot's record: whole
+    //    lines, stored by 16 lanes of wavefront 0. Wavefront 3 sums the extra tile's partials (in
+    //    wavefront order), finishes it like the others and stores its 32 bytes.
+    if (wv == 0 && act0 && lane < 16)
+      st_agent64(reinterpret_cast<uint64_t *>(la.hterm + (size_t)slot0 * kHRecBytes + 32 * tt0) + lane,
+                 *reinterpret_cast<const uint64_t *>(s_hp + 8 * lane));
+    if (wv == kLayerWaves - 1 && actx) {
+      if (j == 0) {
+        const float4 biasx = reinterpret_cast<const float4 *>(recx + a.gub_off)[ttx * 4 + g];
+        float v[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) hv[i] = s_h32[8 * lane + i];
-        uint2 q[kTerms];
-        uint32_t s4;
-        split8_fp8(hv, q, s4);
-        uint8_t *rec_h = la.hterm + (size_t)slot * Act::kBytes;
+        for (int e = 0; e < 4; e++) v[e] = ((s_xp[0][4 * g + e] + s_xp[1][4 * g + e]) + s_xp[2][4 * g + e]) + s_xp[3][4 * g + e];
+        const float h0 = swiglu(v[0] + biasx.x, v[1] + biasx.y, a.limit);
+        const float h1 = swiglu(v[2] + biasx.z, v[3] + biasx.w, a.limit);
+        const uint64_t q = split2_fp8_fixed(h0, h1, la.hexp);
 #pragma unroll
-        for (int tt = 0; tt < kTerms; tt++) {
-          uint32_t *dst = reinterpret_cast<uint32_t *>(rec_h + Act::term(tt, hb) + 8 * lane);
-          st_agent(dst, q[tt].x);
-          st_agent(dst + 1, q[tt].y);
-        }
-        if (lane == 0) {
-#pragma unroll
-          for (int tt = 0; tt < kTerms; tt++)
-            __hip_atomic_store(rec_h + Act::scale(tt, hb), (uint8_t)(s4 >> (8 * tt)), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int te = 0; te < kTerms; te++)
+          *reinterpret_cast<uint16_t *>(s_hp + 32 * kLayerWaves + 8 * te + 2 * g) = (uint16_t)(q >> (16 * te));
       }
-      wait_mem();
-      MOE_TRACE(6);
-      if (lane < kFlagReplicas) st_agent(&hdr->hflag[lane][slot][hb], ep + 1);
-      MOE_TRACE(4);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (lane < 4)
+        st_agent64(reinterpret_cast<uint64_t *>(la.hterm + (size_t)slotx * kHRecBytes + 32 * ttx) + lane,
+                   *reinterpret_cast<const uint64_t *>(s_hp + 32 * kLayerWaves + 8 * lane));
     }
+    wait_mem();
+    MOE_TRACE(6);
+    __syncthreads();
+    if (wv == 0 && lane < kFlagReplicas) st_agent(&hdr->gflag[lane][b], ep + 1);
+    MOE_TRACE(4);
     return;
   }
 
@@ -409,51 +551,51 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   TileRegs<kLayerNs> r;
   tile_load<kLayerNs>(r, rec + a.dn_off, a.dn, ok ? t : 0, ok, lane);
   const float4 bias = reinterpret_cast<const float4 *>(rec + a.dnb_off)[(ok ? t : 0) * 4 + g];
+  MOE_TRACE(9);
   if (wv == 0) {
     release_end(la.sync, rc, nrep, rel, readers, E, ep, lane);
     if (!timeout) route_weights(tc, l, lane, ord, s_order, s_w, &s_sel);  // read after the combine's barrier
   }
-  // 3. wavefront `slot`: wait for the NGS h blocks of its slot, then bring the slot's h record
-  //    into LDS, 1 KB per instruction, straight into LDS (the last instruction only on the lanes
-  //    inside the record, so no byte of a neighbour's record is written)
+  // 3. wavefront 0 waits until every gate_up block has published (its replica of the block flags
+  //    reads epoch + 1); then wavefront `slot` brings its slot's h record (the kTerms term rows)
+  //    into LDS, 1 KB per instruction, straight into LDS (the last one only on the lanes inside
+  //    the rows, so no byte of a neighbour's record is written)
   bool wfail = false;
-  if (ok) {
+  if (wv == 0 && sel > 0) {
     const uint32_t want = s_ep + 1;
-    const uint32_t *f = hdr->hflag[t % kFlagReplicas][slot];
+    const uint32_t *f = hdr->gflag[t % kFlagReplicas];
     for (uint32_t n = 0;; n++) {
-      const bool d0 = lane >= NGS || ld_agent(f + lane) == want;
-      const bool d1 = lane + 64 >= NGS || ld_agent(f + lane + 64) == want;
-      if (__all(d0 && d1)) break;
+      bool d = true;
+#pragma unroll
+      for (int i = 0; i < kLayerMaxGu / 64; i++)
+        d = d && (lane + 64 * i >= n_gu || ld_agent(f + lane + 64 * i) == want);
+      if (__all(d)) break;
       if (n >= la.spin_limit) {
         wfail = true;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    MOE_TRACE(2);
-    if (!wfail) {
-      const uint8_t *src = la.hterm + (size_t)slot * Act::kBytes;
-      uint8_t *dst = s_h + (size_t)slot * Act::kBytes;
-#pragma unroll
-      for (int cix = 0; cix < Act::kBytes / 1024; cix++)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src + (size_t)cix * 1024) + lane,
-                                         (__attribute__((address_space(3))) void *)(dst + (size_t)cix * 1024),
-                                         16, 0, 16);
-      constexpr int kTail = Act::kBytes % 1024;
-      if (kTail && 16 * lane < kTail)
-        __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const uint4 *>(src + (size_t)(Act::kBytes - kTail)) + lane,
-            (__attribute__((address_space(3))) void *)(dst + (size_t)(Act::kBytes - kTail)), 16, 0, 16);
-      wait_mem();
-    }
-    MOE_TRACE(3);
   }
-  if (lane == 0) s_wfail[wv] = wfail;
+  if (wv == 0 && lane == 0) s_wfail[0] = wfail;
+  __syncthreads();
+  MOE_TRACE(2);
+  wfail = s_wfail[0];
   if (ok && !wfail) {
-    const uint8_t *hrec = s_h + (size_t)slot * Act::kBytes;
-    uint32_t bsw[kLayerNq];
-    load_bsw<kLayerNs>(hrec, bsw, lane);
-    const f32x4 acc = tile_mfma_f8<kLayerNs>(r, hrec, bsw, lane);
+    const uint8_t *src = la.hterm + (size_t)slot * kHRecBytes;
+    uint8_t *dst = s_h + (size_t)slot * kHRecBytes;
+#pragma unroll
+    for (int cix = 0; cix < kHRecBytes / 1024; cix++)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src + (size_t)cix * 1024) + lane,
+                                       (__attribute__((address_space(3))) void *)(dst + (size_t)cix * 1024),
+                                       16, 0, 16);
+    wait_mem();
+  }
+  MOE_TRACE(3);
+  if (ok && !wfail) {
+    const uint8_t *hrec = s_h + (size_t)slot * kHRecBytes;
+    const uint32_t sb = j < kTerms ? (uint32_t)(127 + la.hexp - 4 * j) * 0x01010101u : 0u;
+    const f32x4 acc = tile_mfma_h<kLayerNs>(r, hrec, sb, lane);
     float v[4];
     sum_terms(acc, v);
     if (j == 0) {
@@ -465,7 +607,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
   }
   __syncthreads();
   MOE_TRACE(5);
-  const bool failed = timeout || s_wfail[0] || s_wfail[1] || s_wfail[2] || s_wfail[3];
+  const bool failed = timeout || wfail;
   if (tid < 16) {  // session.rs:974-980: y = 0; y += w_s * out_s in slot order
     float y = 0.0f;
     if (failed) {
@@ -481,31 +623,53 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(3
 }
 
 size_t decode_layer_lds(const LayerArgs &) { return (size_t)4 * Act::kBytes; }
+static_assert(kHRecBytes <= Act::kBytes, "down blocks hold 4 h records");
 
-// Derived geometry of the one-launch kernel for la.d (the host fills la.d, sync, hterm and
-// spin_limit).
-void layer_geometry(LayerArgs &la) {
-  la.n_gu_per_slot = (int)(la.d.gu.tiles / 4);
-  la.n_dn = (int)la.d.dn.tiles;
-  la.n_rt = (la.d.E + kLayerWaves - 1) / kLayerWaves;
+// Derived geometry of the one-launch kernel for la.d on a device of n_cu compute units (the
+// host fills la.d, sync, hterm and spin_limit): router blocks, down blocks, and as many gate_up
+// blocks as make the grid two blocks per CU (each CU then streams about the same bytes: 4 or 5
+// weight tiles per block), within [ceil(tiles / 5), ceil(tiles / 4)] so a block takes 4 or 5
+// tiles.
+void layer_geometry(LayerArgs &la, int n_cu) {
+  const DecodeArgs &a = la.d;
+  la.n_tps = (int)a.gu.tiles;
+  la.n_dn = (int)a.dn.tiles;
+  la.n_rt = (a.E + kLayerWaves - 1) / kLayerWaves;
+  const int tiles = a.k * la.n_tps;
+  const int lo = (tiles + 4) / 5, hi = (tiles + 3) / 4;
+  la.n_gu = std::min(hi, std::max(lo, 2 * n_cu - la.n_rt - la.n_dn));
+  la.hexp = layer_hexp(a.limit);
 }
 
-size_t layer_hterm_bytes() { return (size_t)4 * Act::kBytes; }
+// The exponent of the first h term: |h| <= max(limit, 1/4) * (limit + 1) for every finite h
+// (gate <= limit, |up| <= limit, gate * sigmoid(1.702 gate) >= -1/4), so h * 2^-hexp stays below
+// 256, inside e4m3's range. Large limits leave small values below the last term's resolution
+// (2^(hexp - 21)); kLayerMaxHexp bounds that at 2^-16.
+int layer_hexp(float limit) {
+  const float bound = std::max(limit, 0.25f) * (limit + 1.0f);
+  int e;
+  (void)std::frexp(bound, &e);  // bound in [2^(e-1), 2^e)
+  return e - 1 - 7;
+}
+
+size_t layer_hterm_bytes() { return (size_t)4 * kHRecBytes; }
 
 bool decode_layer_supported(const LayerArgs &la) {
   const DecodeArgs &a = la.d;
+  const int tiles = a.k * la.n_tps;
   return a.k >= 1 && a.k <= 4 && a.E >= 1 && a.E <= kLayerMaxE && a.k <= a.E && a.rnq >= 1 && a.rnq <= 6 &&
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          a.gu.ns <= (uint32_t)kLayerNs && a.dn.ns <= (uint32_t)kLayerNs && a.H % 32 == 0 &&
-         a.I % 32 == 0 && a.gu.tiles % 4 == 0 && a.gu.tiles / 4 <= (uint32_t)kMaxHBlocks &&
-         la.n_rt == (a.E + kLayerWaves - 1) / kLayerWaves &&
-         la.n_rt + a.k * la.n_gu_per_slot + la.n_dn <= kLayerMaxBlocks;
+         a.I % 32 == 0 && a.I <= kLayerMaxK && la.n_tps == (int)a.gu.tiles && la.n_tps <= kLayerMaxTps &&
+         la.n_rt == (a.E + kLayerWaves - 1) / kLayerWaves && la.n_gu >= 1 && la.n_gu <= kLayerMaxGu &&
+         5 * la.n_gu >= tiles && la.hexp == layer_hexp(a.limit) && la.hexp <= kLayerMaxHexp &&
+         la.n_rt + la.n_gu + la.n_dn <= kLayerMaxBlocks;
 }
 
 hipError_t launch_decode_layer(const LayerArgs &la, hipStream_t s) {
   const DecodeArgs &a = la.d;
   if (!decode_layer_supported(la) || !la.sync || !la.hterm) return hipErrorInvalidValue;
-  const dim3 grid(la.n_rt + a.k * la.n_gu_per_slot + la.n_dn), block(kLayerThreads);
+  const dim3 grid(la.n_rt + la.n_gu + la.n_dn), block(kLayerThreads);
   const size_t lds = decode_layer_lds(la);
   switch (a.rnq) {  // router chain length per lane, in 16-byte loads (6 for H = 2880)
     case 1: hipLaunchKernelGGL(k_decode_layer<1>, grid, block, lds, s, la); break;
@@ -522,7 +686,7 @@ hipError_t launch_decode_layer(const LayerArgs &la, hipStream_t s) {
 
 #ifdef MOE_TRACE_TIMELINE
 extern "C" int moe_trace_read(long long *out, int n_blocks) {
-  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(moe::moe_trace_ts), (size_t)n_blocks * 8 * 8, 0,
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(moe::moe_trace_ts), (size_t)n_blocks * 16 * 8, 0,
                                   hipMemcpyDeviceToHost);
 }
 #endif

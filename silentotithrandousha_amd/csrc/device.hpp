@@ -48,10 +48,14 @@ __device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
   return __uint_as_float(bits | ((n & 8u) << 28));
 }
 
-// GPT-OSS SwiGLU of session.rs:109-117: gate = min(g, L) (NaN-ignoring), up = clamp(u, +-L),
-// glu = gate / (1 + exp(-gate * 1.702)), h = (up + 1) * glu.
+// GPT-OSS SwiGLU of session.rs:109-117: gate = min(g, L), up = clamp(u, +-L),
+// glu = gate / (1 + exp(-gate * 1.702)), h = (up + 1) * glu. Identical for every non-NaN g; a NaN
+// g stays NaN here, where the reference's NaN-ignoring min gives L. A NaN gate only arises from
+// non-finite weights or inputs, where these paths can hold NaN in place of the reference's
+// infinity (an E8M0 255 block is NaN to the block-scaled MFMA); propagating it keeps every
+// output that is non-finite in the fp32 path non-finite here.
 __device__ __forceinline__ float swiglu(float g, float u, float limit) {
-  float gate = fminf(g, limit);
+  float gate = g != g ? g : fminf(g, limit);
   float up = rclamp(u, -limit, limit);
   float glu = gate / (1.0f + expf(-gate * 1.702f));
   return (up + 1.0f) * glu;
@@ -537,6 +541,24 @@ __device__ __forceinline__ void split8_fp8_with_max(const float x[8], float m, b
     q[t] = make_uint2(w[0], w[1]);
     s4 |= (uint32_t)(e + 127) << (8 * t);
   }
+}
+
+// Two values of a range known in advance (|v| < 2^(e0 + 8)) as kTerms e4m3 terms with the fixed
+// exponents e_t = e0 - 4t, no block maximum needed: the same term arithmetic as above, so each
+// term divides a value's remaining error by at least 2^4 until the residual falls below the last
+// term's resolution 2^(e0 - 4(kTerms-1) - 9). Bits 16t .. 16t+15 of the result: term t of v0
+// (low byte) and of v1. A NaN value gives NaN bytes in every term.
+__device__ __forceinline__ uint64_t split2_fp8_fixed(float v0, float v1, int e0) {
+  uint64_t out = 0;
+#pragma unroll
+  for (int t = 0; t < kTerms; t++) {
+    const int e = e0 - 4 * t;
+    const int p = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v0, -e), ldexpf(v1, -e), 0, false);
+    v0 = v0 - ldexpf(__builtin_amdgcn_cvt_f32_fp8(p, 0), e);
+    v1 = v1 - ldexpf(__builtin_amdgcn_cvt_f32_fp8(p, 1), e);
+    out |= (uint64_t)(p & 0xFFFF) << (16 * t);
+  }
+  return out;
 }
 
 __device__ __forceinline__ void split8_fp8(const float x[8], uint2 q[kTerms], uint32_t &s4) {

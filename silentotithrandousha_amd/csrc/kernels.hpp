@@ -107,20 +107,23 @@ struct DecodeArgs {
 // One-launch single-token layer (decode_layer.hip): DecodeArgs plus the cross-block
 // signalling area (zeroed once at context creation and after a reported error; its logit copies
 // return to zero after every launch, its launch numbers and h flags only advance) and the
-// h-terms buffer (zeroed once; padding blocks stay zero).
+// h records of the four slots (zeroed once; the values past I stay zero).
 constexpr int kLayerMaxBlocks = 1024;
 struct LayerArgs {
   DecodeArgs d;
   void *sync;            // layer_sync_bytes() bytes
-  uint8_t *hterm;        // layer_hterm_bytes() bytes: per slot the fp8 terms of h + scales
+  uint8_t *hterm;        // layer_hterm_bytes() bytes: per slot the fp8 term rows of h
   uint32_t spin_limit;   // polls before a wait gives up
-  int n_gu_per_slot;     // filled by layer_geometry: gate_up tiles / 4 = h blocks of 32
-  int n_dn;              //                           down tiles
+  int hexp;              // filled by layer_geometry: exponent of the first h term
+  int n_tps;             // filled by layer_geometry: gate_up tiles per slot
+  int n_gu;              //                           gate_up blocks
+  int n_dn;              //                           down blocks = down tiles
   int n_rt;              //                           router blocks, ceil(E / 4)
 };
 size_t layer_sync_bytes();
 size_t layer_hterm_bytes();
-void layer_geometry(LayerArgs &la);
+int layer_hexp(float limit);
+void layer_geometry(LayerArgs &la, int n_cu);
 bool decode_layer_supported(const LayerArgs &la);
 hipError_t launch_decode_layer(const LayerArgs &a, hipStream_t s);
 

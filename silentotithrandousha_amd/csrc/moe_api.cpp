@@ -124,7 +124,8 @@ struct moe_ctx {
   int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 4 entries, 2 always, 0 never
   int gemm_shape = 0;  // grouped GEMM block shape override (tuning)
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
-  DevBuf layer_h;     // h terms of the one-launch kernel (padding stays zero)
+  DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
+  int n_cu = 256;     // compute units of the device (the one-launch grid is sized to it)
   uint32_t spin_limit = 1u << 20;
   std::vector<TimingRec> recs;
   std::vector<hipEvent_t> pool;
@@ -425,7 +426,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     la.sync = c->layer_sync.p;
     la.hterm = (uint8_t *)c->layer_h.p;
     la.spin_limit = c->spin_limit;
-    layer_geometry(la);
+    layer_geometry(la, c->n_cu);
     if (c->decode_mode == 2 && decode_layer_supported(la))
       return timed(c, K_DECODE_LAYER, s, [&] { return launch_decode_layer(la, s); });
     if (decode_supported(da)) {
@@ -535,6 +536,7 @@ int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ct
                 prop.gcnArchName);
   moe_ctx *c = new moe_ctx();
   c->dev = dev;
+  c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   c->H = hidden_size;
   c->I = inter_size;
   c->clamp = swiglu_clamp;

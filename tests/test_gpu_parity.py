@@ -453,6 +453,42 @@ def test_single_token_ties_and_nan_across_halves(orc, mode):
     d.close()
 
 
+@pytest.mark.parametrize("mode", MODES)
+def test_single_token_nonfinite_weights(orc, mode):
+    """E8M0 255 blocks (+inf in the reference decode, NaN in the OCP MX spec and to the
+    block-scaled MFMA). The contract on non-finite weights: every output the fp32 path makes
+    non-finite is non-finite here; where the fp32 path clamps an infinite intermediate back to a
+    finite value (SwiGLU's +-limit), the output is either that value (within tolerance) or NaN.
+    Case 1: +-inf on an up row (clamped to +-7 in the fp32 path). Case 2: nibbles -1.0 against a
+    positive x on a gate row of a chosen expert: gate = -inf, glu = -inf / inf = NaN, so that
+    expert's whole down product is NaN."""
+    H, I, E = 64, 64, 4
+    L = syn.make_layer(H, I, E, seed=370, scale_lo=120, scale_hi=124)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    x = (np.abs(syn.hidden(1, H, seed=371)) + 0.5).astype(np.float32)
+    gs = L["gu_scales"].copy()
+    gb = L["gu_blocks"].copy()
+    gs[:, 11, 0] = 255          # up row of h[5]
+    gb[:, 11, 0, :] = 0x22
+    L["gu_scales"], L["gu_blocks"] = gs, gb
+    d.preload_layer(0, L)
+    d.set_fused_decode(mode)
+    want, _, _, _ = orc.moe_layer(x, L, 2)
+    got = d.layer_forward(0, x, 2)
+    assert np.all(np.isfinite(want))
+    if not np.all(np.isnan(got)):
+        assert_rel_l2(got, want, f"clamped inf mode {mode}")
+    gs[1, 10, 0] = 255          # gate row of h[5] of expert 1
+    gb[1, 10, 0, :] = 0xAA
+    L["gu_scales"], L["gu_blocks"] = gs, gb
+    d.preload_layer(0, L)
+    want, _, idx, _ = orc.moe_layer(x, L, E)
+    got = d.layer_forward(0, x, E)
+    assert 1 in idx[0] and not np.any(np.isfinite(want))
+    assert not np.any(np.isfinite(got))
+    d.close()
+
+
 def test_one_launch_tiny_grids_in_sequence(orc):
     """A layer so small that the one-launch kernel has fewer blocks than logit copies (k gate_up
     blocks + 4 down blocks): consecutive tokens with different routings and k in one context
