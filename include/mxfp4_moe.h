@@ -79,9 +79,19 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * MFMA (activations as fp8 terms, exact to 2^-12) when 1 (default) and experts average at
  * least 4 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
  * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical.
- * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM for experts averaging 48+ entries: 0
- * (default) 8 wavefronts x 64 rows, 1 4 wavefronts x 128 rows (tuning; results identical). */
-enum moe_option { MOE_OPT_FUSED_DECODE = 1, MOE_OPT_SPIN_LIMIT = 2, MOE_OPT_BATCH_GEMM = 3, MOE_OPT_GEMM_SHAPE = 4 };
+ * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM: 0 (default) by the mean entries per
+ * expert; for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2;
+ * 2 and 3 force the 256-row x 32- and 16-entry blocks (tuning; results identical).
+ * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
+ * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results
+ * identical). */
+enum moe_option {
+  MOE_OPT_FUSED_DECODE = 1,
+  MOE_OPT_SPIN_LIMIT = 2,
+  MOE_OPT_BATCH_GEMM = 3,
+  MOE_OPT_GEMM_SHAPE = 4,
+  MOE_OPT_GEMM_BAND = 5
+};
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 
 /* ------------------------------------------------------------------ weights */

@@ -21,6 +21,7 @@ MOE_OPT_FUSED_DECODE = 1
 MOE_OPT_SPIN_LIMIT = 2
 MOE_OPT_BATCH_GEMM = 3
 MOE_OPT_GEMM_SHAPE = 4
+MOE_OPT_GEMM_BAND = 5
 
 _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p

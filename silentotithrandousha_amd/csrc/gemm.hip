@@ -25,29 +25,27 @@ using G = GemmRec;  // step-major activation record (kernels.hpp)
 
 // ------------------------------------------------------------------ fp6 activation terms
 
-// E2M3 (fp6: sign, 2 exponent bits with bias 1, 3 mantissa bits; no Inf/NaN, largest 7.5) code
-// of t, rounded to nearest even and saturated at 7.5; q = the value of the code. The grid is
-// 1/8 below 2, 1/4 in [2, 4), 1/2 in [4, 8): n = rint(|t| / grid) counts grid steps exactly,
-// and the code is n, n + 8 or n + 16 in the three ranges (n = 16 at a range's top is the next
-// range's first code).
-__device__ __forceinline__ uint32_t e2m3_rne(float t, float &q) {
-  const float a = fabsf(t);
-  const bool r0 = a < 2.0f, r1 = a < 4.0f;
-  const float inv = r0 ? 8.0f : (r1 ? 4.0f : 2.0f);
-  float n = rintf(a * inv);
-  if (!r1) n = fminf(n, 15.0f);
-  const uint32_t code = (uint32_t)n + (r0 ? 0u : (r1 ? 8u : 16u));
-  const float m = n * (r0 ? 0.125f : (r1 ? 0.25f : 0.5f));
-  q = t < 0.0f ? -m : m;
-  return code | (t < 0.0f ? 0x20u : 0u);
-}
+// E2M3 (fp6: sign, 2 exponent bits with bias 1, 3 mantissa bits; no Inf/NaN, largest 7.5)
+// conversion in hardware: v_cvt_scalef32_2xpk16_fp6_f32 divides 2 x 16 f32 by a power-of-two
+// scale and rounds each to the nearest E2M3 code, ties to even, saturating at +-7.5; output
+// field 2i is a[i], field 2i+1 is b[i] (value u of a 32-value group at bits 6u); the pk32 back
+// conversion returns the codes' values times the scale in field order. Measured on gfx950 against
+// a software RNE on every E2M3 grid point, every midpoint, values past 7.5, +-inf and random
+// values: identical codes except -0 for -0.0. The destination must not share registers with the
+// sources (register allocations that reuse the unused upper source registers for the result gave
+// wrong codes, deterministically), so both are issued as inline assembly with early-clobber
+// outputs.
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+typedef float f32x32v __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x6v __attribute__((ext_vector_type(6)));
 
 // Split of 16 values of a 32-value block (block max |x| = m, bad = some value of the block is
 // not finite) into kGemmTerms E2M3 terms: term t has scale 2^(E - 2 - 5t) where m = f 2^E,
 // f in [1/2, 1) (so term 0 holds the block in [-4, 4)), and takes the exact residual of the
 // terms before it (the activation is then exact to about 2^-13 of the block maximum). Codes of
 // value u at bits 6u of d[t][0..2]; sb byte t = the E8M0 scale of term t (0xFF, NaN, for a bad
-// block: the products come out NaN, as the f32 arithmetic would).
+// block: the products come out NaN, as the f32 arithmetic would). Scales stop at 2^-126 (a
+// normal f32) for blocks below about 2^-120.
 __device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool bad, uint32_t (&d)[kGemmTerms][3],
                                             uint32_t &sb) {
   int E = 0;
@@ -58,22 +56,24 @@ __device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool 
   sb = 0;
 #pragma unroll
   for (int t = 0; t < kGemmTerms; t++) {
-    const int se = max(E - 2 - 5 * t, -127);
+    const int se = max(E - 2 - 5 * t, -126);
     sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
-    uint64_t lo = 0, hi = 0;  // 96 bits: values 0..9 in lo (bits 0..59), 10..15 in hi (60..95)
+    const float sc = __builtin_amdgcn_ldexpf(1.0f, se);
+    f32x16v a = {}, b = {};
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      float q;
-      const uint32_t c = e2m3_rne(__builtin_amdgcn_ldexpf(r[i], -se), q);
-      r[i] = r[i] - __builtin_amdgcn_ldexpf(q, se);
-      if (i < 10)
-        lo |= (uint64_t)c << (6 * i);
-      else
-        hi |= (uint64_t)c << (6 * (i - 10));
+    for (int i = 0; i < 8; i++) {
+      a[i] = r[2 * i];
+      b[i] = r[2 * i + 1];
     }
-    d[t][0] = (uint32_t)lo;
-    d[t][1] = (uint32_t)(lo >> 32) | (uint32_t)(hi << 28);
-    d[t][2] = (uint32_t)(hi >> 4);
+    u32x6v c;
+    f32x32v q;
+    asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(c) : "v"(a), "v"(b), "v"(sc));
+    asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
+#pragma unroll
+    for (int i = 0; i < 16; i++) r[i] = r[i] - q[i];
+    d[t][0] = c[0];
+    d[t][1] = c[1];
+    d[t][2] = c[2];
   }
 }
 
@@ -256,12 +256,30 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   const int wr = wv % WR, wc = wv / WR;
   const int j = lane & 15, g = lane >> 4;
 
-  // ---- tile: global column tile cl (over the experts' kCols-entry tiles) and row block, row
-  //      blocks fastest, so neighbouring blocks share the entries' activation records.
+  // ---- tile: global column tile cl (over the experts' kCols-entry tiles) and row block rblk.
+  //      a.band == 0: workgroup p is tile p, row blocks fastest. a.band > 0: workgroups go to
+  //      the 8 XCDs round-robin (workgroup p to XCD p % 8), so XCD x takes the logical tiles
+  //      [x C, x C + C) in order, and logical tiles run in bands of a.band row blocks, column
+  //      tile by column tile. The orders differ by a few percent, by matrix (measured).
   //      Wavefront 0 finds the expert of tile cl: lanes read 64 experts' entry ranges at once,
   //      a prefix sum of their tile counts places cl.
+  int cl, rblk_l;
+  {
+    const int C = (a.n_tiles + 7) / 8;
+    const int L = a.band ? ((int)blockIdx.x % 8) * C + (int)blockIdx.x / 8 : (int)blockIdx.x;
+    if (L >= a.n_tiles) return;
+    const int nrb = a.n_row_blocks, nct = a.n_tiles / nrb, RB = a.band ? min(a.band, nrb) : nrb, full = nrb / RB;
+    if (L < full * RB * nct) {
+      const int band = L / (RB * nct), r = L - band * RB * nct;
+      cl = r / RB;
+      rblk_l = band * RB + r % RB;
+    } else {
+      const int rem = nrb - full * RB, r = L - full * RB * nct;
+      cl = r / rem;
+      rblk_l = full * RB + r % rem;
+    }
+  }
   if (wv == 0) {
-    const int cl = (int)blockIdx.x / a.n_row_blocks;
     const int na = min(*a.n_active, a.max_active);
     int ex = -1, beg = 0, cnt = 0, base = 0;
     for (int q0 = 0; q0 < na; q0 += 64) {
@@ -298,7 +316,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       s_tile[0] = ex;
       s_tile[1] = beg;
       s_tile[2] = cnt;
-      s_tile[3] = (int)blockIdx.x - cl * a.n_row_blocks;
+      s_tile[3] = rblk_l;
     }
   }
   __syncthreads();
@@ -512,8 +530,11 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
   a.n_row_blocks = (int)((a.d.rows + S::kRows - 1) / S::kRows);
   const size_t col_tiles = (size_t)a.max_active + (a.n_entries + S::kCols - 1) / S::kCols;
-  const size_t blocks = (size_t)a.n_row_blocks * col_tiles;
-  if (!blocks) return hipSuccess;
+  const size_t tiles = (size_t)a.n_row_blocks * col_tiles;
+  if (!tiles) return hipSuccess;
+  if (tiles > (size_t)INT32_MAX - 8) return hipErrorInvalidValue;
+  a.n_tiles = (int)tiles;
+  const size_t blocks = a.band ? (tiles + 7) / 8 * 8 : tiles;
   hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D>), dim3((unsigned)blocks), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
@@ -525,6 +546,8 @@ template <int MODE>
 static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   const size_t active = std::max<size_t>(1, std::min<size_t>((size_t)a.max_active, a.n_entries));
   const size_t mean = a.n_entries / active;
+  if (a.shape == 2) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3>(a, s);
+  if (a.shape == 3) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
   if (mean >= 48)
     return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2>(a, s);
   if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3>(a, s);

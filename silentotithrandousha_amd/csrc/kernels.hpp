@@ -78,7 +78,9 @@ struct GemmArgs {
   int max_active;            // upper bound of *n_active
   size_t n_entries;          // entries over all experts (sets the column tiles)
   int shape;                 // block shape override for tuning (0: by the mean entries per expert)
-  int n_row_blocks;          // set by launch_gemm_fp8 (row blocks of the launch)
+  int band;                  // row blocks per band of the XCD-local tile order (0: workgroup order)
+  int n_row_blocks;          // set by launch_gemm_fp8: row blocks of the launch
+  int n_tiles;               //                         row blocks x column tiles
 };
 hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *rec, hipStream_t s);
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);

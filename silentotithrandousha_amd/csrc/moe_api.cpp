@@ -123,6 +123,7 @@ struct moe_ctx {
   int decode_mode = 2;
   int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 4 entries, 2 always, 0 never
   int gemm_shape = 0;  // grouped GEMM block shape override (tuning)
+  int gemm_band = 0;   // grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
   int n_cu = 256;     // compute units of the device (the one-launch grid is sized to it)
@@ -483,6 +484,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     ga.max_active = max_active;
     ga.n_entries = N;
     ga.shape = c->gemm_shape;
+    ga.band = c->gemm_band;  // default: gate_up in workgroup order, down in XCD bands of 1 row block
     GemmArgs gu = ga;
     gu.mat_off = c->L.gu_off;
     gu.bias_off = c->L.gub_off;
@@ -492,6 +494,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     gu.out = c->w.hrec;
     RETURN_IF(timed(c, K_GATE_UP, s, [&] { return launch_gemm_fp8(GEMV_GATE_UP, gu, s); }));
     GemmArgs dn = ga;
+    if (!c->gemm_band) dn.band = 1;
     dn.mat_off = c->L.dn_off;
     dn.bias_off = c->L.dnb_off;
     dn.d = c->L.dn;
@@ -981,8 +984,12 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
       c->batch_gemm = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_SHAPE:
-      if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0 or 1");
+      if (value < 0 || value > 3) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..3");
       c->gemm_shape = (int)value;
+      return MOE_OK;
+    case MOE_OPT_GEMM_BAND:
+      if (value < 0 || value > 64) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_BAND is 0..64");
+      c->gemm_band = (int)value;
       return MOE_OK;
     case MOE_OPT_SPIN_LIMIT:
       if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");

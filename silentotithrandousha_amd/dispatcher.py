@@ -135,9 +135,14 @@ class GpuMoeDispatcher:
         check(lib().moe_set_option(self._ctx, MOE_OPT_BATCH_GEMM, int(mode)))
 
     def set_gemm_shape(self, shape):
-        """Grouped GEMM block shape for large batches (0 default, 1 alternative; tuning only)."""
+        """Grouped GEMM block shape (0 by batch size, 1..3 forced alternatives; tuning only)."""
         from ._ffi import MOE_OPT_GEMM_SHAPE
         check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_SHAPE, int(shape)))
+
+    def set_gemm_band(self, band):
+        """Row blocks per band of the grouped GEMM's per-XCD tile order (0 default; tuning only)."""
+        from ._ffi import MOE_OPT_GEMM_BAND
+        check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_BAND, int(band)))
 
     def set_spin_limit(self, polls):
         from ._ffi import MOE_OPT_SPIN_LIMIT
