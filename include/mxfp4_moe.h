@@ -44,7 +44,8 @@ enum moe_status {
   MOE_ERR_STATE = 2,     /* call out of order: layer / router / LM head not loaded */
   MOE_ERR_HIP = 3,       /* HIP runtime error (message names the call) */
   MOE_ERR_NO_DEVICE = 4, /* no gfx950 device visible */
-  MOE_ERR_OOM = 5        /* device allocation failed */
+  MOE_ERR_OOM = 5,       /* device allocation failed */
+  MOE_ERR_IO = 6         /* a file cannot be opened, mapped or parsed */
 };
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -130,6 +131,22 @@ int moe_preload_router(moe_ctx *ctx, size_t layer, size_t n_experts,
  * weights loaded through bf16_to_f32, weights.rs:141-147), else MOE_ERR_INVALID. */
 int moe_preload_router_f32(moe_ctx *ctx, size_t layer, size_t n_experts, const float *weight,
                            const float *bias);
+
+/* Safetensors MXFP4 loader — the reference's ShardReader (weights.rs:103-139) and the per-layer
+ * tensor names of load_weights (weights.rs:228-346), reading local shards instead of the hub
+ * download (weights.rs:168-213). Loads layer `layer`'s experts
+ *   model.layers.{layer}.mlp.experts.{gate_up,down}_proj_{blocks,scales} (U8) and _bias (BF16)
+ * and router model.layers.{layer}.mlp.router.{weight,bias} (BF16), each from the first shard
+ * that has it, checking dtype and shape against the context (E = n_experts, H, I); the experts
+ * go through moe_preload_layer straight from the memory-mapped shard (biases widened from bf16
+ * to f32, exactly), the router through moe_preload_router. MOE_ERR_IO: a shard cannot be opened
+ * or its header parsed; MOE_ERR_INVALID: a tensor is missing or has another dtype or shape. */
+int moe_load_safetensors_layer(moe_ctx *ctx, const char *const *shard_paths, size_t n_shards, size_t layer,
+                               size_t n_experts);
+/* Header lookup (no device needed): dtype (NUL-terminated, truncated to dtype_cap), rank, the
+ * first shape_cap dimensions and the tensor's byte range [begin, end) in the file. */
+int moe_safetensors_find(const char *path, const char *name, char *dtype, size_t dtype_cap, uint64_t *shape,
+                         size_t shape_cap, size_t *rank, uint64_t *begin, uint64_t *end);
 
 /* ------------------------------------------------------------------ per-expert dispatch */
 

@@ -16,6 +16,7 @@ MOE_ERR_STATE = 2
 MOE_ERR_HIP = 3
 MOE_ERR_NO_DEVICE = 4
 MOE_ERR_OOM = 5
+MOE_ERR_IO = 6
 
 MOE_OPT_FUSED_DECODE = 1
 MOE_OPT_SPIN_LIMIT = 2
@@ -62,6 +63,10 @@ SIGNATURES = {
                                   _vp, _sz, _vp, _sz]),
     "moe_preload_router": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "moe_preload_router_f32": (_int, [_vp, _sz, _sz, _vp, _vp]),
+    "moe_load_safetensors_layer": (_int, [_vp, ctypes.POINTER(ctypes.c_char_p), _sz, _sz, _sz]),
+    "moe_safetensors_find": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _sz,
+                                    ctypes.POINTER(ctypes.c_uint64), _sz, ctypes.POINTER(_sz),
+                                    ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "moe_dispatch_expert_preloaded": (_int, [_vp, _vp, _sz, _sz, _vp]),
     "moe_dispatch_expert": (_int, [_vp, _vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz,
                                    _vp, _sz, _vp]),

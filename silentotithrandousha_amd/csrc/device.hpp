@@ -41,6 +41,16 @@ __device__ __forceinline__ float rclamp(float v, float lo, float hi) {
   return v;
 }
 
+// swiglu with the hardware exponential (v_exp_f32 on x log2(e), ~1 ulp) and reciprocal instead
+// of the correctly rounded expf and division: for the grouped GEMM, whose h then enters as three
+// fp6 terms (relative error ~1e-5), so the last bits of h do not reach the output.
+__device__ __forceinline__ float swiglu_fast(float g, float u, float limit) {
+  float gate = g != g ? g : fminf(g, limit);
+  float up = rclamp(u, -limit, limit);
+  float glu = gate * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gate * (-1.702f * 1.4426950408889634f)));
+  return (up + 1.0f) * glu;
+}
+
 // E2M1 nibble -> f32 bits: sign | (e == 0 ? 0.5*m : 2^(e-1) * (1 + m/2)).
 __device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
   uint32_t mag = n & 7u;

@@ -458,7 +458,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
           const f32x4 &av = acc[4 * hbk + r][c];
           const float4 &b4 = bv[4 * hbk + r];
           *reinterpret_cast<float2 *>(se + 8 * r + 2 * g) =
-              make_float2(swiglu(av[0] + b4.x, av[1] + b4.y, a.limit), swiglu(av[2] + b4.z, av[3] + b4.w, a.limit));
+              make_float2(swiglu_fast(av[0] + b4.x, av[1] + b4.y, a.limit), swiglu_fast(av[2] + b4.z, av[3] + b4.w, a.limit));
         }
       }
       const int st = hb >> 2, i = hb & 3;

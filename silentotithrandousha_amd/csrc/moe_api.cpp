@@ -1070,3 +1070,15 @@ int moe_reset_timing(moe_ctx *c) {
 }
 
 }  // extern "C"
+
+// For the library's other host sources (safetensors.cpp): record the failure message that
+// moe_last_error returns, and read a context's dimensions.
+namespace moe {
+int api_fail(int code, const char *msg) { return fail(code, "%s", msg); }
+int ctx_dims(const moe_ctx *c, size_t *H, size_t *I) {
+  if (!c) return fail(MOE_ERR_INVALID, "null context");
+  *H = c->H;
+  *I = c->I;
+  return MOE_OK;
+}
+}  // namespace moe

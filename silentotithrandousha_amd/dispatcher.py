@@ -108,6 +108,18 @@ class GpuMoeDispatcher:
                                            _p(_c(layer["router_w"], np.uint16)),
                                            _p(_c(layer["router_b"], np.float32))))
 
+    def load_safetensors_layer(self, shards, layer_idx, n_experts):
+        """Layer `layer_idx`'s experts and router from local safetensors shards (the reference's
+        ShardReader and tensor names, weights.rs:103-139, 228-346). `shards`: a directory (every
+        *.safetensors in it, sorted, as the reference sorts the shard names) or a list of paths."""
+        import os
+        if isinstance(shards, (str, os.PathLike)) and os.path.isdir(shards):
+            shards = sorted(os.path.join(shards, f) for f in os.listdir(shards) if f.endswith(".safetensors"))
+        elif isinstance(shards, (str, os.PathLike)):
+            shards = [shards]
+        paths = (ctypes.c_char_p * len(shards))(*[os.fsencode(p) for p in shards])
+        check(lib().moe_load_safetensors_layer(self._ctx, paths, len(shards), layer_idx, n_experts))
+
     def preload_experts(self, layers):
         """preload_experts(&layers, &config) — all layers, index = position."""
         for i, layer in enumerate(layers):
@@ -277,3 +289,16 @@ def mxfp4_pack(blocks_dev, scales_dev, rows, cols):
 def mxfp4_matvec(disp, packed_dev, rows, cols, x_dev, y_dev, stream=None):
     check(lib().moe_mxfp4_matvec_device(disp.ctx, packed_dev.ptr, rows, cols, x_dev.ptr,
                                         y_dev.ptr, stream))
+
+
+def safetensors_find(path, name):
+    """Header entry of tensor `name` in a safetensors file: (dtype, shape, (begin, end)) with the
+    byte range in the file. Needs no device."""
+    import os
+    dt = ctypes.create_string_buffer(16)
+    shape = (ctypes.c_uint64 * 8)()
+    rank = ctypes.c_size_t()
+    b, e = ctypes.c_uint64(), ctypes.c_uint64()
+    check(lib().moe_safetensors_find(os.fsencode(path), name.encode(), dt, 16, shape, 8, ctypes.byref(rank),
+                                     ctypes.byref(b), ctypes.byref(e)))
+    return dt.value.decode(), tuple(shape[i] for i in range(min(rank.value, 8))), (b.value, e.value)

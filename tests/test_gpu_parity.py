@@ -589,3 +589,45 @@ def test_batch_gemm_adaptive_dropped_slots(orc):
     assert (idx < 0).any()
     assert_rel_l2(d.layer_forward(0, xs, 4), want, "adaptive batch gemm")
     d.close()
+
+
+# ---------------------------------------------------------------- safetensors loader
+
+def test_load_safetensors_layer(orc, tmp_path):
+    """A checkpoint layer in GPT-OSS tensor names (weights.rs:262-283), split over two shards
+    (experts in one, router in the other, as the reference searches every shard): loaded through
+    moe_load_safetensors_layer it gives the same bits as preload_layer on the decoded tensors
+    (bf16 biases widened to f32), both within tolerance of the oracle; a wrong shape is refused
+    naming the tensor."""
+    from tests.helpers import gpt_oss_layer_tensors, write_safetensors
+    from silentotithrandousha_amd._ffi import MoeError
+    H, I, E, li = 64, 64, 8, 3
+    L = syn.make_layer(H, I, E, seed=400)
+    L["gu_bias"] = syn.bf16_round(L["gu_bias"])
+    L["d_bias"] = syn.bf16_round(L["d_bias"])
+    t = gpt_oss_layer_tensors(L, li)
+    experts = {k: v for k, v in t.items() if ".experts." in k}
+    router = {k: v for k, v in t.items() if ".router." in k}
+    write_safetensors(tmp_path / "model-00001-of-00002.safetensors", experts, metadata={"format": "pt"})
+    write_safetensors(tmp_path / "model-00002-of-00002.safetensors", router, pad=7)
+    x = syn.hidden(3, H, seed=401)
+    d1 = GpuMoeDispatcher(H, I, 7.0)
+    d1.load_safetensors_layer(str(tmp_path), li, E)
+    d2 = GpuMoeDispatcher(H, I, 7.0)
+    d2.preload_layer(li, L)
+    for mode in (2, 0):
+        d1.set_fused_decode(mode)
+        d2.set_fused_decode(mode)
+        for T in (1, 3):
+            got = d1.layer_forward(li, x[:T], 4)
+            assert_bit_exact(got, d2.layer_forward(li, x[:T], 4), f"loader vs preload mode {mode} T={T}")
+            want, _, _, _ = orc.moe_layer(x[:T], L, 4)
+            assert_rel_l2(got, want, f"loader vs oracle mode {mode} T={T}")
+    bad = dict(experts)
+    k = f"model.layers.{li}.mlp.experts.down_proj_scales"
+    bad[k] = ("U8", L["d_scales"][:, :, :1], (E, H, 1))
+    write_safetensors(tmp_path / "bad.safetensors", bad)
+    with pytest.raises(MoeError, match="down_proj_scales"):
+        d1.load_safetensors_layer([str(tmp_path / "bad.safetensors"), str(tmp_path / "model-00002-of-00002.safetensors")], li, E)
+    d1.close()
+    d2.close()
