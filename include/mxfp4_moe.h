@@ -132,6 +132,11 @@ int moe_preload_router(moe_ctx *ctx, size_t layer, size_t n_experts,
 int moe_preload_router_f32(moe_ctx *ctx, size_t layer, size_t n_experts, const float *weight,
                            const float *bias);
 
+/* Post-attention RMSNorm weight of one layer (LayerWeights::post_attn_layernorm_weight,
+ * weights.rs:32, loaded at weights.rs:267-268, bf16 widened to f32) and
+ * GptOssConfig::rms_norm_eps (config.rs:42-43, default 1e-5 at :59-61). */
+int moe_preload_norm(moe_ctx *ctx, size_t layer, const float *gamma, float eps);
+
 /* Safetensors MXFP4 loader — the reference's ShardReader (weights.rs:103-139) and the per-layer
  * tensor names of load_weights (weights.rs:228-346), reading local shards instead of the hub
  * download (weights.rs:168-213). Loads layer `layer`'s experts
@@ -139,10 +144,12 @@ int moe_preload_router_f32(moe_ctx *ctx, size_t layer, size_t n_experts, const f
  * and router model.layers.{layer}.mlp.router.{weight,bias} (BF16), each from the first shard
  * that has it, checking dtype and shape against the context (E = n_experts, H, I); the experts
  * go through moe_preload_layer straight from the memory-mapped shard (biases widened from bf16
- * to f32, exactly), the router through moe_preload_router. MOE_ERR_IO: a shard cannot be opened
- * or its header parsed; MOE_ERR_INVALID: a tensor is missing or has another dtype or shape. */
+ * to f32, exactly), the router through moe_preload_router; and, when the shards hold it,
+ * model.layers.{layer}.post_attention_layernorm.weight (BF16 [H]) through moe_preload_norm with
+ * rms_norm_eps. MOE_ERR_IO: a shard cannot be opened or its header parsed; MOE_ERR_INVALID: a
+ * tensor is missing or has another dtype or shape. */
 int moe_load_safetensors_layer(moe_ctx *ctx, const char *const *shard_paths, size_t n_shards, size_t layer,
-                               size_t n_experts);
+                               size_t n_experts, float rms_norm_eps);
 /* Header lookup (no device needed): dtype (NUL-terminated, truncated to dtype_cap), rank, the
  * first shape_cap dimensions and the tensor's byte range [begin, end) in the file. */
 int moe_safetensors_find(const char *path, const char *name, char *dtype, size_t dtype_cap, uint64_t *shape,
@@ -223,6 +230,19 @@ int moe_layer_forward(moe_ctx *ctx, size_t layer, const float *x, size_t n_token
 int moe_layer_forward_device(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens,
                              size_t top_k, float *y, void *stream);
 
+/* The MoE block with the post-attention RMSNorm before it and the residual add after it: the
+ * router fusion of build_decode_output_proj_router (executables.rs:260-317: router(RMSNorm(h)))
+ * in the fp32 form of session.rs:483-493, and the residual add of session.rs:982-994:
+ * out = x + MoE(n), n = (x * inv_rms) * gamma, inv_rms = 1 / sqrt(sum(x^2) / H + eps).
+ * The sum of squares is taken in a fixed order (64 lane-strided partial sums combined by a xor
+ * butterfly) rather than the reference's sequential one, so inv_rms can differ from it in the
+ * last bit; the single-token one-launch kernel fuses the norm into its router and gate_up blocks
+ * and the residual into its combine. Needs moe_preload_norm. x, out: [n_tokens, H]. */
+int moe_block_forward(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens, size_t top_k,
+                      float *out);
+int moe_block_forward_device(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens,
+                             size_t top_k, float *out, void *stream);
+
 /* ------------------------------------------------------------------ MXFP4 primitives */
 
 /* dequant_mxfp4_row / dequant_expert_{gate_up,down}_into — weights.rs:350-423, bit-exact:
@@ -283,7 +303,8 @@ int moe_graph_destroy(void *graph_exec);
 int moe_set_timing(moe_ctx *ctx, int enabled);
 /* kernel: 0 route, 1 bucket, 2 gate_up, 3 down, 4 combine, 5 single-token router+gate_up,
  * 6 single-token down+combine, 7 single-token layer in one launch, 8 activation split of a
- * batch (grouped GEMM path; kernels 2 and 3 are then the grouped GEMMs).
+ * batch (grouped GEMM path; kernels 2 and 3 are then the grouped GEMMs), 9 RMSNorm and residual
+ * add of moe_block_forward where they are not fused.
  * Returns accumulated milliseconds
  * and launch count since the last reset; synchronises the context stream. */
 int moe_get_timing(moe_ctx *ctx, int kernel, double *ms, uint64_t *launches);

@@ -389,6 +389,50 @@ void orc_combine(const float *outs, const float *w, size_t n, size_t H, int skip
   }
 }
 
+float orc_rms_inv(const float *x, size_t H, float eps) {
+  float p[64];
+  for (size_t l = 0; l < 64; l++) {
+    float a = 0.0f;
+    for (size_t i = l; i < H; i += 64) {
+      const float sq = x[i] * x[i];
+      a = a + sq;
+    }
+    p[l] = a;
+  }
+  for (size_t o = 32; o >= 1; o >>= 1) {
+    float q[64];
+    for (size_t l = 0; l < 64; l++) q[l] = p[l] + p[l ^ o];
+    memcpy(p, q, sizeof(p));
+  }
+  const float mean = p[0] / (float)H;
+  return 1.0f / sqrtf(mean + eps); /* session.rs:487: (mean_sq + eps).sqrt().recip() */
+}
+
+void orc_rms_norm(const float *x, size_t T, size_t H, const float *gamma, float eps, float *n) {
+  for (size_t t = 0; t < T; t++) {
+    const float r = orc_rms_inv(x + t * H, H, eps);
+    for (size_t d = 0; d < H; d++) {
+      const float v = x[t * H + d] * r; /* session.rs:491: hidden * inv_rms * gamma, left to right */
+      n[t * H + d] = v * gamma[d];
+    }
+  }
+}
+
+void orc_moe_block_f32(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k, float limit,
+                       const float *gamma, float eps, const uint16_t *router_w_bf16, const float *router_b,
+                       const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                       const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                       const orc_adaptive *ad, float *out, float *logits, int32_t *idx, float *w) {
+  float *n = (float *)malloc(T * H * sizeof(float));
+  float *y = (float *)malloc(T * H * sizeof(float));
+  orc_rms_norm(x, T, H, gamma, eps, n);
+  orc_moe_layer_f32(n, T, H, I, E, k, limit, router_w_bf16, router_b, gu_blocks, gu_scales, gu_bias, d_blocks,
+                    d_scales, d_bias, ad, y, logits, idx, w);
+  for (size_t i = 0; i < T * H; i++) out[i] = canon(x[i] + y[i]); /* session.rs:982-994 residual add */
+  free(n);
+  free(y);
+}
+
 void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k,
                        float limit, const uint16_t *router_w_bf16, const float *router_b,
                        const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,

@@ -111,6 +111,24 @@ void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, s
                        const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
                        const orc_adaptive *ad, float *y, float *logits, int32_t *idx, float *w);
 
+/* Post-attention RMSNorm of the reference's fp32 restatement (session.rs:483-493):
+ * inv_rms = 1 / sqrt(mean(x^2) + eps) (mean = sum / H, sqrt and reciprocal correctly rounded),
+ * n[d] = (x[d] * inv_rms) * gamma[d]. The sum of squares runs in the canonical order of the GPU
+ * kernels, not the reference's sequential one (they differ by rounding only): 64 lane partials
+ * p_l = sum over i ascending of x[l + 64 i]^2, then the xor butterfly p_l += p_(l^o) for
+ * o = 32, 16, 8, 4, 2, 1 (every lane ends with the same bits: each step adds a commuted pair). */
+float orc_rms_inv(const float *x, size_t H, float eps);
+void orc_rms_norm(const float *x, size_t T, size_t H, const float *gamma, float eps, float *n);
+
+/* The MoE block with the norm and residual around it (executables.rs:260-317 router fusion,
+ * session.rs:483-493, 943-997): n = RMSNorm(x) * gamma, y = MoE(n) as orc_moe_layer_f32,
+ * out = x + y. */
+void orc_moe_block_f32(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k, float limit,
+                       const float *gamma, float eps, const uint16_t *router_w_bf16, const float *router_b,
+                       const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                       const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                       const orc_adaptive *ad, float *out, float *logits, int32_t *idx, float *w);
+
 /* session.rs:974-980 combine: y[d] = 0; y[d] += w_s * out_s[d] for slots in rank order.
  * skip_nonfinite = 1 gives the moe_dispatch.rs:594-603 variant (non-finite out_s[d] skipped). */
 void orc_combine(const float *outs, const float *w, size_t n, size_t H, int skip_nonfinite,

@@ -65,6 +65,12 @@ def lib():
                                     _u8p, _u8p, _f32p, _u8p, _u8p, _f32p, ctypes.c_void_p, _f32p,
                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     L.orc_combine.argtypes = [_f32p, _f32p, _sz, _sz, ctypes.c_int, _f32p]
+    L.orc_rms_inv.argtypes = [_f32p, _sz, ctypes.c_float]
+    L.orc_rms_inv.restype = ctypes.c_float
+    L.orc_rms_norm.argtypes = [_f32p, _sz, _sz, _f32p, ctypes.c_float, _f32p]
+    L.orc_moe_block_f32.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_float, _f32p, ctypes.c_float,
+                                    _u16p, _f32p, _u8p, _u8p, _f32p, _u8p, _u8p, _f32p, ctypes.c_void_p, _f32p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     L.orc_matvec_f16xf32.argtypes = [_u16p, _f32p, _f32p, _sz, _sz]
     L.orc_live_moe_token.argtypes = [_f32p, _sz, _sz, _sz, _i32p, _f32p, _u8p, _u8p, _f32p, _u8p,
                                      _u8p, _f32p, ctypes.c_int, _f32p]
@@ -171,6 +177,42 @@ def moe_layer(x, layer, k, limit=7.0, adaptive=None):
                             _c(layer["d_bias"], np.float32).reshape(-1), ad, y.reshape(-1),
                             _ptr(logits), _ptr(idx), _ptr(w))
     return y, logits, idx, w
+
+
+def rms_inv(x, eps=1e-5):
+    """1 / sqrt(mean(x^2) + eps) in the canonical lane-butterfly order (session.rs:483-487)."""
+    x = _c(x, np.float32).reshape(-1)
+    return lib().orc_rms_inv(x, x.size, eps)
+
+
+def rms_norm(x, gamma, eps=1e-5):
+    """session.rs:483-493: (x * inv_rms) * gamma per row."""
+    gamma = _c(gamma, np.float32)
+    H = gamma.size
+    x = _c(x, np.float32).reshape(-1, H)
+    n = np.empty_like(x)
+    lib().orc_rms_norm(x.reshape(-1), x.shape[0], H, gamma, eps, n.reshape(-1))
+    return n
+
+
+def moe_block(x, layer, k, gamma, eps=1e-5, limit=7.0, adaptive=None):
+    """x + MoE(RMSNorm(x) * gamma): the norm and residual around the path (executables.rs:260-317,
+    session.rs:483-493, 982-994). Returns (out, logits, idx, w)."""
+    H, I, E = layer["H"], layer["I"], layer["E"]
+    x = _c(x, np.float32).reshape(-1, H)
+    T = x.shape[0]
+    out = np.empty((T, H), np.float32)
+    logits = np.empty((T, E), np.float32)
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    ad = ctypes.byref(adaptive) if adaptive is not None else None
+    lib().orc_moe_block_f32(x.reshape(-1), T, H, I, E, k, limit, _c(gamma, np.float32), eps,
+                            _c(layer["router_w"], np.uint16).reshape(-1), _c(layer["router_b"], np.float32).reshape(-1),
+                            _c(layer["gu_blocks"], np.uint8).reshape(-1), _c(layer["gu_scales"], np.uint8).reshape(-1),
+                            _c(layer["gu_bias"], np.float32).reshape(-1), _c(layer["d_blocks"], np.uint8).reshape(-1),
+                            _c(layer["d_scales"], np.uint8).reshape(-1), _c(layer["d_bias"], np.float32).reshape(-1),
+                            ad, out.reshape(-1), _ptr(logits), _ptr(idx), _ptr(w))
+    return out, logits, idx, w
 
 
 def combine(outs, w, skip_nonfinite=False):

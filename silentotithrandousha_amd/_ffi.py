@@ -63,7 +63,10 @@ SIGNATURES = {
                                   _vp, _sz, _vp, _sz]),
     "moe_preload_router": (_int, [_vp, _sz, _sz, _vp, _vp]),
     "moe_preload_router_f32": (_int, [_vp, _sz, _sz, _vp, _vp]),
-    "moe_load_safetensors_layer": (_int, [_vp, ctypes.POINTER(ctypes.c_char_p), _sz, _sz, _sz]),
+    "moe_load_safetensors_layer": (_int, [_vp, ctypes.POINTER(ctypes.c_char_p), _sz, _sz, _sz, _f]),
+    "moe_preload_norm": (_int, [_vp, _sz, _vp, _f]),
+    "moe_block_forward": (_int, [_vp, _sz, _vp, _sz, _sz, _vp]),
+    "moe_block_forward_device": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _vp]),
     "moe_safetensors_find": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _sz,
                                     ctypes.POINTER(ctypes.c_uint64), _sz, ctypes.POINTER(_sz),
                                     ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),

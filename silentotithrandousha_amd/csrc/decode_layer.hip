@@ -322,6 +322,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
   __shared__ int s_flag;
   __shared__ uint32_t s_ep;
   __shared__ int s_wfail[1];
+  __shared__ float s_rinv;
   __shared__ float s_o[4][16];
   __shared__ __align__(16) uint8_t s_hp[32 * (kLayerWaves + 1)];  // h record pieces of a gate_up block's tiles
   __shared__ __align__(16) float s_xp[kLayerWaves][16];             // the extra tile's partial sums
@@ -346,6 +347,20 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
       for (int i = 0; i < XI; i++)
         if (lane + 64 * i >= H) xr[i] = 0.0f;
+      if (la.gamma) {  // the block forward: the router reads RMSNorm(x) gamma (rms_inv_wave's order)
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+          const float sq = xr[i] * xr[i];
+          p = p + sq;
+        }
+        const float r = 1.0f / sqrtf(wave_sum_xor(p) / (float)H + la.eps);
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+          const float v = xr[i] * r;
+          xr[i] = lane + 64 * i < H ? v * la.gamma[min(lane + 64 * i, H - 1)] : 0.0f;
+        }
+      }
       const float lg = router_logit<RNQ>(a.rw, a.rb, xr, e, lane);
       if (lane < nrep) st_agent64(&logit_copy(la.sync, lane)->logit[e], (1ull << 32) | __float_as_uint(lg));
     }
@@ -368,6 +383,13 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
     // 1. x as kTerms fp8 terms in LDS, 8 values per thread (a quad of lanes = one 32-block);
     //    blocks past H up to nbpx are zeros.
     uint8_t *s_x = reinterpret_cast<uint8_t *>(smem);  // activation record of x
+    if (la.gamma) {  // the block forward: x is RMSNorm(x) gamma; wavefront 0 finds 1 / rms
+      if (wv == 0) {
+        const float r = rms_inv_wave(a.x, H, la.eps, lane);
+        if (lane == 0) s_rinv = r;
+      }
+      __syncthreads();
+    }
     for (int u = tid; u < 16 * kLayerNs; u += kLayerThreads) {  // uniform trip count per quad
       float xv[8];
       if (8 * u < H) {
@@ -375,6 +397,17 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
         const float4 v1 = reinterpret_cast<const float4 *>(a.x)[2 * u + 1];
         xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
         xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+        if (la.gamma) {
+          const float r = s_rinv;
+          const float4 g0 = reinterpret_cast<const float4 *>(la.gamma)[2 * u];
+          const float4 g1 = reinterpret_cast<const float4 *>(la.gamma)[2 * u + 1];
+          const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const float v = xv[i] * r;
+            xv[i] = v * gv[i];
+          }
+        }
       } else {
 #pragma unroll
         for (int i = 0; i < 8; i++) xv[i] = 0.0f;
@@ -616,6 +649,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
       for (int s = 0; s < 4 && s < K; s++)
         if (s < sel) y = y + s_w[s] * s_o[s][tid];
     }
+    if (la.gamma) y = a.x[t * 16 + tid] + y;  // the block forward's residual (session.rs:982-994)
     a.y[t * 16 + tid] = canon_nan(y);
   }
   MOE_TRACE(4);

@@ -119,6 +119,21 @@ __device__ __forceinline__ float wave_sum_xor(float p) {
   return p;
 }
 
+// 1 / sqrt(sum(x^2) / H + eps) of a row, every lane of the wavefront taking part: lane l sums
+// x[l + 64 i]^2 over i ascending (squares rounded, then added), the xor butterfly of
+// wave_sum_xor combines the 64 partial sums (each step adds a commuted pair, so every lane holds
+// the same bits), then the mean, sqrt and reciprocal, each correctly rounded (session.rs:483-487
+// up to the order of the sum).
+__device__ __forceinline__ float rms_inv_wave(const float *x, int H, float eps, int lane) {
+  float p = 0.0f;
+  for (int i = lane; i < H; i += 64) {
+    const float sq = x[i] * x[i];
+    p = p + sq;
+  }
+  const float mean = wave_sum_xor(p) / (float)H;
+  return 1.0f / sqrtf(mean + eps);
+}
+
 __device__ __forceinline__ float wave_max(float m) {
   m = fmaxf(m, xor_lane<32>(m));
   m = fmaxf(m, xor_lane<16>(m));

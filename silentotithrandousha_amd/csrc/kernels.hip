@@ -682,6 +682,42 @@ __global__ __launch_bounds__(256) void k_lm_head(const float *w, const float *x,
   if (lane == 0) y[row] = acc;
 }
 
+// ------------------------------------------------------------------ RMSNorm and residual
+
+// n[t] = (x[t] * inv_rms) * gamma, one wavefront per row (session.rs:483-493, the sum of squares
+// in rms_inv_wave's order).
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *x, int T, int H, const float *gamma, float eps,
+                                                 float *n) {
+  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float *xr = x + (size_t)t * H;
+  const float r = rms_inv_wave(xr, H, eps, lane);
+  for (int d = lane; d < H; d += 64) {
+    const float v = xr[d] * r;
+    n[(size_t)t * H + d] = v * gamma[d];
+  }
+}
+
+hipError_t launch_rmsnorm(const float *x, size_t T, size_t H, const float *gamma, float eps, float *n,
+                          hipStream_t s) {
+  if (!T) return hipSuccess;
+  if (H > (size_t)INT32_MAX || T > (size_t)INT32_MAX / 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, x, (int)T, (int)H, gamma, eps, n);
+  return hipGetLastError();
+}
+
+// y = x + y (session.rs:982-994: hidden + moe_out), NaN canonical.
+__global__ __launch_bounds__(256) void k_add_rows(float *y, const float *x, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = canon_nan(x[i] + y[i]);
+}
+
+hipError_t launch_add_rows(float *y, const float *x, size_t n, hipStream_t s) {
+  if (!n) return hipSuccess;
+  hipLaunchKernelGGL(k_add_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, x, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_lm_head(const float *w, const float *x, size_t vocab, size_t H, float *y,
                           hipStream_t s) {
   if (H % 4 || !vocab) return hipErrorInvalidValue;

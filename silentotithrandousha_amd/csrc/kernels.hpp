@@ -117,6 +117,8 @@ struct LayerArgs {
   uint8_t *hterm;        // layer_hterm_bytes() bytes: per slot the fp8 term rows of h
   uint32_t spin_limit;   // polls before a wait gives up
   int hexp;              // filled by layer_geometry: exponent of the first h term
+  const float *gamma;    // non-null: the block forward (RMSNorm of d.x before, d.x + y after)
+  float eps;
   int n_tps;             // filled by layer_geometry: gate_up tiles per slot
   int n_gu;              //                           gate_up blocks
   int n_dn;              //                           down blocks = down tiles
@@ -151,5 +153,9 @@ hipError_t launch_synth(void *dst, size_t n, int kind, uint64_t seed, float a, f
                         hipStream_t s);
 hipError_t launch_lm_head(const float *w, const float *x, size_t vocab, size_t H, float *y,
                           hipStream_t s);
+// Post-attention RMSNorm of T rows (rms_inv_wave's order) and the residual add y += x.
+hipError_t launch_rmsnorm(const float *x, size_t T, size_t H, const float *gamma, float eps, float *n,
+                          hipStream_t s);
+hipError_t launch_add_rows(float *y, const float *x, size_t n, hipStream_t s);
 
 }  // namespace moe

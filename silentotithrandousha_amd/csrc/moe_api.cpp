@@ -75,11 +75,14 @@ struct Layer {
   size_t n_loaded = 0;
   DevBuf router;   // load-major bf16 [E][KIp/8][64][8] then [E] f32
   size_t router_experts = 0;
+  DevBuf norm;     // post-attention RMSNorm weight, f32 [H]
+  float eps = 0.0f;
+  bool has_norm = false;
 };
 
 // Per-call device scratch, carved from one allocation.
 struct Work {
-  float *x, *y, *logits, *wts, *o;
+  float *x, *y, *logits, *wts, *o, *xn;  // xn: normalised rows of the block forward
   uint16_t *xsplit, *hsplit;
   uint8_t *xrec, *hrec;  // grouped GEMM activation records: tokens, entries (padding zero)
   int32_t *idx, *n_active, *active_ids, *active_off, *entry_src, *pos;
@@ -87,7 +90,7 @@ struct Work {
 
 enum {
   K_ROUTE = 0, K_BUCKET, K_GATE_UP, K_DOWN, K_COMBINE, K_DECODE_GATE_UP, K_DECODE_DOWN,
-  K_DECODE_LAYER, K_SPLIT, K_COUNT
+  K_DECODE_LAYER, K_SPLIT, K_NORM, K_COUNT
 };
 
 struct TimingRec {
@@ -203,6 +206,7 @@ int ensure_work(moe_ctx *c, size_t T, size_t k, size_t E) {
   size_t off = 0;
   size_t o_x = off; off = al(off + T * H * 4);
   size_t o_y = off; off = al(off + T * H * 4);
+  size_t o_xn = off; off = al(off + T * H * 4);
   size_t o_lg = off; off = al(off + T * E * 4);
   size_t o_wt = off; off = al(off + N * 4);
   size_t o_o = off; off = al(off + N * H * 4);
@@ -224,6 +228,7 @@ int ensure_work(moe_ctx *c, size_t T, size_t k, size_t E) {
   c->w.hrec = (uint8_t *)(b + o_hr);
   c->w.x = (float *)(b + o_x);
   c->w.y = (float *)(b + o_y);
+  c->w.xn = (float *)(b + o_xn);
   c->w.logits = (float *)(b + o_lg);
   c->w.wts = (float *)(b + o_wt);
   c->w.o = (float *)(b + o_o);
@@ -377,8 +382,10 @@ int set_single_token_list(moe_ctx *c, size_t n, const int32_t *ids) {
   return MOE_OK;
 }
 
+// norm: the block forward (RMSNorm of x before, x + result after); the one-launch decode fuses
+// both, the other paths run k_rmsnorm into the workspace first and k_add_rows last.
 int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k, float *y,
-                   hipStream_t s) {
+                   hipStream_t s, bool norm = false) {
   RETURN_IF(check_layer(c, layer, true));
   Layer &Ly = c->layers[layer];
   const size_t E = Ly.n_experts;
@@ -391,6 +398,19 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     return fail(MOE_ERR_INVALID, "top_k %zu outside [1, min(%d, %zu)]", k, kMaxTopK, E);
   if (T > (size_t)1 << 20) return fail(MOE_ERR_INVALID, "n_tokens %zu too large", T);
   RETURN_IF(ensure_work(c, T, k, E));
+  if (norm && !Ly.has_norm) return fail(MOE_ERR_STATE, "layer %zu has no RMSNorm weight", layer);
+  const float *resid = nullptr;  // x for the residual add of the unfused paths
+  if (norm) {
+    const bool fused = T == 1 && c->decode_mode == 2;
+    if (!fused || (reinterpret_cast<uintptr_t>(x) & 15)) {
+      RETURN_IF(timed(c, K_NORM, s, [&] {
+        return launch_rmsnorm(x, T, c->H, (const float *)Ly.norm.p, Ly.eps, c->w.xn, s);
+      }));
+      resid = x;
+      x = c->w.xn;
+      norm = false;
+    }
+  }
   if (T == 1 && c->decode_mode > 0) {
     DecodeArgs da{};
     da.rw = (const uint16_t *)Ly.router.p;
@@ -427,12 +447,26 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     la.sync = c->layer_sync.p;
     la.hterm = (uint8_t *)c->layer_h.p;
     la.spin_limit = c->spin_limit;
+    if (norm) {
+      la.gamma = (const float *)Ly.norm.p;
+      la.eps = Ly.eps;
+    }
     layer_geometry(la, c->n_cu);
     if (c->decode_mode == 2 && decode_layer_supported(la))
       return timed(c, K_DECODE_LAYER, s, [&] { return launch_decode_layer(la, s); });
+    if (norm) {  // the fused kernel refused the shape: normalise first, add the residual last
+      RETURN_IF(timed(c, K_NORM, s, [&] {
+        return launch_rmsnorm(x, T, c->H, (const float *)Ly.norm.p, Ly.eps, c->w.xn, s);
+      }));
+      resid = x;
+      x = c->w.xn;
+      da.x = x;
+    }
     if (decode_supported(da)) {
       RETURN_IF(timed(c, K_DECODE_GATE_UP, s, [&] { return launch_decode_gate_up(da, s); }));
-      return timed(c, K_DECODE_DOWN, s, [&] { return launch_decode_down(da, s); });
+      RETURN_IF(timed(c, K_DECODE_DOWN, s, [&] { return launch_decode_down(da, s); }));
+      if (resid) RETURN_IF(timed(c, K_NORM, s, [&] { return launch_add_rows(y, resid, T * c->H, s); }));
+      return MOE_OK;
     }
   }
   RouteArgs ra{};
@@ -508,6 +542,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
   RETURN_IF(timed(c, K_COMBINE, s, [&] {
     return launch_combine(c->w.o, c->w.pos, c->w.wts, (int)T, (int)k, (int)c->H, 0, y, s);
   }));
+  if (resid) RETURN_IF(timed(c, K_NORM, s, [&] { return launch_add_rows(y, resid, T * c->H, s); }));
   return MOE_OK;
 }
 
@@ -865,6 +900,39 @@ int moe_layer_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T,
                              float *y, void *stream) {
   RETURN_IF(use_dev(c));
   return forward_device(c, layer, x, T, k, y, pick(c, stream));
+}
+
+int moe_block_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k, float *out) {
+  RETURN_IF(use_dev(c));
+  if (!x || !out) return fail(MOE_ERR_INVALID, "null x or out");
+  if (T == 0) return MOE_OK;
+  RETURN_IF(check_layer(c, layer, true));
+  RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
+  HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
+  RETURN_IF(forward_device(c, layer, c->w.x, T, k, c->w.y, c->stream, true));
+  HIP_TRY(hipMemcpyAsync(out, c->w.y, T * c->H * 4, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return check_layer_sync(c);
+}
+
+int moe_block_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
+                             float *out, void *stream) {
+  RETURN_IF(use_dev(c));
+  if (x == out) return fail(MOE_ERR_INVALID, "out must not alias x");
+  return forward_device(c, layer, x, T, k, out, pick(c, stream), true);
+}
+
+int moe_preload_norm(moe_ctx *c, size_t layer, const float *gamma, float eps) {
+  RETURN_IF(use_dev(c));
+  if (!gamma) return fail(MOE_ERR_INVALID, "null gamma");
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(MOE_ERR_INVALID, "eps must be finite and >= 0");
+  if (c->layers.size() <= layer) c->layers.resize(layer + 1);
+  Layer &Ly = c->layers[layer];
+  RETURN_IF(Ly.norm.ensure(c->H * 4));
+  HIP_TRY(hipMemcpy(Ly.norm.p, gamma, c->H * 4, hipMemcpyHostToDevice));
+  Ly.eps = eps;
+  Ly.has_norm = true;
+  return MOE_OK;
 }
 
 int moe_mxfp4_dequant_device(const uint8_t *blocks, const uint8_t *scales, size_t rows,

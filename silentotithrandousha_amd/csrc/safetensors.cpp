@@ -312,7 +312,7 @@ extern "C" int moe_safetensors_find(const char *path, const char *name, char *dt
 }
 
 extern "C" int moe_load_safetensors_layer(moe_ctx *ctx, const char *const *shard_paths, size_t n_shards,
-                                          size_t layer, size_t n_experts) {
+                                          size_t layer, size_t n_experts, float rms_norm_eps) {
   size_t hidden = 0, inter = 0;
   if (int r = moe::ctx_dims(ctx, &hidden, &inter)) return r;
   if (!shard_paths || !n_shards) return fail(MOE_ERR_INVALID, "no shards");
@@ -336,5 +336,15 @@ extern "C" int moe_load_safetensors_layer(moe_ctx *ctx, const char *const *shard
   if (int r = moe_preload_layer(ctx, layer, n_experts, gub, gus, gb.data(), db, ds, dbf.data())) return r;
   std::vector<uint16_t> rwb(E * H);
   std::memcpy(rwb.data(), rw, rwb.size() * 2);  // bf16 bits, little-endian as stored
-  return moe_preload_router(ctx, layer, n_experts, rwb.data(), rbf.data());
+  if (int r = moe_preload_router(ctx, layer, n_experts, rwb.data(), rbf.data())) return r;
+  // the post-attention RMSNorm weight, when the shards hold it (weights.rs:267-268)
+  const std::string nn = "model.layers." + std::to_string(layer) + ".post_attention_layernorm.weight";
+  for (const Shard &sh : shards)
+    if (sh.tensors.count(nn)) {
+      const uint8_t *g;
+      if (int r = find(shards, nn, "BF16", {H}, &g)) return r;
+      const std::vector<float> gf = bf16_to_f32(g, H);
+      return moe_preload_norm(ctx, layer, gf.data(), rms_norm_eps);
+    }
+  return MOE_OK;
 }

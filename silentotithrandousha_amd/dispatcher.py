@@ -108,7 +108,7 @@ class GpuMoeDispatcher:
                                            _p(_c(layer["router_w"], np.uint16)),
                                            _p(_c(layer["router_b"], np.float32))))
 
-    def load_safetensors_layer(self, shards, layer_idx, n_experts):
+    def load_safetensors_layer(self, shards, layer_idx, n_experts, rms_norm_eps=1e-5):
         """Layer `layer_idx`'s experts and router from local safetensors shards (the reference's
         ShardReader and tensor names, weights.rs:103-139, 228-346). `shards`: a directory (every
         *.safetensors in it, sorted, as the reference sorts the shard names) or a list of paths."""
@@ -118,7 +118,19 @@ class GpuMoeDispatcher:
         elif isinstance(shards, (str, os.PathLike)):
             shards = [shards]
         paths = (ctypes.c_char_p * len(shards))(*[os.fsencode(p) for p in shards])
-        check(lib().moe_load_safetensors_layer(self._ctx, paths, len(shards), layer_idx, n_experts))
+        check(lib().moe_load_safetensors_layer(self._ctx, paths, len(shards), layer_idx, n_experts, rms_norm_eps))
+
+    def preload_norm(self, layer_idx, gamma, eps=1e-5):
+        """Post-attention RMSNorm weight (weights.rs:32, 267-268) and rms_norm_eps (config.rs:42-43)."""
+        check(lib().moe_preload_norm(self._ctx, layer_idx, _p(_c(gamma, np.float32)), float(eps)))
+
+    def block_forward(self, layer_idx, x, top_k):
+        """x + MoE(RMSNorm(x) gamma): the post-attention norm and residual around the path
+        (executables.rs:260-317, session.rs:483-493, 982-994)."""
+        x = _c(x, np.float32).reshape(-1, self.hidden_size)
+        out = np.empty_like(x)
+        check(lib().moe_block_forward(self._ctx, layer_idx, _p(x), x.shape[0], top_k, _p(out)))
+        return out
 
     def preload_experts(self, layers):
         """preload_experts(&layers, &config) — all layers, index = position."""
@@ -238,6 +250,9 @@ class GpuMoeDispatcher:
         y = np.empty_like(x)
         check(lib().moe_layer_forward(self._ctx, layer, _p(x), x.shape[0], top_k, _p(y)))
         return y
+
+    def block_forward_device(self, layer, x_dev, n_tokens, top_k, out_dev, stream=None):
+        check(lib().moe_block_forward_device(self._ctx, layer, x_dev.ptr, n_tokens, top_k, out_dev.ptr, stream))
 
     def layer_forward_device(self, layer, x_dev, n_tokens, top_k, y_dev, stream=None):
         check(lib().moe_layer_forward_device(self._ctx, layer, x_dev.ptr, n_tokens, top_k,

@@ -609,6 +609,8 @@ def test_load_safetensors_layer(orc, tmp_path):
     experts = {k: v for k, v in t.items() if ".experts." in k}
     router = {k: v for k, v in t.items() if ".router." in k}
     write_safetensors(tmp_path / "model-00001-of-00002.safetensors", experts, metadata={"format": "pt"})
+    gamma = syn.bf16_round((1 + 0.1 * np.random.default_rng(402).standard_normal(H)).astype(np.float32))
+    router[f"model.layers.{li}.post_attention_layernorm.weight"] = ("BF16", syn.bf16_bits(gamma), (H,))
     write_safetensors(tmp_path / "model-00002-of-00002.safetensors", router, pad=7)
     x = syn.hidden(3, H, seed=401)
     d1 = GpuMoeDispatcher(H, I, 7.0)
@@ -623,6 +625,9 @@ def test_load_safetensors_layer(orc, tmp_path):
             assert_bit_exact(got, d2.layer_forward(li, x[:T], 4), f"loader vs preload mode {mode} T={T}")
             want, _, _, _ = orc.moe_layer(x[:T], L, 4)
             assert_rel_l2(got, want, f"loader vs oracle mode {mode} T={T}")
+    d2.preload_norm(li, gamma, 1e-5)
+    for T in (1, 3):
+        assert_bit_exact(d1.block_forward(li, x[:T], 4), d2.block_forward(li, x[:T], 4), f"loaded norm T={T}")
     bad = dict(experts)
     k = f"model.layers.{li}.mlp.experts.down_proj_scales"
     bad[k] = ("U8", L["d_scales"][:, :, :1], (E, H, 1))
@@ -631,3 +636,37 @@ def test_load_safetensors_layer(orc, tmp_path):
         d1.load_safetensors_layer([str(tmp_path / "bad.safetensors"), str(tmp_path / "model-00002-of-00002.safetensors")], li, E)
     d1.close()
     d2.close()
+
+
+# ---------------------------------------------------------------- RMSNorm + router + residual
+
+@pytest.mark.parametrize("T", [1, 2, 64])
+def test_block_forward_norm_and_residual(orc, disp20, layer20, T):
+    """out = x + MoE(RMSNorm(x) gamma) (executables.rs:260-317, session.rs:483-493, 982-994).
+    The norm is bit-exact with the oracle's canonical order: for every path (one launch with the
+    norm fused into its router and gate_up blocks, two launches, the batch path) the block gives
+    the same bits as x + layer_forward(oracle RMSNorm(x)); and within tolerance of the oracle's
+    whole block."""
+    rng = np.random.default_rng(500 + T)
+    gamma = (1 + 0.2 * rng.standard_normal(H20)).astype(np.float32)
+    disp20.preload_norm(0, gamma, 1e-5)
+    x = (syn.hidden(T, H20, seed=501 + T) * 3).astype(np.float32)
+    n = orc.rms_norm(x, gamma, 1e-5)
+    want, _, idx, _ = orc.moe_block(x, layer20, 4, gamma, 1e-5)
+    for mode in (MODES if T == 1 else [2]):
+        disp20.set_fused_decode(mode)
+        got = disp20.block_forward(0, x, 4)
+        ref = disp20.layer_forward(0, n, 4)
+        assert_bit_exact(got, (x + ref).astype(np.float32), f"block vs x + layer(n) T={T} mode {mode}")
+        assert_rel_l2(got - x, want - x, f"block vs oracle T={T} mode {mode}")
+    disp20.set_fused_decode(2)
+
+
+def test_block_forward_needs_norm():
+    from silentotithrandousha_amd._ffi import MoeError
+    H, I, E = 64, 32, 4
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, syn.make_layer(H, I, E, seed=510))
+    with pytest.raises(MoeError, match="RMSNorm"):
+        d.block_forward(0, syn.hidden(1, H, seed=511), 2)
+    d.close()

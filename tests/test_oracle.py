@@ -321,3 +321,47 @@ def test_live_path_close_to_fp32_path(orc):
     outs = np.stack([orc.expert_ffn(x, *syn.expert_slice(L, e), H, I)[0] for e in idx[0]])
     y_f32 = orc.combine(outs, w[0])
     assert rel_l2(y_live, y_f32) < 5e-3   # fp16 biases and the NEON sum order
+
+
+# ---------------------------------------------------------------- RMSNorm (session.rs:483-493)
+
+def test_rms_inv_against_float64_and_closed_forms(orc):
+    """The canonical-order inv_rms agrees with float64 to a few ulp on random rows; closed forms:
+    a constant row c gives 1 / sqrt(c^2 + eps); a zero row 1 / sqrt(eps); scaling the row by a
+    power of two scales inv_rms by its inverse when eps is negligible (the rounding is the
+    same); the reference's sequential sum differs by rounding only."""
+    rng = np.random.default_rng(7)
+    for H in (64, 2880, 3072):
+        for _ in range(5):
+            x = (rng.standard_normal(H) * rng.uniform(0.1, 10)).astype(np.float32)
+            r = orc.rms_inv(x, 1e-5)
+            r64 = 1.0 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5)
+            assert abs(r / r64 - 1) < 4 * 2.0 ** -24 * np.log2(H), (H, r, r64)
+            seq = np.float32(0)
+            for v in x:
+                seq = np.float32(seq + np.float32(v * v))
+            r_seq = np.float32(1) / np.sqrt(np.float32(seq / np.float32(H)) + np.float32(1e-5))
+            assert abs(r / r_seq - 1) < 2.0 ** -16
+    for c in (0.5, 3.0, 100.0):
+        x = np.full(2880, c, np.float32)
+        assert orc.rms_inv(x, 1e-5) == np.float32(1) / np.sqrt(np.float32(c * c) + np.float32(1e-5))
+    assert orc.rms_inv(np.zeros(2880, np.float32), 1e-5) == np.float32(1) / np.sqrt(np.float32(1e-5))
+    x = rng.standard_normal(2880).astype(np.float32)
+    assert orc.rms_inv(x * 4, 0.0) == orc.rms_inv(x, 0.0) / 4
+
+
+def test_rms_norm_rows_and_block_residual(orc):
+    """n = (x * inv_rms) * gamma per row; the block is x + MoE(n) (oracle composition)."""
+    from silentotithrandousha_amd import synthetic as syn
+    H, I, E = 64, 32, 8
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((3, H)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    n = orc.rms_norm(x, g, 1e-5)
+    for t in range(3):
+        r = orc.rms_inv(x[t], 1e-5)
+        assert np.array_equal(n[t], (x[t] * np.float32(r)) * g)
+    L = syn.make_layer(H, I, E, seed=9)
+    out, lg, idx, w = orc.moe_block(x, L, 2, g, 1e-5)
+    y, lg2, idx2, w2 = orc.moe_layer(n, L, 2)
+    assert np.array_equal(out, x + y) and np.array_equal(lg, lg2) and np.array_equal(idx, idx2)
