@@ -85,13 +85,17 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * 2 and 3 force the 256-row x 32- and 16-entry blocks (tuning; results identical).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
  * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results
- * identical). */
+ * identical).
+ * MOE_OPT_MATVEC: moe_mxfp4_matvec_device runs in one launch on the block-scaled MFMA (x as 4
+ * fp8 terms, exact to 2^-16) when 1 (default) and cols <= 3072 with x 16-byte aligned; otherwise,
+ * and when 0, as two launches on the bf16 MFMA (x as bf16 hi + lo). Results agree to 1e-5. */
 enum moe_option {
   MOE_OPT_FUSED_DECODE = 1,
   MOE_OPT_SPIN_LIMIT = 2,
   MOE_OPT_BATCH_GEMM = 3,
   MOE_OPT_GEMM_SHAPE = 4,
-  MOE_OPT_GEMM_BAND = 5
+  MOE_OPT_GEMM_BAND = 5,
+  MOE_OPT_MATVEC = 6
 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 
@@ -261,7 +265,8 @@ size_t moe_mxfp4_packed_size(size_t rows, size_t cols);
 int moe_mxfp4_pack_device(const uint8_t *blocks, const uint8_t *scales, size_t rows, size_t cols,
                           uint8_t *packed, void *stream);
 /* y[rows] = W x for a packed MXFP4 matrix (the reference's dequant + matvec, weights.rs:350-371
- * with session.rs:75-85). x, y: device f32. Uses ctx scratch for the split of x. */
+ * with session.rs:75-85). x, y: device f32. One launch (MOE_OPT_MATVEC); the two-launch form
+ * uses ctx scratch for the split of x. */
 int moe_mxfp4_matvec_device(moe_ctx *ctx, const uint8_t *packed, size_t rows, size_t cols,
                             const float *x, float *y, void *stream);
 

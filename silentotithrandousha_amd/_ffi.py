@@ -23,6 +23,7 @@ MOE_OPT_SPIN_LIMIT = 2
 MOE_OPT_BATCH_GEMM = 3
 MOE_OPT_GEMM_SHAPE = 4
 MOE_OPT_GEMM_BAND = 5
+MOE_OPT_MATVEC = 6
 
 _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p

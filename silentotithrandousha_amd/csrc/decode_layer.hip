@@ -157,32 +157,6 @@ __device__ __forceinline__ f32x4 tile_mfma_h(const TileRegs<NSMAX> &r, const uin
   return acc0 + acc1;
 }
 
-// tile_mfma_f8 over steps [s0, s0 + NS) of a tile whose chunks for those steps are in raw[] (zeros
-// past the tile) and whose scale words are all in sw[]; rec, bsw as for tile_mfma_f8. One
-// accumulator: the extra tile's quarter is short.
-template <int NSMAX, int NS, int s0>
-__device__ __forceinline__ f32x4 tile_mfma_f8_steps(const uint4 (&raw)[NS], const uint32_t *sw,
-                                                    const uint8_t *rec, const uint32_t *bsw, int lane) {
-  using R = ActRecord<NSMAX>;
-  const int j = lane & 15, gb = lane >> 4;
-  const uint8_t *bt = rec + R::term(j & (kTerms - 1), gb >> 1) + 16 * (gb & 1);
-  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int k = 0; k < NS; k++) {
-    const int s = s0 + k;
-    if (s < NSMAX) {
-      const uint4 b0 = *reinterpret_cast<const uint4 *>(bt + s * 128);
-      const uint4 b1 = *reinterpret_cast<const uint4 *>(bt + s * 128 + 64);
-      const uint4 a = raw[k];
-      const i32x8 A = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
-      const i32x8 B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                       (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-      acc = mfma_fp4_fp8(s & 3, A, B, acc, sw[s / 4], bsw[s / 4]);
-    }
-  }
-  return acc;
-}
-
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -151,6 +151,11 @@ hipError_t launch_pack(const uint8_t *blocks, const uint8_t *scales, size_t rows
                        uint8_t *packed, hipStream_t s);
 hipError_t launch_synth(void *dst, size_t n, int kind, uint64_t seed, float a, float b,
                         hipStream_t s);
+// One MXFP4 matvec in one launch on the block-scaled MFMA (matvec.hip): rows % 16 == 0,
+// cols % 32 == 0, cols <= 3072, x 16-byte aligned.
+bool matvec_fp4_supported(size_t rows, size_t cols, const float *x);
+hipError_t launch_matvec_fp4(const uint8_t *packed, size_t rows, size_t cols, const float *x,
+                             float *y, hipStream_t s);
 hipError_t launch_lm_head(const float *w, const float *x, size_t vocab, size_t H, float *y,
                           hipStream_t s);
 // Post-attention RMSNorm of T rows (rms_inv_wave's order) and the residual add y += x.

@@ -126,6 +126,7 @@ struct moe_ctx {
   int decode_mode = 2;
   int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 4 entries, 2 always, 0 never
   int gemm_shape = 0;  // grouped GEMM block shape override (tuning)
+  int matvec_one_launch = 1;  // moe_mxfp4_matvec_device: one launch (1) or split + GEMV (0)
   int gemm_band = 0;   // grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
@@ -977,6 +978,10 @@ int moe_mxfp4_matvec_device(moe_ctx *c, const uint8_t *packed, size_t rows, size
   if (!rows || !cols || rows % 16 || cols % 32)
     return fail(MOE_ERR_INVALID, "rows %zu must be a multiple of 16 and cols %zu of 32", rows, cols);
   hipStream_t s = pick(c, stream);
+  if (c->matvec_one_launch && matvec_fp4_supported(rows, cols, x)) {
+    HIP_TRY(launch_matvec_fp4(packed, rows, cols, x, y, s));
+    return MOE_OK;
+  }
   RETURN_IF(ensure_work(c, 1, 1, 1));
   const size_t cap0 = c->mv_split.cap;
   RETURN_IF(c->mv_split.ensure(256 + al(cols * 2 * 2)));
@@ -1058,6 +1063,10 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
     case MOE_OPT_GEMM_BAND:
       if (value < 0 || value > 64) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_BAND is 0..64");
       c->gemm_band = (int)value;
+      return MOE_OK;
+    case MOE_OPT_MATVEC:
+      if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_MATVEC is 0 or 1");
+      c->matvec_one_launch = (int)value;
       return MOE_OK;
     case MOE_OPT_SPIN_LIMIT:
       if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");

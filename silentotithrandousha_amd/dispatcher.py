@@ -168,6 +168,12 @@ class GpuMoeDispatcher:
         from ._ffi import MOE_OPT_GEMM_BAND
         check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_BAND, int(band)))
 
+    def set_matvec(self, one_launch):
+        """mxfp4_matvec in one launch on the block-scaled MFMA (1, default) or as split + bf16
+        GEMV (0); results agree to 1e-5."""
+        from ._ffi import MOE_OPT_MATVEC
+        check(lib().moe_set_option(self._ctx, MOE_OPT_MATVEC, int(one_launch)))
+
     def set_spin_limit(self, polls):
         from ._ffi import MOE_OPT_SPIN_LIMIT
         check(lib().moe_set_option(self._ctx, MOE_OPT_SPIN_LIMIT, int(polls)))

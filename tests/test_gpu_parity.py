@@ -76,7 +76,11 @@ def test_resident_copy_lossless(orc):
 
 # ---------------------------------------------------------------- MXFP4 matvec (config 1)
 
-def _matvec(disp, blocks, scales, rows, cols, x):
+MATVEC_PATHS = [1, 0]  # one launch on the block-scaled MFMA; split + bf16 GEMV
+
+
+def _matvec(disp, blocks, scales, rows, cols, x, path=1):
+    disp.set_matvec(path)
     b = DeviceBuffer.from_array(blocks)
     s = DeviceBuffer.from_array(scales)
     packed = mxfp4_pack(b, s, rows, cols)
@@ -87,21 +91,23 @@ def _matvec(disp, blocks, scales, rows, cols, x):
     return yd.download(np.float32, rows)
 
 
-def test_matvec_config1(orc):
+@pytest.mark.parametrize("path", MATVEC_PATHS)
+def test_matvec_config1(orc, path):
     rows = cols = 2880
     rng = np.random.default_rng(11)
     blocks = rng.integers(0, 256, size=(rows, cols // 32, 16), dtype=np.uint8)
     scales = rng.integers(118, 131, size=(rows, cols // 32), dtype=np.uint8)
     x = rng.normal(0, 1, cols).astype(np.float32)
     d = GpuMoeDispatcher(cols, cols, 7.0)
-    got = _matvec(d, blocks, scales, rows, cols, x)
+    got = _matvec(d, blocks, scales, rows, cols, x, path)
     want = orc.mxfp4_matvec(blocks, scales, rows, cols, x)
     e = assert_rel_l2(got, want, "2880x2880 MXFP4 matvec")
-    assert e < 1e-5, f"matvec error {e:.2e} larger than the hi/lo split allows"
+    assert e < 1e-5, f"matvec error {e:.2e} larger than the activation split allows"
     d.close()
 
 
-def test_matvec_one_hot_columns_exact(orc):
+@pytest.mark.parametrize("path", MATVEC_PATHS)
+def test_matvec_one_hot_columns_exact(orc, path):
     """x = e_k returns column k of W exactly: the in-kernel decode is bit-exact (up to the
     sign of zero, which a sum cannot carry)."""
     rows, cols = 64, 256
@@ -113,28 +119,30 @@ def test_matvec_one_hot_columns_exact(orc):
     for k in [0, 1, 2, 7, 8, 31, 32, 33, 100, 255]:
         x = np.zeros(cols, np.float32)
         x[k] = 1.0
-        got = _matvec(d, blocks, scales, rows, cols, x)
+        got = _matvec(d, blocks, scales, rows, cols, x, path)
         assert np.array_equal(got, W[:, k]), f"column {k}"
     d.close()
 
 
-def test_matvec_ragged_shapes(orc):
+@pytest.mark.parametrize("path", MATVEC_PATHS)
+def test_matvec_ragged_shapes(orc, path):
     """Block counts that are not a multiple of 4 (partial last step) and of 16 (partial
     last scale word)."""
     rng = np.random.default_rng(13)
     d = GpuMoeDispatcher(32, 32, 7.0)
-    for rows, nb in [(16, 1), (32, 2), (16, 3), (48, 5), (16, 17), (32, 90)]:
+    for rows, nb in [(16, 1), (32, 2), (16, 3), (48, 5), (16, 17), (32, 90), (16, 95), (16, 96), (32, 97)]:
         cols = 32 * nb
         blocks = rng.integers(0, 256, size=(rows, nb, 16), dtype=np.uint8)
         scales = rng.integers(118, 131, size=(rows, nb), dtype=np.uint8)
         x = rng.normal(0, 1, cols).astype(np.float32)
-        got = _matvec(d, blocks, scales, rows, cols, x)
+        got = _matvec(d, blocks, scales, rows, cols, x, path)
         assert_rel_l2(got, orc.mxfp4_matvec(blocks, scales, rows, cols, x), f"{rows}x{cols}",
                       tol=1e-5)
     d.close()
 
 
-def test_matvec_edge_scales(orc):
+@pytest.mark.parametrize("path", MATVEC_PATHS)
+def test_matvec_edge_scales(orc, path):
     """E8M0 bytes 0 (scale +0.0) and 255 (scale +inf in the reference decode, NaN in the OCP
     MX spec). Rows touching a 255 block are non-finite exactly where the fp32 path is; the
     GEMV does not promise the reference's choice between +-inf and NaN there, because the
@@ -152,7 +160,7 @@ def test_matvec_edge_scales(orc):
     blocks[11, 1, 0] = 0x10
     x = np.abs(rng.normal(0, 1, cols).astype(np.float32)) + 0.5
     d = GpuMoeDispatcher(cols, cols, 7.0)
-    got = _matvec(d, blocks, scales, rows, cols, x)
+    got = _matvec(d, blocks, scales, rows, cols, x, path)
     want = orc.mxfp4_matvec(blocks, scales, rows, cols, x)
     assert np.array_equal(np.isfinite(got), np.isfinite(want)), (got[[9, 11]], want[[9, 11]])
     assert not np.isfinite(want[9]) and not np.isfinite(want[11])
