@@ -132,7 +132,7 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
     disp = GpuMoeDispatcher(H, I, 7.0)
     disp.set_fused_decode(args.fused)
     disp.set_batch_gemm(args.batch_gemm)
-    disp.set_gemm_shape(args.gemm_shape)
+    disp.set_gemm_shape(args.gemm_shape, args.gemm_shape_down)
     disp.set_gemm_band(args.gemm_band)
     log(f"synthesising {n_layers} layers x {E} experts ({n_layers * E * sum(expert_bytes(H, I)) / 1e9:.2f} GB MXFP4)")
     Layers(disp, H, I, E, n_layers)
@@ -439,7 +439,9 @@ def main():
                     help="single-token steps through the multi-kernel path")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
-    ap.add_argument("--gemm-shape", type=int, default=0, choices=(0, 1, 2, 3), help="grouped GEMM block shape (tuning)")
+    ap.add_argument("--gemm-shape", type=int, default=0, choices=range(8), help="grouped GEMM block shape (tuning)")
+    ap.add_argument("--gemm-shape-down", type=int, default=0, choices=range(8),
+                    help="block shape of the down GEMM alone (0: as --gemm-shape; tuning)")
     ap.add_argument("--gemm-band", type=int, default=0, help="grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)")
     ap.add_argument("--batch-gemm", type=int, default=1, choices=(0, 1, 2),
                     help="batches: 0 GEMV kernels, 1 grouped GEMM when experts average >= 4 entries, 2 always GEMM")

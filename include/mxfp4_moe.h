@@ -81,8 +81,12 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * least 4 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
  * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical.
  * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM: 0 (default) by the mean entries per
- * expert; for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2;
- * 2 and 3 force the 256-row x 32- and 16-entry blocks (tuning; results identical).
+ * expert (48+: 512 rows x 64 entries in 8 wavefronts; 24+: 128 x 32 in 2; else 128 x 16 in 2);
+ * for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2; 2 and 3
+ * force 256-row x 32- and 16-entry blocks of 4 wavefronts, 4 the 128-row x 16-entry block of 4
+ * wavefronts (down only; gate_up takes 3), 5 the 128 x 16 block of 2 wavefronts, 6 a 64 x 16
+ * block of 1, 7 the 128 x 32 block of 2 (tuning; results identical). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
+ * (0, default: as MOE_OPT_GEMM_SHAPE).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
  * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results
  * identical).
@@ -95,7 +99,8 @@ enum moe_option {
   MOE_OPT_BATCH_GEMM = 3,
   MOE_OPT_GEMM_SHAPE = 4,
   MOE_OPT_GEMM_BAND = 5,
-  MOE_OPT_MATVEC = 6
+  MOE_OPT_MATVEC = 6,
+  MOE_OPT_GEMM_SHAPE_DOWN = 7
 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 

@@ -250,7 +250,8 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   __shared__ __attribute__((aligned(1024))) uint8_t s_r0[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r1[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
-  __shared__ __attribute__((aligned(16))) float s_bias[W * RT * 16];  // per wavefront: its rows' bias
+  constexpr int kBiasTiles = RT < 4 ? 4 : RT;  // the bias DMA moves 64 rows (4 tiles) per wavefront load
+  __shared__ __attribute__((aligned(16))) float s_bias[W * kBiasTiles * 16];  // per wavefront: its rows' bias
   __shared__ int s_tile[4];  // expert record index, first entry, entry count, row block
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wr = wv % WR, wc = wv / WR;
@@ -384,8 +385,8 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   {
     const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
 #pragma unroll
-    for (int k = 0; k < RT / 4; k++)
-      lds_dma4(bias + min(t0 * 16 + 64 * k + lane, (int)d.rows - 1), s_bias + (wv * RT + 4 * k) * 16);
+    for (int k = 0; k < kBiasTiles / 4; k++)
+      lds_dma4(bias + min(t0 * 16 + 64 * k + lane, (int)d.rows - 1), s_bias + (wv * kBiasTiles + 4 * k) * 16);
   }
 
   // ---- K loop, unrolled by D so that each step names its ring slots: step s computes from
@@ -431,8 +432,8 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   // ---- epilogue
   float4 bv[RT];
 #pragma unroll
-  for (int r = 0; r < RT; r++) bv[r] = *reinterpret_cast<const float4 *>(s_bias + (wv * RT + r) * 16 + 4 * g);
-  if (MODE == GEMV_GATE_UP) {
+  for (int r = 0; r < RT; r++) bv[r] = *reinterpret_cast<const float4 *>(s_bias + (wv * kBiasTiles + r) * 16 + 4 * g);
+  if constexpr (MODE == GEMV_GATE_UP) {
     // every 4 row tiles (64 rows) of the wavefront = h block hb (h values 32 hb .. 32 hb + 31)
     // of its entries. The SwiGLU values are staged in the (now free) ring as f32 [entry][32];
     // then lane 2 e + h takes half h of entry e's block: the kGemmTerms E2M3 terms of its 16
@@ -441,6 +442,15 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     constexpr int kWaveCols = 16 * CGW;  // entries of the wavefront
     static_assert(kWaveCols <= 32 || kWaveCols == 64, "one or two passes of 64 lanes");
     static_assert(W <= 8 && 4 * kWaveCols * 128 <= S::kSlot, "staging fits in two ring slots");
+    // with D = 3 the loop ends with one step's loads (the repeat of the last step) still in
+    // flight into a ring slot, which may be a staging slot: every wavefront's loads complete
+    // before any wavefront stages
+    if constexpr (D > 2) {
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
     uint8_t *hout = reinterpret_cast<uint8_t *>(a.out);
     float *stage = reinterpret_cast<float *>((wv < 4 ? s_r0 : s_r1) + (wv & 3) * kWaveCols * 128);
     const int e0 = kWaveCols * wc;                                     // first entry of the wavefront
@@ -541,17 +551,27 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
 
 // Column tile width from the mean entries per active expert (the per-expert counts live on the
 // device): 64 entries once experts average 48 or more (8 wavefronts, two per SIMD, so that one
-// wavefront's LDS reads overlap the other's MFMAs), down to 16 for a few per expert.
+// wavefront's LDS reads overlap the other's MFMAs); below that 128-row blocks of 2 wavefronts
+// with 32 or 16 entries, small enough (50-60 KB of LDS) for 2-3 blocks per CU, which keeps
+// every CU streaming weights when the grid is only a few blocks per CU (measured at 64, 128 and
+// 256 tokens against the 256-row blocks of 4 wavefronts: 4-10 % faster layers).
 template <int MODE>
 static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   const size_t active = std::max<size_t>(1, std::min<size_t>((size_t)a.max_active, a.n_entries));
   const size_t mean = a.n_entries / active;
   if (a.shape == 2) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3>(a, s);
   if (a.shape == 3) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
+  if (a.shape == 4) {  // 128 rows in 4 wavefronts of 2 row tiles: down only (gate_up needs whole h blocks)
+    if constexpr (MODE == GEMV_GATE_UP) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
+    else return launch_gemm_shape<MODE, 2, 1, 4, 1, 3>(a, s);
+  }
+  if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3>(a, s);
+  if (a.shape == 6) return launch_gemm_shape<MODE, 4, 1, 1, 1, 3>(a, s);
+  if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3>(a, s);
   if (mean >= 48)
     return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2>(a, s);
-  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3>(a, s);
-  return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
+  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3>(a, s);
+  return launch_gemm_shape<MODE, 4, 1, 2, 1, 3>(a, s);
 }
 
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s) {

@@ -127,7 +127,8 @@ struct moe_ctx {
   int batch_gemm = 1;  // batches: 1 grouped GEMM when experts average >= 4 entries, 2 always, 0 never
   int gemm_shape = 0;  // grouped GEMM block shape override (tuning)
   int matvec_one_launch = 1;  // moe_mxfp4_matvec_device: one launch (1) or split + GEMV (0)
-  int gemm_band = 0;   // grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)
+  int gemm_band = 0;
+  int gemm_shape_down = 0;  // block shape of the down GEMM (0: as gemm_shape)   // grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
   int n_cu = 256;     // compute units of the device (the one-launch grid is sized to it)
@@ -530,6 +531,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     RETURN_IF(timed(c, K_GATE_UP, s, [&] { return launch_gemm_fp8(GEMV_GATE_UP, gu, s); }));
     GemmArgs dn = ga;
     if (!c->gemm_band) dn.band = 1;
+    if (c->gemm_shape_down) dn.shape = c->gemm_shape_down;
     dn.mat_off = c->L.dn_off;
     dn.bias_off = c->L.dnb_off;
     dn.d = c->L.dn;
@@ -1057,12 +1059,16 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
       c->batch_gemm = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_SHAPE:
-      if (value < 0 || value > 3) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..3");
+      if (value < 0 || value > 7) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..7");
       c->gemm_shape = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_BAND:
       if (value < 0 || value > 64) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_BAND is 0..64");
       c->gemm_band = (int)value;
+      return MOE_OK;
+    case MOE_OPT_GEMM_SHAPE_DOWN:
+      if (value < 0 || value > 7) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE_DOWN is 0..7");
+      c->gemm_shape_down = (int)value;
       return MOE_OK;
     case MOE_OPT_MATVEC:
       if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_MATVEC is 0 or 1");

@@ -565,8 +565,9 @@ def test_batch_gemm_matches_oracle_and_gemv(orc, shape):
 
 
 def test_batch_gemm_block_shapes_identical(orc):
-    """The two block shapes for large batches (8 wavefronts x 64 rows, 4 x 128) accumulate every
-    output in the same K and term order: identical results."""
+    """Every block shape (large-batch 8 wavefronts as 4 x 2 or 8 x 1; forced 256-row x 32- and
+    16-entry blocks; 128-row blocks of 4 or 2 wavefronts, the 2-row-tile one for down only)
+    accumulates every output in the same K and term order: identical results."""
     H, I, E, k, T = 512, 512, 16, 4, 300
     L = syn.make_layer(H, I, E, seed=410, scale_lo=120, scale_hi=126, router_sigma=0.1)
     d = GpuMoeDispatcher(H, I, 7.0)
@@ -574,13 +575,35 @@ def test_batch_gemm_block_shapes_identical(orc):
     x = syn.hidden(T, H, seed=411)
     d.set_batch_gemm(2)
     outs = []
-    for shape in (0, 1):
-        d.set_gemm_shape(shape)
+    shapes = [(0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (0, 4), (2, 5), (5, 4), (7, 6)]
+    for shape, down in shapes:
+        d.set_gemm_shape(shape, down)
         outs.append(d.layer_forward(0, x, k))
     d.set_gemm_shape(0)
-    assert np.array_equal(outs[0], outs[1])
+    for (shape, down), o in zip(shapes[1:], outs[1:]):
+        assert np.array_equal(outs[0], o), f"shape {shape} down {down}"
     assert_rel_l2(outs[1], orc.moe_layer(x, L, k)[0], "gemm shape 1")
     d.close()
+
+
+def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
+    """The block shapes at the 20B dimensions, where K = 2880 takes 23 steps: with a ring of
+    three slots the loop ends with the repeat of the last step still loading into the slot that
+    the gate_up epilogue stages its SwiGLU values in (a missing wait there corrupted the h
+    records of the small-block shapes)."""
+    x = syn.hidden(64, H20, seed=430)
+    want = orc.moe_layer(x, layer20, 4)[0]
+    disp20.set_batch_gemm(2)
+    outs = []
+    shapes = [(0, 0), (3, 3), (5, 5), (6, 6), (7, 7), (2, 2), (5, 4)]
+    for shape, down in shapes:
+        disp20.set_gemm_shape(shape, down)
+        outs.append(disp20.layer_forward(0, x, 4))
+    disp20.set_gemm_shape(0)
+    disp20.set_batch_gemm(1)
+    assert_rel_l2(outs[0], want, "20B gemm T=64")
+    for (shape, down), o in zip(shapes[1:], outs[1:]):
+        assert np.array_equal(outs[0], o), f"shape {shape} down {down}"
 
 
 def test_batch_gemm_adaptive_dropped_slots(orc):
