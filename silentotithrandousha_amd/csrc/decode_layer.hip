@@ -157,25 +157,6 @@ __device__ __forceinline__ f32x4 tile_mfma_h(const TileRegs<NSMAX> &r, const uin
   return acc0 + acc1;
 }
 
-__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_agent64(const uint64_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent64(uint64_t *p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Wait until every memory operation this wavefront issued has completed.
-__device__ __forceinline__ void wait_mem() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 __device__ __forceinline__ LogitCopy *logit_copy(void *sync, int r) {
   return reinterpret_cast<LogitCopy *>(reinterpret_cast<uint8_t *>(sync) + sizeof(LayerSyncHdr) +
                                        (size_t)r * kCopyBytes);

@@ -763,6 +763,113 @@ __device__ __forceinline__ void load_bsw(const uint8_t *rec, uint32_t *bsw, int 
     bsw[q] = j < kTerms ? *reinterpret_cast<const uint32_t *>(rec + R::scale(j, gb) + 4 * q) : 0u;
 }
 
+// Cross-block communication without fences: agent-scope (device-coherent) relaxed loads and
+// stores, which bypass the non-coherent cache levels, and a wait for the wavefront's own memory
+// operations; a writer stores, waits, then signals; a reader sees the signal, then loads.
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent64(const uint64_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent64(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this wavefront issued has completed.
+__device__ __forceinline__ void wait_mem() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// ------------------------------------------------------------------ fp6 activation terms
+
+// E2M3 (fp6: sign, 2 exponent bits with bias 1, 3 mantissa bits; no Inf/NaN, largest 7.5)
+// conversion in hardware: v_cvt_scalef32_2xpk16_fp6_f32 divides 2 x 16 f32 by a power-of-two
+// scale and rounds each to the nearest E2M3 code, ties to even, saturating at +-7.5; output
+// field 2i is a[i], field 2i+1 is b[i] (value u of a 32-value group at bits 6u); the pk32 back
+// conversion returns the codes' values times the scale in field order. Measured on gfx950 against
+// a software RNE on every E2M3 grid point, every midpoint, values past 7.5, +-inf and random
+// values: identical codes except -0 for -0.0. The destination must not share registers with the
+// sources (register allocations that reuse the unused upper source registers for the result gave
+// wrong codes, deterministically), so both are issued as inline assembly with early-clobber
+// outputs.
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+typedef float f32x32v __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x6v __attribute__((ext_vector_type(6)));
+
+// Split of 16 values of a 32-value block (block max |x| = m, bad = some value of the block is
+// not finite) into kGemmTerms E2M3 terms: term t has scale 2^(E - 2 - 5t) where m = f 2^E,
+// f in [1/2, 1) (so term 0 holds the block in [-4, 4)), and takes the exact residual of the
+// terms before it (the activation is then exact to about 2^-13 of the block maximum). Codes of
+// value u at bits 6u of d[t][0..2]; sb byte t = the E8M0 scale of term t (0xFF, NaN, for a bad
+// block: the products come out NaN, as the f32 arithmetic would). Scales stop at 2^-126 (a
+// normal f32) for blocks below about 2^-120.
+__device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool bad, uint32_t (&d)[kGemmTerms][3],
+                                            uint32_t &sb) {
+  int E = 0;
+  if (m > 0.0f && isfinite(m)) frexpf(m, &E);
+  float r[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) r[i] = bad ? 0.0f : x[i];
+  sb = 0;
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    const int se = max(E - 2 - 5 * t, -126);
+    sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
+    const float sc = __builtin_amdgcn_ldexpf(1.0f, se);
+    f32x16v a = {}, b = {};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      a[i] = r[2 * i];
+      b[i] = r[2 * i + 1];
+    }
+    u32x6v c;
+    f32x32v q;
+    asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(c) : "v"(a), "v"(b), "v"(sc));
+    asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
+#pragma unroll
+    for (int i = 0; i < 16; i++) r[i] = r[i] - q[i];
+    d[t][0] = c[0];
+    d[t][1] = c[1];
+    d[t][2] = c[2];
+  }
+}
+
+
+// Thread p (< 8 kGemmNs writes; every lane of the pair must run it) of a row's split: half
+// p & 1 (values 16 h .. 16 h + 15) of 32-value block p >> 1, given in v, into the row's GemmRec
+// record r: the kGemmTerms E2M3 terms of the half (block maximum and finiteness shared with the
+// neighbouring lane, which holds the other half) and, from the h = 0 lane, the terms' scales.
+__device__ __forceinline__ void rec_split_half(const float (&v)[16], int p, uint8_t *r) {
+  float m = 0.0f, bad = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    m = fmaxf(m, fabsf(v[i]));
+    if (!isfinite(v[i])) bad = 1.0f;
+  }
+  m = fmaxf(m, xor_lane<1>(m));
+  bad = fmaxf(bad, xor_lane<1>(bad));
+  uint32_t d[kGemmTerms][3], sb;
+  split16_fp6(v, m, bad != 0.0f, d, sb);
+  if (p >= 8 * kGemmNs) return;
+  const int b = p >> 1, h = p & 1, st = b >> 2, i = b & 3;
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    uint32_t *dst = reinterpret_cast<uint32_t *>(r + GemmRec::half(st, t, i, h));
+    dst[0] = d[t][0];
+    dst[1] = d[t][1];
+    dst[2] = d[t][2];
+  }
+  if (h == 0) {
+#pragma unroll
+    for (int t = 0; t < kGemmTerms; t++) r[GemmRec::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+  }
+}
+
 // tile_mfma_f8 over steps [s0, s0 + NS) of a tile whose chunks for those steps are in raw[] (zeros
 // past the tile) and whose scale words are all in sw[]; rec, bsw as for tile_mfma_f8. One
 // accumulator: a quarter of a tile's steps is a short chain.

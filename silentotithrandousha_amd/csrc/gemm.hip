@@ -2,15 +2,14 @@
 // applied to every (token, slot) entry routed to an expert, session.rs:943-972) on the
 // block-scaled MFMA v_mfma_scale_f32_16x16x128_f8f6f4: A = the expert's MXFP4 weights as
 // stored (E2M1 nibbles + E8M0 scales, resident tile16 layout), B = the activations of the
-// expert's entries as kTerms fp8 terms (split8_fp8), f32 accumulation.
+// expert's entries as kGemmTerms E2M3 terms (split16_fp6; the batch router writes the tokens'
+// records, rec_split_half), f32 accumulation.
 //
-//   k_split_rows   f32 rows (x) -> step-major activation records
-//   k_gemm_fp8     one block = 64 RT weight rows x 16 CG entries of one expert; each wavefront
-//                  owns 16 RT rows (RT tiles of 16) x all the block's entries (CG column
-//                  groups) x kGemmTerms activation terms.
-//                  K-steps of 128 run through a ring of 3: the B records of the entries go
-//                  straight into LDS by LDS-DMA (global_load_lds), A tiles into registers, two
-//                  steps ahead of the MFMAs.
+//   k_gemm_fp8     one block = WR x WC wavefronts; wavefront (wr, wc) owns RT tiles of 16 weight
+//                  rows x CGW column groups of 16 entries of one expert, x kGemmTerms terms.
+//                  K-steps of 128 run through a ring of D = 2 or 3 LDS slots: the entries' B
+//                  records, the A chunks and their scale words all go into LDS by LDS-DMA
+//                  (global_load_lds), D - 1 steps ahead of the MFMAs.
 //                  GATE_UP epilogue: bias, SwiGLU (gate = row 2i, up = row 2i+1) and the split
 //                  of the wavefront's 32 h values per entry into the h records; DOWN epilogue:
 //                  bias and +-65504 clamp into f32 [entry][H].
@@ -22,113 +21,6 @@
 namespace moe {
 
 using G = GemmRec;  // step-major activation record (kernels.hpp)
-
-// ------------------------------------------------------------------ fp6 activation terms
-
-// E2M3 (fp6: sign, 2 exponent bits with bias 1, 3 mantissa bits; no Inf/NaN, largest 7.5)
-// conversion in hardware: v_cvt_scalef32_2xpk16_fp6_f32 divides 2 x 16 f32 by a power-of-two
-// scale and rounds each to the nearest E2M3 code, ties to even, saturating at +-7.5; output
-// field 2i is a[i], field 2i+1 is b[i] (value u of a 32-value group at bits 6u); the pk32 back
-// conversion returns the codes' values times the scale in field order. Measured on gfx950 against
-// a software RNE on every E2M3 grid point, every midpoint, values past 7.5, +-inf and random
-// values: identical codes except -0 for -0.0. The destination must not share registers with the
-// sources (register allocations that reuse the unused upper source registers for the result gave
-// wrong codes, deterministically), so both are issued as inline assembly with early-clobber
-// outputs.
-typedef float f32x16v __attribute__((ext_vector_type(16)));
-typedef float f32x32v __attribute__((ext_vector_type(32)));
-typedef uint32_t u32x6v __attribute__((ext_vector_type(6)));
-
-// Split of 16 values of a 32-value block (block max |x| = m, bad = some value of the block is
-// not finite) into kGemmTerms E2M3 terms: term t has scale 2^(E - 2 - 5t) where m = f 2^E,
-// f in [1/2, 1) (so term 0 holds the block in [-4, 4)), and takes the exact residual of the
-// terms before it (the activation is then exact to about 2^-13 of the block maximum). Codes of
-// value u at bits 6u of d[t][0..2]; sb byte t = the E8M0 scale of term t (0xFF, NaN, for a bad
-// block: the products come out NaN, as the f32 arithmetic would). Scales stop at 2^-126 (a
-// normal f32) for blocks below about 2^-120.
-__device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool bad, uint32_t (&d)[kGemmTerms][3],
-                                            uint32_t &sb) {
-  int E = 0;
-  if (m > 0.0f && isfinite(m)) frexpf(m, &E);
-  float r[16];
-#pragma unroll
-  for (int i = 0; i < 16; i++) r[i] = bad ? 0.0f : x[i];
-  sb = 0;
-#pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-    const int se = max(E - 2 - 5 * t, -126);
-    sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
-    const float sc = __builtin_amdgcn_ldexpf(1.0f, se);
-    f32x16v a = {}, b = {};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      a[i] = r[2 * i];
-      b[i] = r[2 * i + 1];
-    }
-    u32x6v c;
-    f32x32v q;
-    asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(c) : "v"(a), "v"(b), "v"(sc));
-    asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
-#pragma unroll
-    for (int i = 0; i < 16; i++) r[i] = r[i] - q[i];
-    d[t][0] = c[0];
-    d[t][1] = c[1];
-    d[t][2] = c[2];
-  }
-}
-
-// ------------------------------------------------------------------ activation records
-
-// grid (1, rows), 256 threads: thread p < 8 kGemmNs handles half p & 1 of 32-block p >> 1 of
-// row `row` (values past K are zeros, blocks up to 4 * kGemmNs written); the two halves of a
-// block are neighbouring lanes.
-__global__ __launch_bounds__(256) void k_split_rows(const float *src, int K, uint8_t *rec) {
-  const int row = blockIdx.y, p = threadIdx.x;
-  const int b = p >> 1, h = p & 1;
-  const int k0 = 32 * b + 16 * h;
-  float v[16];
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (p < 8 * kGemmNs && k0 + 4 * q < K) a = *reinterpret_cast<const float4 *>(src + (size_t)row * K + k0 + 4 * q);
-    v[4 * q] = a.x;
-    v[4 * q + 1] = a.y;
-    v[4 * q + 2] = a.z;
-    v[4 * q + 3] = a.w;
-  }
-  float m = 0.0f, bad = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    m = fmaxf(m, fabsf(v[i]));
-    if (!isfinite(v[i])) bad = 1.0f;
-  }
-  m = fmaxf(m, xor_lane<1>(m));
-  bad = fmaxf(bad, xor_lane<1>(bad));
-  uint32_t d[kGemmTerms][3], sb;
-  split16_fp6(v, m, bad != 0.0f, d, sb);
-  if (p >= 8 * kGemmNs) return;
-  uint8_t *r = rec + (size_t)row * G::kBytes;
-  const int st = b >> 2, i = b & 3;
-#pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-    uint32_t *dst = reinterpret_cast<uint32_t *>(r + G::half(st, t, i, h));
-    dst[0] = d[t][0];
-    dst[1] = d[t][1];
-    dst[2] = d[t][2];
-  }
-  if (h == 0) {
-#pragma unroll
-    for (int t = 0; t < kGemmTerms; t++) r[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
-  }
-}
-
-hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *rec, hipStream_t s) {
-  static_assert(8 * kGemmNs <= 256, "one thread per half block");
-  if (K % 8 || K > (size_t)kGemmNs * 128) return hipErrorInvalidValue;
-  if (!rows) return hipSuccess;
-  hipLaunchKernelGGL(k_split_rows, dim3(1, (unsigned)rows), dim3(256), 0, s, src, (int)K, rec);
-  return hipGetLastError();
-}
 
 // ------------------------------------------------------------------ grouped GEMM
 

@@ -26,12 +26,91 @@ namespace moe {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteTokens = 8;  // tokens per block for large batches: the router weights load once per block
 
+// Groups the T*k (token, slot) entries by expert, in one block of 1024 threads. Active
+// experts are listed in ascending id; entries of one expert are ordered by t*k + slot.
+// pos[t*k + slot] = entry index (or -1). LDS: s_count[E], s_base[E], s_wave[16][E].
+template <bool kAgentLoads>  // idx written by other blocks of the same launch: agent-scope loads
+__device__ __forceinline__ void bucket_block(const int32_t *idx, int T, int k, int E, int32_t *n_active,
+                             int32_t *active_ids, int32_t *active_off, int32_t *entry_src,
+                             int32_t *pos, int *s_count, int *s_base, int *s_wave) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int N = T * k;
+  for (int e = tid; e < E; e += 1024) s_count[e] = 0;
+  for (int i = tid; i < 16 * E; i += 1024) s_wave[i] = 0;
+  __syncthreads();
+  auto ld_idx = [&](int n) {
+    return kAgentLoads ? (int)ld_agent(reinterpret_cast<const uint32_t *>(idx) + n) : idx[n];
+  };
+  for (int n = tid; n < N; n += 1024) {
+    int e = ld_idx(n);
+    if (e >= 0) atomicAdd(&s_count[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int na = 0, off = 0;
+    for (int e = 0; e < E; e++) {
+      s_base[e] = off;
+      if (s_count[e] > 0) {
+        active_ids[na] = e;
+        active_off[na] = off;
+        off += s_count[e];
+        na++;
+      }
+    }
+    active_off[na] = off;
+    *n_active = na;
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < N; c0 += 1024) {
+    const int n = c0 + tid;
+    const int e = n < N ? ld_idx(n) : -1;
+    // lanes of this wavefront holding the same value (9-bit match through ballots)
+    const uint32_t v = (uint32_t)(e + 1);
+    uint64_t same = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 9; bit++) {
+      uint64_t b = __ballot((v >> bit) & 1u);
+      same &= ((v >> bit) & 1u) ? b : ~b;
+    }
+    const int rank_in_wave = __popcll(same & ((1ull << lane) - 1ull));
+    const bool leader = (same & ((1ull << lane) - 1ull)) == 0;
+    if (leader && e >= 0) s_wave[wv * E + e] = __popcll(same);
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += 1024) {  // exclusive prefix over wavefronts
+      int run = 0;
+      for (int w = 0; w < 16; w++) {
+        int c = s_wave[w * E + ee];
+        s_wave[w * E + ee] = run;
+        run += c;
+      }
+      s_count[ee] = run;  // this chunk's total for expert ee
+    }
+    __syncthreads();
+    if (e >= 0) {
+      int ge = s_base[e] + s_wave[wv * E + e] + rank_in_wave;
+      entry_src[ge] = n / k;
+      pos[n] = ge;
+    } else if (n < N) {
+      pos[n] = -1;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += 1024) s_base[ee] += s_count[ee];
+    for (int i = tid; i < 16 * E; i += 1024) s_wave[i] = 0;
+    __syncthreads();
+  }
+}
+
+// Length of a token's x staging in k_route (floats): the router lane chains' length.
+__host__ __device__ constexpr int route_hp(int H) { return ((H + 63) / 64 + 7) / 8 * 512; }
+
 // Router + top-k for TB tokens per block (block b: tokens TB b .. TB b + TB - 1). x of the tokens
 // is staged in LDS (zero padded to the router chains' length; with xsplit != NULL its bf16
 // hi + lo split is written for the GEMV path); wavefront w computes experts w, w + 16, ... for
 // every token of the block from one load of the expert's weights (router_dot's canonical order
 // per token); then wavefront w runs the top-k of token w (wave_topk_order/weights, k <= 4,
 // E <= 128: block_topk's arithmetic), or for larger k the block runs block_topk per token.
+// With xrec the block also writes its tokens' grouped-GEMM records; with bucket_ticket the last
+// block to finish groups every entry by expert (bucket_block) in its free x staging area.
 template <int KI, int TB>
 __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
   __shared__ float s_logit[TB][kMaxExperts];
@@ -39,6 +118,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
   __shared__ int s_order[TB][kMaxTopK];
   __shared__ float s_w[TB][kMaxTopK];
   __shared__ int s_sel[TB];
+  __shared__ int s_last;
   const int t0 = blockIdx.x * TB;
   const int nt = min(TB, a.T - t0);
   const int lane = threadIdx.x & 63;
@@ -46,8 +126,15 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
   const int nw = kRouteThreads / 64;
   const int H = a.H, E = a.E;
   const int nq = ((H + 63) / 64 + 7) / 8;  // uint4 per lane chain
-  const int Hp = nq * 8 * 64;
+  const int Hp = route_hp(H);
   extern __shared__ float s_x[];  // TB * Hp floats
+  // the wavefront's first expert's weights, in flight while x is staged (then one expert ahead)
+  uint4 v[KI > 0 ? KI : 1];
+  if (KI > 0 && wv < E) {
+    const uint4 *wq = reinterpret_cast<const uint4 *>(a.w + (size_t)wv * nq * 512) + lane;
+#pragma unroll
+    for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
+  }
   for (int tb = 0; tb < nt; tb++) {
     const float *x = a.x + (size_t)(t0 + tb) * H;
     uint16_t *xs = a.xsplit ? a.xsplit + (size_t)(t0 + tb) * 2 * H : nullptr;
@@ -63,13 +150,27 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
     }
   }
   __syncthreads();
+  if (a.xrec) {  // the grouped GEMM's activation records of the block's tokens (rec_split_half)
+    for (int u = threadIdx.x; u < nt * 256; u += kRouteThreads) {  // whole wavefronts
+      const int tb = u >> 8, p = u & 255, k0 = 32 * (p >> 1) + 16 * (p & 1);
+      const float *xt = s_x + tb * Hp;
+      float xv[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) xv[i] = p < 8 * kGemmNs && k0 + i < H ? xt[k0 + i] : 0.0f;
+      rec_split_half(xv, p, a.xrec + (size_t)(t0 + tb) * GemmRec::kBytes);
+    }
+  }
   for (int e = wv; e < E; e += nw) {
     const uint16_t *w_e = a.w + (size_t)e * nq * 512;
     if (KI > 0) {
-      uint4 v[KI > 0 ? KI : 1];
-      const uint4 *wq = reinterpret_cast<const uint4 *>(w_e) + lane;
+      uint4 cur[KI > 0 ? KI : 1];
 #pragma unroll
-      for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
+      for (int q = 0; q < KI; q++) cur[q] = v[q];
+      if (e + nw < E) {  // the next expert's weights load during this one's dot products
+        const uint4 *wq = reinterpret_cast<const uint4 *>(a.w + (size_t)(e + nw) * nq * 512) + lane;
+#pragma unroll
+        for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
+      }
 #pragma unroll
       for (int tb = 0; tb < TB; tb++) {
         if (tb < nt) {
@@ -77,7 +178,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
           float p = 0.0f;
 #pragma unroll
           for (int q = 0; q < KI; q++) {
-            const uint32_t u[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+            const uint32_t u[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
 #pragma unroll
             for (int h = 0; h < 8; h++) {
               const uint16_t bw = (uint16_t)(u[h >> 1] >> (16 * (h & 1)));
@@ -119,7 +220,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
       }
       if (lane < a.k) {
         const size_t o = (size_t)t * a.k + lane;
-        a.idx[o] = s_order[tb][lane];
+        st_agent(reinterpret_cast<uint32_t *>(a.idx) + o, (uint32_t)s_order[tb][lane]);
         a.wts[o] = s_w[tb][lane];
       }
     }
@@ -130,7 +231,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
       block_topk(c, s_logit[tb], s_p, s_order[tb], s_w[tb], &s_sel[tb]);
       if (threadIdx.x < a.k) {
         const size_t o = (size_t)t * a.k + threadIdx.x;
-        a.idx[o] = s_order[tb][threadIdx.x];
+        st_agent(reinterpret_cast<uint32_t *>(a.idx) + o, (uint32_t)s_order[tb][threadIdx.x]);
         a.wts[o] = s_w[tb][threadIdx.x];
       }
     }
@@ -145,6 +246,18 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
     }
     a.active_off[sel] = sel;
     for (int s2 = 0; s2 < a.k; s2++) a.pos[s2] = s2 < sel ? s2 : -1;
+  }
+  if (a.bucket_ticket) {
+    wait_mem();  // this thread's idx stores (agent scope) have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.bucket_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x == 0) st_agent(a.bucket_ticket, 0u);  // zero again for the next launch
+    int *ws = reinterpret_cast<int *>(s_x);  // (2 + 16) E ints; the host checked they fit
+    bucket_block<true>(a.idx, a.T, a.k, E, a.n_active, a.active_ids, a.active_off, a.entry_src,
+                       a.pos, ws, ws + E, ws + 2 * E);
   }
 }
 
@@ -165,9 +278,12 @@ static void launch_route_ki(const RouteArgs &a, int nq, hipStream_t s) {
   }
 }
 
+bool route_bucket_fits(int H, int E) { return 18 * E <= route_hp(H); }
+
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
   if (a.E < 1 || a.E > kMaxExperts || a.k < 1 || a.k > kMaxTopK || a.k > a.E || a.T < 1 ||
-      a.H < 1 || (a.fuse_bucket && a.T != 1))
+      a.H < 1 || (a.fuse_bucket && a.T != 1) || (a.xrec && a.H > 128 * kGemmNs) ||
+      (a.bucket_ticket && (a.fuse_bucket || !route_bucket_fits(a.H, a.E))))
     return hipErrorInvalidValue;
   const int nq = ((a.H + 63) / 64 + 7) / 8;
   const size_t lds = (size_t)nq * 8 * 64 * sizeof(float);
@@ -183,77 +299,14 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
 
 // ------------------------------------------------------------------ bucketing
 
-// Groups the T*k (token, slot) entries by expert. Active experts are listed in ascending id;
-// entries of one expert are ordered by t*k + slot. pos[t*k + slot] = entry index (or -1).
 __global__ __launch_bounds__(1024) void k_bucket(const int32_t *idx, int T, int k, int E,
                                                  int32_t *n_active, int32_t *active_ids,
                                                  int32_t *active_off, int32_t *entry_src,
                                                  int32_t *pos) {
   __shared__ int s_count[kMaxExperts];
   __shared__ int s_base[kMaxExperts];
-  __shared__ int s_wave[16][kMaxExperts];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int N = T * k;
-  for (int e = tid; e < E; e += 1024) s_count[e] = 0;
-  for (int i = tid; i < 16 * kMaxExperts; i += 1024) (&s_wave[0][0])[i] = 0;
-  __syncthreads();
-  for (int n = tid; n < N; n += 1024) {
-    int e = idx[n];
-    if (e >= 0) atomicAdd(&s_count[e], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int na = 0, off = 0;
-    for (int e = 0; e < E; e++) {
-      s_base[e] = off;
-      if (s_count[e] > 0) {
-        active_ids[na] = e;
-        active_off[na] = off;
-        off += s_count[e];
-        na++;
-      }
-    }
-    active_off[na] = off;
-    *n_active = na;
-  }
-  __syncthreads();
-  for (int c0 = 0; c0 < N; c0 += 1024) {
-    const int n = c0 + tid;
-    const int e = n < N ? idx[n] : -1;
-    // lanes of this wavefront holding the same value (9-bit match through ballots)
-    const uint32_t v = (uint32_t)(e + 1);
-    uint64_t same = ~0ull;
-#pragma unroll
-    for (int bit = 0; bit < 9; bit++) {
-      uint64_t b = __ballot((v >> bit) & 1u);
-      same &= ((v >> bit) & 1u) ? b : ~b;
-    }
-    const int rank_in_wave = __popcll(same & ((1ull << lane) - 1ull));
-    const bool leader = (same & ((1ull << lane) - 1ull)) == 0;
-    if (leader && e >= 0) s_wave[wv][e] = __popcll(same);
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += 1024) {  // exclusive prefix over wavefronts
-      int run = 0;
-      for (int w = 0; w < 16; w++) {
-        int c = s_wave[w][ee];
-        s_wave[w][ee] = run;
-        run += c;
-      }
-      s_count[ee] = run;  // this chunk's total for expert ee
-    }
-    __syncthreads();
-    if (e >= 0) {
-      int ge = s_base[e] + s_wave[wv][e] + rank_in_wave;
-      entry_src[ge] = n / k;
-      pos[n] = ge;
-    } else if (n < N) {
-      pos[n] = -1;
-    }
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += 1024) s_base[ee] += s_count[ee];
-    for (int i = tid; i < 16 * kMaxExperts; i += 1024) (&s_wave[0][0])[i] = 0;
-    __syncthreads();
-  }
+  __shared__ int s_wave[16 * kMaxExperts];
+  bucket_block<false>(idx, T, k, E, n_active, active_ids, active_off, entry_src, pos, s_count, s_base, s_wave);
 }
 
 hipError_t launch_bucket(const int32_t *idx, int T, int k, int E, int32_t *n_active,

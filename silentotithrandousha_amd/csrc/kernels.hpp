@@ -25,8 +25,10 @@ struct RouteArgs {
   int32_t *idx;          // [T, k]
   float *wts;            // [T, k]
   uint16_t *xsplit;      // [T, 2, H] bf16 hi / lo
+  uint8_t *xrec;         // [T] GemmRec records of x (grouped GEMM operands; H <= 128 kGemmNs)
   int fuse_bucket;       // T == 1: also write the expert list
   int32_t *n_active, *active_ids, *active_off, *entry_src, *pos;
+  uint32_t *bucket_ticket;  // T > 1: zeroed counter; the last block buckets (route_bucket_fits)
 };
 
 struct GemvArgs {
@@ -82,7 +84,6 @@ struct GemmArgs {
   int n_row_blocks;          // set by launch_gemm_fp8: row blocks of the launch
   int n_tiles;               //                         row blocks x column tiles
 };
-hipError_t launch_split_rows(const float *src, size_t rows, size_t K, uint8_t *rec, hipStream_t s);
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
 
 // Single-token MoE layer in two launches (decode.hip).
@@ -136,6 +137,8 @@ hipError_t launch_decode_gate_up(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
 
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+// Whether k_route's x staging (one token) holds bucket_block's LDS for E experts.
+bool route_bucket_fits(int H, int E);
 hipError_t launch_bucket(const int32_t *idx, int T, int k, int E, int32_t *n_active,
                          int32_t *active_ids, int32_t *active_off, int32_t *entry_src,
                          int32_t *pos, hipStream_t s);

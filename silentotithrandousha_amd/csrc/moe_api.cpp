@@ -129,6 +129,7 @@ struct moe_ctx {
   int matvec_one_launch = 1;  // moe_mxfp4_matvec_device: one launch (1) or split + GEMV (0)
   int gemm_band = 0;
   int gemm_shape_down = 0;  // block shape of the down GEMM (0: as gemm_shape)   // grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)
+  DevBuf route_ticket;  // k_route's block counter for the fused bucketing, zero between launches
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
   int n_cu = 256;     // compute units of the device (the one-launch grid is sized to it)
@@ -494,14 +495,17 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
                         c->L.gu.ns <= (uint32_t)kGemmNs && c->L.dn.ns <= (uint32_t)kGemmNs &&
                         (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   ra.xsplit = use_gemm ? nullptr : c->w.xsplit;
+  ra.xrec = use_gemm ? c->w.xrec : nullptr;  // the router writes the GEMM's activation records
   ra.fuse_bucket = T == 1;
   ra.n_active = c->w.n_active;
   ra.active_ids = c->w.active_ids;
   ra.active_off = c->w.active_off;
   ra.entry_src = c->w.entry_src;
   ra.pos = c->w.pos;
+  const bool fuse_bucket = T > 1 && route_bucket_fits((int)c->H, (int)E);
+  ra.bucket_ticket = fuse_bucket ? (uint32_t *)c->route_ticket.p : nullptr;
   RETURN_IF(timed(c, K_ROUTE, s, [&] { return launch_route(ra, s); }));
-  if (T > 1)
+  if (T > 1 && !fuse_bucket)
     RETURN_IF(timed(c, K_BUCKET, s, [&] {
       return launch_bucket(c->w.idx, (int)T, (int)k, (int)E, c->w.n_active, c->w.active_ids,
                            c->w.active_off, c->w.entry_src, c->w.pos, s);
@@ -509,7 +513,6 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
   const int max_active = (int)std::min(E, T * k);
   if (use_gemm) {
     const size_t N = T * k;
-    RETURN_IF(timed(c, K_SPLIT, s, [&] { return launch_split_rows(x, T, c->H, c->w.xrec, s); }));
     GemmArgs ga{};
     ga.base = (const uint8_t *)Ly.experts.p;
     ga.stride = c->L.stride;
@@ -589,6 +592,7 @@ int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ct
   }
   const size_t sb = layer_sync_bytes(), hb = layer_hterm_bytes();
   if (c->layer_sync.ensure(sb) != MOE_OK || hipMemset(c->layer_sync.p, 0, sb) != hipSuccess ||
+      c->route_ticket.ensure(256) != MOE_OK || hipMemset(c->route_ticket.p, 0, 256) != hipSuccess ||
       c->layer_h.ensure(hb) != MOE_OK || hipMemset(c->layer_h.p, 0, hb) != hipSuccess) {
     moe_destroy(c);
     return fail(MOE_ERR_OOM, "signalling area of %zu bytes", sb);
