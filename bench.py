@@ -235,7 +235,10 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
                    "experts": E, "top_k": k, "tokens_per_layer": T, "layers_per_step": layers_per_step,
                    "resident_layers": n_layers,
                    "weights": "MXFP4 E2M1 + E8M0 (checkpoint layout repacked on preload)",
-                   "arithmetic": "exact MXFP4->bf16 decode x f32 activation as bf16 hi+lo, f32 MFMA accumulate",
+                   "arithmetic": ("MXFP4 weights as stored on the block-scaled MFMA; x as 4 fp8 terms, h as "
+                                  "fixed-exponent fp8 terms; f32 accumulate" if T == 1 and args.fused else
+                                  "MXFP4 weights as stored on the block-scaled MFMA; activations as 3 E2M3 "
+                                  "terms (grouped GEMM) or bf16 hi+lo (GEMV path); f32 accumulate"),
                    "graph_replay": bool(graph), "fused_decode": bool(args.fused and T == 1)},
         "roofline": {"bound": "hbm",
                      "kernel": {"decode_layer": "k_decode_layer", "decode_gate_up": "k_decode_gate_up",
