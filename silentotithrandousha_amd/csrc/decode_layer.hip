@@ -553,10 +553,14 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
     const uint32_t want = s_ep + 1;
     const uint32_t *f = hdr->gflag[t % kFlagReplicas];
     for (uint32_t n = 0;; n++) {
+      // all of a poll's loads in flight at once (flags past n_gu are in bounds and ignored); a
+      // short-circuit test would issue them one round trip after another
+      uint32_t fv[kLayerMaxGu / 64];
+#pragma unroll
+      for (int i = 0; i < kLayerMaxGu / 64; i++) fv[i] = ld_agent(f + lane + 64 * i);
       bool d = true;
 #pragma unroll
-      for (int i = 0; i < kLayerMaxGu / 64; i++)
-        d = d && (lane + 64 * i >= n_gu || ld_agent(f + lane + 64 * i) == want);
+      for (int i = 0; i < kLayerMaxGu / 64; i++) d = d & ((lane + 64 * i >= n_gu) | (fv[i] == want));
       if (__all(d)) break;
       if (n >= la.spin_limit) {
         wfail = true;
