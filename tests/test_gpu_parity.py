@@ -606,6 +606,29 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
         assert np.array_equal(outs[0], o), f"shape {shape} down {down}"
 
 
+@pytest.mark.parametrize("H,E", [(64, 8), (64, 32), (512, 128)])
+def test_batch_grouping_in_router_and_separate(orc, H, E):
+    """The router's last block groups the entries by expert when its x staging holds the
+    grouping's LDS (18 E ints within one token's staging: H = 64 with 8 experts, 512 with 128),
+    else the separate grouping kernel runs (H = 64 with 32 experts); both give the oracle's
+    routing and outputs, on the GEMM and the GEMV paths, over repeated calls."""
+    I, k = 32, 4
+    L = syn.make_layer(H, I, E, seed=440 + E, scale_lo=120, scale_hi=126, router_sigma=0.2)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    d.preload_layer(0, L)
+    for T in (2, 5, 70):
+        x = syn.hidden(T, H, seed=441 + T)
+        want, _, idx, _ = orc.moe_layer(x, L, k)
+        for gemm in (2, 0):
+            d.set_batch_gemm(gemm)
+            for _ in range(2):
+                got = d.layer_forward(0, x, k)
+                assert_rel_l2(got, want, f"H={H} E={E} T={T} gemm {gemm}")
+        gidx, _ = d.router_topk(0, x, k)
+        assert np.array_equal(gidx, idx)
+    d.close()
+
+
 def test_batch_gemm_adaptive_dropped_slots(orc):
     """Adaptive top-k drops slots: their entries are absent from the expert groups."""
     H, I, E = 256, 128, 8
