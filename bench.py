@@ -199,7 +199,7 @@ def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers
     disp.synchronize()
     kt = {name: disp.get_timing(kid) for kid, name in
           enumerate(["route", "bucket", "gate_up", "down", "combine", "decode_gate_up",
-                     "decode_down", "decode_layer", "split"])}
+                     "decode_down", "decode_layer", "reserved"])}
     disp.set_timing(False)
     if graph:
         check(L.moe_graph_destroy(graph))

@@ -311,10 +311,11 @@ int moe_graph_destroy(void *graph_exec);
 /* Per-kernel GPU time of the last device forward calls, accumulated with HIP events on the
  * stream the kernels run on when enabled (no reference counterpart). */
 int moe_set_timing(moe_ctx *ctx, int enabled);
-/* kernel: 0 route, 1 bucket, 2 gate_up, 3 down, 4 combine, 5 single-token router+gate_up,
- * 6 single-token down+combine, 7 single-token layer in one launch, 8 activation split of a
- * batch (grouped GEMM path; kernels 2 and 3 are then the grouped GEMMs), 9 RMSNorm and residual
- * add of moe_block_forward where they are not fused.
+/* kernel: 0 route (on the grouped GEMM path also the activation records and, mostly, the
+ * grouping by expert), 1 bucket (the separate grouping), 2 gate_up, 3 down, 4 combine,
+ * 5 single-token router+gate_up, 6 single-token down+combine, 7 single-token layer in one
+ * launch, 8 reserved (no kernel records it), 9 RMSNorm and residual add of moe_block_forward
+ * where they are not fused.
  * Returns accumulated milliseconds
  * and launch count since the last reset; synchronises the context stream. */
 int moe_get_timing(moe_ctx *ctx, int kernel, double *ms, uint64_t *launches);

@@ -10,4 +10,4 @@ from .dispatcher import (DeviceBuffer, GpuMoeDispatcher, mxfp4_dequant, mxfp4_ma
                          mxfp4_pack, safetensors_find)
 
 (KERNEL_ROUTE, KERNEL_BUCKET, KERNEL_GATE_UP, KERNEL_DOWN, KERNEL_COMBINE, KERNEL_DECODE_GATE_UP,
- KERNEL_DECODE_DOWN, KERNEL_DECODE_LAYER, KERNEL_SPLIT, KERNEL_NORM) = range(10)
+ KERNEL_DECODE_DOWN, KERNEL_DECODE_LAYER, KERNEL_RESERVED, KERNEL_NORM) = range(10)

@@ -90,7 +90,7 @@ struct Work {
 
 enum {
   K_ROUTE = 0, K_BUCKET, K_GATE_UP, K_DOWN, K_COMBINE, K_DECODE_GATE_UP, K_DECODE_DOWN,
-  K_DECODE_LAYER, K_SPLIT, K_NORM, K_COUNT
+  K_DECODE_LAYER, K_RESERVED, K_NORM, K_COUNT
 };
 
 struct TimingRec {
