@@ -1,19 +1,34 @@
 // One MXFP4 matvec y = W x in one launch (the matvec of session.rs:16-85, here on the resident
-// tile16 layout): one block per 16-row tile, whose 4 wavefronts split K (wavefront w takes
-// steps [6w, 6w + 6), 4 MXFP4 blocks per step). Each wavefront issues its weight loads first;
+// tile16 layout): one block per 16-row tile, whose kMvWaves wavefronts split K (wavefront w
+// takes steps [kMvSteps w, kMvSteps (w + 1)), 4 MXFP4 blocks per step). Each wavefront issues
+// its weight loads first;
 // while they are in flight the block splits x into the 4-term fp8 activation record in LDS
-// (split8_fp8); then every wavefront runs the block-scaled MFMA over its steps and the four
-// partial sums are added in wavefront order.
+// (split8_fp8); then every wavefront runs the block-scaled MFMA over its steps and the partial
+// sums are added in wavefront order.
 #include "device.hpp"
 #include "kernels.hpp"
 
 namespace moe {
 namespace {
 
-constexpr int kMvWaves = 4;
+constexpr int kMvWaves = 8;
 constexpr int kMvNs = 24;                    // steps per tile: K <= 3072
 constexpr int kMvSteps = kMvNs / kMvWaves;   // steps per wavefront
 using MvAct = ActRecord<kMvNs>;
+static_assert(kMvNs % kMvWaves == 0, "whole step ranges");
+
+// The MFMA sweep of wavefront wv's step range, with the range as a template constant (so every
+// scale word index is static).
+template <int W>
+__device__ __forceinline__ f32x4 mv_steps(int wv, const uint4 (&raw)[kMvSteps], const uint32_t *sw,
+                                          const uint8_t *s_x, const uint32_t *bsw, int lane) {
+  if constexpr (W + 1 == kMvWaves) {
+    return tile_mfma_f8_steps<kMvNs, kMvSteps, W * kMvSteps>(raw, sw, s_x, bsw, lane);
+  } else {
+    if (wv == W) return tile_mfma_f8_steps<kMvNs, kMvSteps, W * kMvSteps>(raw, sw, s_x, bsw, lane);
+    return mv_steps<W + 1>(wv, raw, sw, s_x, bsw, lane);
+  }
+}
 
 __global__ __launch_bounds__(64 * kMvWaves) void k_matvec_fp4(const uint8_t *mat, PackDims d,
                                                               const float *x, float *y) {
@@ -66,20 +81,18 @@ __global__ __launch_bounds__(64 * kMvWaves) void k_matvec_fp4(const uint8_t *mat
   // 3. the wavefront's steps on the block-scaled MFMA, the 4 term columns summed
   uint32_t bsw[kMvNs / 4];
   load_bsw<kMvNs>(s_x, bsw, lane);
-  f32x4 acc;
-  switch (wv) {  // the step range as a constant, so every scale word index is static
-    case 0: acc = tile_mfma_f8_steps<kMvNs, kMvSteps, 0>(raw, sw, s_x, bsw, lane); break;
-    case 1: acc = tile_mfma_f8_steps<kMvNs, kMvSteps, kMvSteps>(raw, sw, s_x, bsw, lane); break;
-    case 2: acc = tile_mfma_f8_steps<kMvNs, kMvSteps, 2 * kMvSteps>(raw, sw, s_x, bsw, lane); break;
-    default: acc = tile_mfma_f8_steps<kMvNs, kMvSteps, 3 * kMvSteps>(raw, sw, s_x, bsw, lane); break;
-  }
+  const f32x4 acc = mv_steps<0>(wv, raw, sw, s_x, bsw, lane);
   float v[4];
   sum_terms(acc, v);
   if (j == 0) *reinterpret_cast<float4 *>(&s_p[wv][4 * g]) = make_float4(v[0], v[1], v[2], v[3]);
   __syncthreads();
   // 4. the partial sums in wavefront order
-  if (tid < 16)
-    y[(size_t)t * 16 + tid] = canon_nan(((s_p[0][tid] + s_p[1][tid]) + s_p[2][tid]) + s_p[3][tid]);
+  if (tid < 16) {
+    float sum = s_p[0][tid];
+#pragma unroll
+    for (int w = 1; w < kMvWaves; w++) sum = sum + s_p[w][tid];
+    y[(size_t)t * 16 + tid] = canon_nan(sum);
+  }
 }
 
 }  // namespace
