@@ -533,12 +533,51 @@ __global__ __launch_bounds__(256) void k_combine(const float *o, const int32_t *
       make_float4(canon_nan(acc[0]), canon_nan(acc[1]), canon_nan(acc[2]), canon_nan(acc[3]));
 }
 
+// k_combine for a fixed k: every slot's row load is issued before the first product, instead of
+// one round trip per slot (the same products and sums in the same order).
+template <int K>
+__global__ __launch_bounds__(256) void k_combine_k(const float *o, const int32_t *pos,
+                                                   const float *w, int T, int H, int skip_nonfinite,
+                                                   float *y) {
+  const int h4 = H / 4;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)T * h4) return;
+  const int t = (int)(i / h4), d4 = (int)(i % h4);
+  int p[K];
+  float ws[K];
+  float4 v[K];
+#pragma unroll
+  for (int s = 0; s < K; s++) {
+    p[s] = pos[(size_t)t * K + s];
+    ws[s] = w[(size_t)t * K + s];
+  }
+#pragma unroll
+  for (int s = 0; s < K; s++)  // a dropped slot (p < 0) reads row 0 and is not used
+    v[s] = reinterpret_cast<const float4 *>(o + (size_t)(p[s] < 0 ? 0 : p[s]) * H)[d4];
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < K; s++) {
+    if (p[s] < 0) continue;
+    const float vv[4] = {v[s].x, v[s].y, v[s].z, v[s].w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      if (skip_nonfinite && !isfinite(vv[c])) continue;
+      acc[c] = acc[c] + ws[s] * vv[c];
+    }
+  }
+  reinterpret_cast<float4 *>(y + (size_t)t * H)[d4] =
+      make_float4(canon_nan(acc[0]), canon_nan(acc[1]), canon_nan(acc[2]), canon_nan(acc[3]));
+}
+
 hipError_t launch_combine(const float *o, const int32_t *pos, const float *w, int T, int k, int H,
                           int skip_nonfinite, float *y, hipStream_t s) {
   if (H % 4 || T < 1 || k < 1) return hipErrorInvalidValue;
   const size_t n = (size_t)T * (H / 4);
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, o, pos, w, T,
-                     k, H, skip_nonfinite, y);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  if (k == 4)
+    hipLaunchKernelGGL(k_combine_k<4>, grid, block, 0, s, o, pos, w, T, H, skip_nonfinite, y);
+  else
+    hipLaunchKernelGGL(k_combine, grid, block, 0, s, o, pos, w, T, k, H, skip_nonfinite, y);
   return hipGetLastError();
 }
 
