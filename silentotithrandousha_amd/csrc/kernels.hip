@@ -135,19 +135,38 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
 #pragma unroll
     for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
   }
-  for (int tb = 0; tb < nt; tb++) {
-    const float *x = a.x + (size_t)(t0 + tb) * H;
-    uint16_t *xs = a.xsplit ? a.xsplit + (size_t)(t0 + tb) * 2 * H : nullptr;
-    for (int k = threadIdx.x; k < Hp; k += kRouteThreads) {
-      const float v = k < H ? x[k] : 0.0f;
-      s_x[tb * Hp + k] = v;
-      if (xs && k < H) {
-        uint16_t hi, lo;
-        split_bf16(v, hi, lo);
-        xs[k] = hi;
-        xs[H + k] = lo;
-      }
+  auto stage = [&](int tb, int k, float xv) {
+    s_x[tb * Hp + k] = xv;
+    if (a.xsplit && k < H) {
+      uint16_t *xs = a.xsplit + (size_t)(t0 + tb) * 2 * H;
+      uint16_t hi, lo;
+      split_bf16(xv, hi, lo);
+      xs[k] = hi;
+      xs[H + k] = lo;
     }
+  };
+  if constexpr (KI > 0) {
+    // the chain length is KI * 512 values: every x load of the block's tokens in flight at once
+    // (a loop with a runtime trip count waited for each load before the next)
+    constexpr int kPer = (KI * 512 + kRouteThreads - 1) / kRouteThreads;
+    float xv[TB][kPer];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+      for (int q = 0; q < kPer; q++) {
+        const int k = (int)threadIdx.x + q * kRouteThreads;
+        xv[tb][q] = tb < nt && k < H ? a.x[(size_t)(t0 + tb) * H + k] : 0.0f;
+      }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+      for (int q = 0; q < kPer; q++) {
+        const int k = (int)threadIdx.x + q * kRouteThreads;
+        if (tb < nt && k < Hp) stage(tb, k, xv[tb][q]);
+      }
+  } else {
+    for (int tb = 0; tb < nt; tb++)
+      for (int k = threadIdx.x; k < Hp; k += kRouteThreads) stage(tb, k, k < H ? a.x[(size_t)(t0 + tb) * H + k] : 0.0f);
   }
   __syncthreads();
   if (a.xrec) {  // the grouped GEMM's activation records of the block's tokens (rec_split_half)
