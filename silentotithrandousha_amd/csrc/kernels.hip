@@ -41,9 +41,14 @@ __device__ __forceinline__ void bucket_block(const int32_t *idx, int T, int k, i
   auto ld_idx = [&](int n) {
     return kAgentLoads ? (int)ld_agent(reinterpret_cast<const uint32_t *>(idx) + n) : idx[n];
   };
-  for (int n = tid; n < N; n += 1024) {
-    int e = ld_idx(n);
-    if (e >= 0) atomicAdd(&s_count[e], 1);
+  // counts, 8 loads in flight per thread at a time (one round trip per 8 K entries)
+  for (int n0 = tid; n0 < N; n0 += 8 * 1024) {
+    int ev[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) ev[i] = n0 + 1024 * i < N ? ld_idx(n0 + 1024 * i) : -1;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (ev[i] >= 0) atomicAdd(&s_count[ev[i]], 1);
   }
   __syncthreads();
   if (tid == 0) {
@@ -61,9 +66,11 @@ __device__ __forceinline__ void bucket_block(const int32_t *idx, int T, int k, i
     *n_active = na;
   }
   __syncthreads();
+  int e_next = tid < N ? ld_idx(tid) : -1;
   for (int c0 = 0; c0 < N; c0 += 1024) {
     const int n = c0 + tid;
-    const int e = n < N ? ld_idx(n) : -1;
+    const int e = e_next;
+    e_next = n + 1024 < N ? ld_idx(n + 1024) : -1;  // the next chunk's entry, in flight meanwhile
     // lanes of this wavefront holding the same value (9-bit match through ballots)
     const uint32_t v = (uint32_t)(e + 1);
     uint64_t same = ~0ull;
