@@ -809,10 +809,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *x, int T, int H, c
   const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float *xr = x + (size_t)t * H;
-  const float r = rms_inv_wave(xr, H, eps, lane);
-  for (int d = lane; d < H; d += 64) {
-    const float v = xr[d] * r;
-    n[(size_t)t * H + d] = v * gamma[d];
+  // rms_inv_wave's arithmetic with kNB loads in flight per lane at a time (a loop with a runtime
+  // trip count waits for each load in turn)
+  constexpr int kNB = 16;
+  float p = 0.0f;
+  for (int i0 = lane; i0 < H; i0 += 64 * kNB) {
+    float v[kNB];
+#pragma unroll
+    for (int u = 0; u < kNB; u++) v[u] = i0 + 64 * u < H ? xr[i0 + 64 * u] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < kNB; u++) {
+      if (i0 + 64 * u >= H) break;
+      const float sq = v[u] * v[u];
+      p = p + sq;
+    }
+  }
+  const float r = 1.0f / sqrtf(wave_sum_xor(p) / (float)H + eps);
+  for (int d0 = lane; d0 < H; d0 += 64 * kNB) {
+    float v[kNB], g[kNB];
+#pragma unroll
+    for (int u = 0; u < kNB; u++) {
+      const bool in = d0 + 64 * u < H;
+      v[u] = in ? xr[d0 + 64 * u] : 0.0f;
+      g[u] = in ? gamma[d0 + 64 * u] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kNB; u++) {
+      if (d0 + 64 * u >= H) break;
+      const float vr = v[u] * r;
+      n[(size_t)t * H + d0 + 64 * u] = vr * g[u];
+    }
   }
 }
 
