@@ -1,15 +1,19 @@
 """Benchmark of the MXFP4 MoE path on one MI355X.
 
-Default workload (config 2 of the benchmark's configuration list): one GPT-OSS-20B-shaped MoE layer at decode batch 1 —
-router 2880->32 (bf16), top-4, 4 experts of gate_up 2880->5760 + down 2880->2880 in MXFP4,
-interleaved SwiGLU, weighted combine. A step is one token through one layer. To keep the
-256 MB MALL from serving the weights, 24 independent layers (10.2 GB of experts) stay
-resident and consecutive steps walk through them with distinct tokens, so every step
-streams its experts from HBM.
+The headline line (`value`) is config 2 of the benchmark's configuration list: one
+GPT-OSS-20B-shaped MoE layer at decode batch 1 — router 2880->32 (bf16), top-4, 4 experts of
+gate_up 2880->5760 + down 2880->2880 in MXFP4, interleaved SwiGLU, weighted combine. A step is
+one token through one layer. To keep the 256 MB MALL from serving the weights, 24 independent
+layers (10.2 GB of experts) stay resident and consecutive steps walk through them with
+distinct tokens, so every step streams its experts from HBM.
 
-Prints ONE JSON line (see the repository's benchmark contract). Other workloads
-(--workload matvec|decode64|prefill|decode1_120b|prefill_120b) print the same kind of line
-as well; the driver runs the default.
+The default run (`--workload all`) also times the other configurations in the same process and
+reports each under `configs` with its own dominant-kernel roofline: config 1 (one 2880x2880
+MXFP4 matvec), config 3 (64 tokens through one layer), config 4 (4096 tokens through all 24
+layers), config 5 (a 120B-shaped layer, 128 experts, at 1 and 2048 tokens). Those use their own
+step counts (in each entry); --steps / --warmup apply to the headline.
+
+Prints ONE JSON line. `--workload <name>` runs one configuration alone (for profiling).
 """
 import argparse
 import ctypes
@@ -30,7 +34,24 @@ from silentotithrandousha_amd._ffi import check, lib  # noqa: E402
 METRIC = "MoE layer tokens/s @GPT-OSS-20B shape (b=1,64,4096) + % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 MXFP4_PEAK_TFLOPS = 10100.0
-BF16_PEAK_TFLOPS = 2500.0
+H20 = I20 = 2880
+
+ARITH_DECODE = ("MXFP4 weights as stored (E2M1 + E8M0) on the block-scaled MFMA; x as 4 fp8 e4m3 "
+                "terms (exact to 2^-16), h as 4 fixed-exponent fp8 terms; f32 accumulate")
+ARITH_GEMM = ("MXFP4 weights as stored (E2M1 + E8M0) on the block-scaled MFMA; activations as 3 "
+              "fp6 E2M3 terms per 32-value block (exact to ~2^-13 of the block maximum); f32 "
+              "accumulate")
+DTYPE_DECODE = "mxfp4 x f32(4 fp8 terms), f32 acc"
+DTYPE_GEMM = "mxfp4 x f32(3 fp6 terms), f32 acc"
+
+# workload -> (config name, experts, tokens per layer, layers per step, default steps, warmup)
+WORKLOADS = {
+    "decode1": ("config2 gpt-oss-20b moe layer decode b=1", 32, 1, 1, 4800, 480),
+    "decode64": ("config3 gpt-oss-20b moe layer decode b=64", 32, 64, 1, 960, 96),
+    "prefill": ("config4 gpt-oss-20b moe prefill 4096 tokens x 24 layers", 32, 4096, 24, 8, 2),
+    "decode1_120b": ("config5 gpt-oss-120b moe layer b=1", 128, 1, 1, 4800, 480),
+    "prefill_120b": ("config5 gpt-oss-120b moe layer 2048 tokens", 128, 2048, 1, 48, 8),
+}
 
 
 def log(msg):
@@ -38,15 +59,16 @@ def log(msg):
 
 
 # ------------------------------------------------------------------ algorithmic bytes / flops
-# Checkpoint-format bytes of one expert (MXFP4 nibbles + E8M0 scales + bf16 biases).
 def expert_bytes(H, I):
+    """Checkpoint-format bytes of one expert's gate_up and down (MXFP4 nibbles + E8M0 scales +
+    bf16 biases)."""
     nbh, nbi = H // 32, I // 32
     gu = 2 * I * nbh * 16 + 2 * I * nbh + 2 * I * 2
     dn = H * nbi * 16 + H * nbi + H * 2
     return gu, dn
 
 
-def layer_traffic(H, I, E, k, T, active):
+def layer_traffic(H, I, E, T, active):
     """Algorithmic HBM bytes of one layer step: `active` experts' weights once, the router
     (bf16 W + f32 bias) once, activations in and out in f32."""
     gu, dn = expert_bytes(H, I)
@@ -57,10 +79,27 @@ def layer_flops(H, I, E, k, T):
     return 2.0 * T * E * H + 2.0 * T * k * (2 * I * H + H * I)
 
 
-# ------------------------------------------------------------------ resident synthetic layers
-class Layers:
-    def __init__(self, disp, H, I, E, n_layers, seed=1234):
-        self.disp, self.H, self.I, self.E = disp, H, I, E
+def expected_active(E, k, T):
+    """Expected distinct experts of T tokens routed to k of E experts each (uniform routing)."""
+    if T == 1:
+        return min(E, k)
+    return E * (1.0 - (1.0 - k / E) ** T)
+
+
+# ------------------------------------------------------------------ resident synthetic model
+class Model:
+    """One dispatcher holding n_layers resident synthetic layers of one shape, generated on the
+    device (nibbles uniform, E8M0 118..130, biases bf16 N(0, 0.01), router bf16 N(0, 0.02))."""
+
+    def __init__(self, H, I, E, n_layers, opts, seed=1234):
+        self.H, self.I, self.E, self.n_layers = H, I, E, n_layers
+        self.disp = GpuMoeDispatcher(H, I, 7.0)
+        self.disp.set_fused_decode(opts.fused)
+        self.disp.set_batch_gemm(opts.batch_gemm)
+        self.disp.set_gemm_shape(opts.gemm_shape, opts.gemm_shape_down)
+        self.disp.set_gemm_band(opts.gemm_band)
+        log(f"synthesising {n_layers} layers x {E} experts "
+            f"({n_layers * E * sum(expert_bytes(H, I)) / 1e9:.2f} GB MXFP4)")
         nbh, nbi = H // 32, I // 32
         sizes = dict(gub=E * 2 * I * nbh * 16, gus=E * 2 * I * nbh, gubias=E * 2 * I * 4,
                      db=E * H * nbi * 16, ds=E * H * nbi, dbias=E * H * 4)
@@ -75,17 +114,19 @@ class Layers:
             check(L.moe_synth_fill_device(stage["db"].ptr, sizes["db"], 0, s0 + 4, 0, 255, None))
             check(L.moe_synth_fill_device(stage["ds"].ptr, sizes["ds"], 0, s0 + 5, 118, 130, None))
             check(L.moe_synth_fill_device(stage["dbias"].ptr, sizes["dbias"] // 4, 3, s0 + 6, 0.01, 0, None))
-            check(L.moe_preload_layer_device(disp.ctx, l, E, stage["gub"].ptr, stage["gus"].ptr,
+            check(L.moe_preload_layer_device(self.disp.ctx, l, E, stage["gub"].ptr, stage["gus"].ptr,
                                              stage["gubias"].ptr, stage["db"].ptr, stage["ds"].ptr,
                                              stage["dbias"].ptr, None))
             rw = syn.bf16_bits(rng.normal(0, 0.02, size=(E, H)).astype(np.float32))
             rb = np.zeros(E, np.float32)
-            check(L.moe_preload_router(disp.ctx, l, E, rw.ctypes.data, rb.ctypes.data))
-            disp.synchronize()
-            if l % 6 == 5 or l == n_layers - 1:
-                log(f"resident layers {l + 1}/{n_layers}")
+            check(L.moe_preload_router(self.disp.ctx, l, E, rw.ctypes.data, rb.ctypes.data))
+            self.disp.synchronize()
         for b in stage.values():
             b.close()
+        log(f"resident: {n_layers} layers")
+
+    def close(self):
+        self.disp.close()
 
 
 class StreamEvents:
@@ -123,162 +164,160 @@ class StreamEvents:
             self.hip.hipEventDestroy(e)
 
 
-# ------------------------------------------------------------------ decode / prefill bench
-def run_layer_bench(args, H, I, E, k, T, n_layers, workload, config_name, layers_per_step=1,
-                    mfma_bound=False):
-    """A step is `layers_per_step` consecutive resident layers, each on its own T tokens
-    (layers_per_step = 24 for the 24-layer prefill of config 4)."""
+def capture(disp, fn, first, count):
+    """A HIP graph of steps first .. first+count-1 on the context stream, launched once
+    (upload and first replay, untimed)."""
     L = lib()
-    disp = GpuMoeDispatcher(H, I, 7.0)
-    disp.set_fused_decode(args.fused)
-    disp.set_batch_gemm(args.batch_gemm)
-    disp.set_gemm_shape(args.gemm_shape, args.gemm_shape_down)
-    disp.set_gemm_band(args.gemm_band)
-    log(f"synthesising {n_layers} layers x {E} experts ({n_layers * E * sum(expert_bytes(H, I)) / 1e9:.2f} GB MXFP4)")
-    Layers(disp, H, I, E, n_layers)
-    P = max(n_layers * 10, 8) if T == 1 else 2 * n_layers
+    check(L.moe_graph_begin(disp.ctx))
+    for i in range(first, first + count):
+        fn(i)
+    g = ctypes.c_void_p()
+    check(L.moe_graph_end(disp.ctx, ctypes.byref(g)))
+    check(L.moe_graph_launch(disp.ctx, g.value))
+    disp.synchronize()
+    return g.value
+
+
+KERNELS = ["route", "bucket", "gate_up", "down", "combine", "decode_gate_up", "decode_down",
+           "decode_layer"]
+
+
+# ------------------------------------------------------------------ layer workloads (configs 2-5)
+def run_layer(model, workload, steps, warmup, graph=True, copy_mib=0, traffic_kib=0.0):
+    config_name, E, T, lps, _, _ = WORKLOADS[workload]
+    assert E == model.E
+    H, I, k, n_layers = model.H, model.I, 4, model.n_layers
+    disp, L = model.disp, lib()
+    P = max(n_layers * 10, 8) if T == 1 else max(2 * n_layers, 2)  # distinct token slots
     x = DeviceBuffer(P * T * H * 4)
     y = DeviceBuffer(P * T * H * 4)
     check(L.moe_synth_fill_device(x.ptr, P * T * H, 2, 99, 1.0, 0, None))
     disp.synchronize()
 
-    def step(i, stream=None):
-        for u in range(layers_per_step):
-            c = i * layers_per_step + u
+    def step(i):
+        for u in range(lps):
+            c = i * lps + u
             j = c % P
             check(L.moe_layer_forward_device(disp.ctx, c % n_layers, x.ptr + j * T * H * 4, T, k,
-                                             y.ptr + j * T * H * 4, stream))
+                                             y.ptr + j * T * H * 4, None))
 
-    log("warmup")
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     disp.synchronize()
+    if copy_mib:
+        copy_calibration(copy_mib)
 
-    if args.copy_mib:
-        copy_calibration(args.copy_mib)
-    graph = None
-    G = (P if layers_per_step == 1 else 1) if args.graph else 0
-    if args.graph:
-        check(L.moe_graph_begin(disp.ctx))
-        for i in range(G):
-            step(i)
-        g = ctypes.c_void_p()
-        check(L.moe_graph_end(disp.ctx, ctypes.byref(g)))
-        graph = g.value
-        check(L.moe_graph_launch(disp.ctx, graph))  # upload / first replay untimed
-        disp.synchronize()
-
-    log(f"timed region: {args.steps} steps ({'graph x' + str(G) if graph else 'eager'})")
+    # every timed step replays from a HIP graph: G steps per launch of the main graph, and the
+    # remainder of steps / G in a second graph
+    graphs = []
+    G = (min(steps, P) if lps == 1 else 1) if graph else 0
+    n_full, rem = divmod(steps, G) if G else (0, steps)
+    if G:
+        graphs.append((capture(disp, step, 0, G), n_full))
+        if rem:
+            graphs.append((capture(disp, step, n_full * G, rem), 1))
     disp.synchronize()
     region = StreamEvents(L.moe_stream(disp.ctx))
     t0 = time.perf_counter()
     region.start()
-    if graph:
-        n_full, rem = divmod(args.steps, G)
-        for _ in range(n_full):
-            check(L.moe_graph_launch(disp.ctx, graph))
-        for i in range(rem):
-            step(i)
+    if G:
+        for g, n in graphs:
+            for _ in range(n):
+                check(L.moe_graph_launch(disp.ctx, g))
     else:
-        for i in range(args.steps):
+        for i in range(steps):
             step(i)
     region.stop()
     disp.synchronize()
     elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
     region_ms = region.elapsed_ms()
     region.close()
+    for g, _ in graphs:
+        check(L.moe_graph_destroy(g))
 
-    # per-kernel durations: HIP events around every launch, same steps, eager
-    log("kernel timing region")
+    # per-kernel durations: HIP events around every launch, eager, over the same steps
     disp.set_timing(True)
     disp.reset_timing()
-    n_kt = min(args.steps, max(240 // layers_per_step, G))
+    n_kt = min(steps, max(240 // lps, 1))
     for i in range(n_kt):
         step(i)
     disp.synchronize()
-    kt = {name: disp.get_timing(kid) for kid, name in
-          enumerate(["route", "bucket", "gate_up", "down", "combine", "decode_gate_up",
-                     "decode_down", "decode_layer", "reserved"])}
+    kt = {name: disp.get_timing(kid) for kid, name in enumerate(KERNELS)}
     disp.set_timing(False)
-    if graph:
-        check(L.moe_graph_destroy(graph))
+    x.close()
+    y.close()
 
-    tokens_per_s = T * args.steps / elapsed
-    active = min(E, T * k) if T == 1 else E  # expected distinct experts per layer
-    traffic = layer_traffic(H, I, E, k, T, active) * layers_per_step
-    flops = layer_flops(H, I, E, k, T) * layers_per_step
-    gu_b, dn_b = expert_bytes(H, I)
-    dom = ("decode_layer" if kt["decode_layer"][1] else
-           "decode_gate_up" if kt["decode_gate_up"][1] else "gate_up")
-    gu_ms, gu_n = kt[dom]
-    gu_avg_s = gu_ms / max(gu_n, 1) / 1e3
+    ms_per_step = elapsed * 1e3 / steps
+    tokens_per_s = T * lps * steps / elapsed
+    active = expected_active(E, k, T)
+    traffic = layer_traffic(H, I, E, T, active) * lps
+    flops = layer_flops(H, I, E, k, T) * lps
+    gu_b, _ = expert_bytes(H, I)
+    dom = "decode_layer" if kt["decode_layer"][1] else "decode_gate_up" if kt["decode_gate_up"][1] else "gate_up"
+    d_ms, d_n = kt[dom]
+    d_avg_s = d_ms / max(d_n, 1) / 1e3
     timing_src = "HIP events around each launch (eager pass over the same steps)"
-    if dom == "decode_layer" and layers_per_step == 1:
+    if dom == "decode_layer" and lps == 1 and G:
         # every step is one launch of this kernel and nothing else: its average duration is the
-        # timed region's span between two events on its stream over the launch count, which
-        # leaves out the per-launch event and dispatch overhead of the eager brackets
-        gu_avg_s = region_ms / args.steps / 1e3
-        timing_src = "HIP events on the context stream around the timed region / launches"
+        # timed region's span between two events on its stream over the launch count, free of
+        # the per-launch event and dispatch overhead of the eager brackets
+        d_avg_s = region_ms / steps / 1e3
+        timing_src = "HIP events on the context stream around the graph-replayed timed region / launches"
     if dom == "decode_layer":  # the whole layer in one launch
-        gu_bytes = layer_traffic(H, I, E, k, T, active)
-        gu_flops = layer_flops(H, I, E, k, T)
+        d_bytes, d_flops = layer_traffic(H, I, E, T, active), layer_flops(H, I, E, k, T)
+        kname = "k_decode_layer"
     else:
-        gu_bytes = active * gu_b + T * H * 4 + T * k * I * 4
-        gu_flops = 2.0 * T * k * 2 * I * H
+        d_bytes = active * gu_b + T * H * 4 + T * k * I * 4
+        d_flops = 2.0 * T * k * 2 * I * H
+        kname = "k_gemm_fp8<gate_up>" if dom == "gate_up" else "k_decode_gate_up"
+    mfma_bound = T >= 4096  # config 4: arithmetic intensity above the MXFP4 ridge point
     res = {
-        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded; nibbles uniform, E8M0 118..130, router N(0,0.02) bf16, biases N(0,0.01) bf16, x N(0,1); device-generated)",
-        "config": {"workload": workload, "name": config_name, "hidden": H, "intermediate": I,
-                   "experts": E, "top_k": k, "tokens_per_layer": T, "layers_per_step": layers_per_step,
+        "value": round(tokens_per_s, 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "dtype": DTYPE_DECODE if T == 1 and dom == "decode_layer" else DTYPE_GEMM,
+        "config": {"workload": config_name, "name": workload, "hidden": H, "intermediate": I,
+                   "experts": E, "top_k": k, "tokens_per_layer": T, "layers_per_step": lps,
                    "resident_layers": n_layers,
                    "weights": "MXFP4 E2M1 + E8M0 (checkpoint layout repacked on preload)",
-                   "arithmetic": ("MXFP4 weights as stored on the block-scaled MFMA; x as 4 fp8 terms, h as "
-                                  "fixed-exponent fp8 terms; f32 accumulate" if T == 1 and args.fused else
-                                  "MXFP4 weights as stored on the block-scaled MFMA; activations as 3 E2M3 "
-                                  "terms (grouped GEMM) or bf16 hi+lo (GEMV path); f32 accumulate"),
-                   "graph_replay": bool(graph), "fused_decode": bool(args.fused and T == 1)},
-        "roofline": {"bound": "hbm",
-                     "kernel": {"decode_layer": "k_decode_layer", "decode_gate_up": "k_decode_gate_up",
-                                "gate_up": "k_gemm_fp8<gate_up>"}[dom],
-                     "achieved": round(gu_bytes / gu_avg_s / 1e9, 1) if gu_n else None,
+                   "arithmetic": ARITH_DECODE if dom == "decode_layer" else ARITH_GEMM,
+                   "graph_replay": ("all steps: %d x graph of %d steps%s" % (n_full, G, f" + graph of {rem}" if rem else "")
+                                    if G else "none (eager launches)")},
+        "roofline": {"bound": "hbm", "kernel": kname,
+                     "achieved": round(d_bytes / d_avg_s / 1e9, 1) if d_n else None,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_bytes / gu_avg_s / 1e9 / HBM_PEAK_GBS, 4) if gu_n else None,
-                     "traffic": args.traffic_kib * 1024 if args.traffic_kib else None,
-                     "algorithmic_bytes_per_launch": gu_bytes,
-                     "avg_launch_us": round(gu_avg_s * 1e6, 3),
-                     "timing": timing_src,
-                     "mfma_TFLOPs": round(gu_flops / gu_avg_s / 1e12, 2) if gu_n else None},
-        "layer_roofline": {"algorithmic_bytes_per_step": traffic, "flops_per_step": flops,
+                     "frac": round(d_bytes / d_avg_s / 1e9 / HBM_PEAK_GBS, 4) if d_n else None,
+                     "traffic": traffic_kib * 1024 if traffic_kib else None,
+                     "algorithmic_bytes_per_launch": int(d_bytes), "flops_per_launch": d_flops,
+                     "avg_launch_us": round(d_avg_s * 1e6, 3), "timing": timing_src,
+                     "TFLOPs": round(d_flops / d_avg_s / 1e12, 2) if d_n else None},
+        "layer_roofline": {"algorithmic_bytes_per_step": int(traffic), "flops_per_step": flops,
                            "achieved_GBps": round(traffic / (ms_per_step / 1e3) / 1e9, 1),
                            "frac_hbm": round(traffic / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                            "achieved_TFLOPs": round(flops / (ms_per_step / 1e3) / 1e12, 2),
                            "frac_mxfp4_peak": round(flops / (ms_per_step / 1e3) / 1e12 / MXFP4_PEAK_TFLOPS, 5)},
         "kernel_us": {n: round(v[0] * 1e3 / max(v[1], 1), 3) for n, v in kt.items() if v[1]},
     }
-    if not args.traffic_kib:  # calibrated PMC measurement of the same kernel and workload
+    if mfma_bound and d_n:
+        # dense regime: the MFMA roofline against the MXFP4 peak, algorithmic flops (one
+        # MXFP4 x MXFP4 product per multiply-add; the path issues 3 activation terms)
+        res["roofline"].update(bound="mfma", achieved=round(d_flops / d_avg_s / 1e12, 2),
+                               peak=MXFP4_PEAK_TFLOPS, unit="TFLOP/s",
+                               frac=round(d_flops / d_avg_s / 1e12 / MXFP4_PEAK_TFLOPS, 5),
+                               hbm_GBps=round(d_bytes / d_avg_s / 1e9, 1))
+    if not traffic_kib:  # calibrated PMC measurement of the same kernel and workload
         tf = os.path.join(ROOT, "profiles", "traffic.json")
-        kname = res["roofline"]["kernel"]
         if os.path.exists(tf):
             rec = json.load(open(tf)).get(kname)
-            if rec and rec.get("workload") == config_name:
+            if rec and rec.get("workload") == workload:
                 res["roofline"]["traffic"] = rec["bytes_per_launch"]
                 res["roofline"]["traffic_source"] = rec["source"]
-    if mfma_bound and gu_n:
-        # dense regime: the MFMA roofline against the MXFP4 peak (the arithmetic runs on the
-        # bf16 MFMA with a hi+lo split of the activations, i.e. 2x these flops)
-        res["roofline"].update(bound="mfma", achieved=round(gu_flops / gu_avg_s / 1e12, 2),
-                               peak=MXFP4_PEAK_TFLOPS, unit="TFLOP/s",
-                               frac=round(gu_flops / gu_avg_s / 1e12 / MXFP4_PEAK_TFLOPS, 5),
-                               hbm_GBps=round(gu_bytes / gu_avg_s / 1e9, 1))
-    disp.close()
     return res
 
 
-def run_matvec_bench(args):
-    """Config 1: y = W x, W 2880x2880 MXFP4; 64 distinct copies back to back."""
+# ------------------------------------------------------------------ config 1: one MXFP4 matvec
+def run_matvec(steps, warmup, graph=True):
+    """y = W x, W 2880x2880 MXFP4; 96 distinct copies (283 MB, above the 256 MB MALL) back to
+    back in a HIP graph."""
     L = lib()
     from silentotithrandousha_amd import mxfp4_matvec, mxfp4_pack
     R = C = 2880
@@ -296,61 +335,53 @@ def run_matvec_bench(args):
     y = DeviceBuffer(R * 4)
     check(L.moe_synth_fill_device(x.ptr, C, 2, 5, 1.0, 0, None))
     disp.synchronize()
-    for i in range(args.warmup):
+
+    def one(i):
         mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
+
+    for i in range(warmup):
+        one(i)
     disp.synchronize()
-    # the copies back to back in one HIP graph (a matvec is ~0.6 us of HBM traffic, below the
-    # cost of a host launch), replayed for the timed region
-    graph = None
-    if args.graph:
-        check(L.moe_graph_begin(disp.ctx))
-        for i in range(copies):
-            mxfp4_matvec(disp, packed[i], R, C, x, y)
-        g = ctypes.c_void_p()
-        check(L.moe_graph_end(disp.ctx, ctypes.byref(g)))
-        graph = g.value
-        check(L.moe_graph_launch(disp.ctx, graph))
-        disp.synchronize()
-    reps = max(1, args.steps // copies) if graph else 0
-    steps = reps * copies if graph else args.steps
+    g = capture(disp, one, 0, copies) if graph else None
+    reps = max(1, steps // copies) if graph else 0
+    steps = reps * copies if graph else steps
     region = StreamEvents(L.moe_stream(disp.ctx))
     t0 = time.perf_counter()
     region.start()
     if graph:
         for _ in range(reps):
-            check(L.moe_graph_launch(disp.ctx, graph))
+            check(L.moe_graph_launch(disp.ctx, g))
     else:
         for i in range(steps):
-            mxfp4_matvec(disp, packed[i % copies], R, C, x, y)
+            one(i)
     region.stop()
     disp.synchronize()
     el = time.perf_counter() - t0
     region_s = region.elapsed_ms() / 1e3
     region.close()
-    if graph:
-        check(L.moe_graph_destroy(graph))
+    if g:
+        check(L.moe_graph_destroy(g))
+    for b in packed + [blocks, scales, x, y]:
+        b.close()
+    disp.close()
     byts = R * nb * 17 + C * 4 + R * 4
-    gbs = byts * steps / el / 1e9
     kgbs = byts * steps / region_s / 1e9  # one k_matvec_fp4 launch per matvec
-    return {"metric": "MXFP4 matvec 2880x2880 GB/s", "value": round(gbs, 1),
-            "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
-            "ms_per_step": round(el * 1e3 / steps, 6), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "config1 matvec 2880x2880", "copies": copies,
-                       "graph_replay": bool(graph)},
-            "roofline": {"bound": "hbm", "kernel": "k_matvec_fp4",
-                         "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(kgbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "algorithmic_bytes_per_launch": byts,
+    return {"value": round(byts * steps / el / 1e9, 1), "unit": "GB/s",
+            "matvecs_per_s": round(steps / el, 1), "steps": steps, "warmup": warmup,
+            "ms_per_step": round(el * 1e3 / steps, 6), "dtype": DTYPE_DECODE,
+            "config": {"workload": "config1 mxfp4 matvec 2880x2880", "copies": copies,
+                       "graph_replay": f"{reps} x graph of {copies} matvecs" if graph else "none"},
+            "roofline": {"bound": "hbm", "kernel": "k_matvec_fp4", "achieved": round(kgbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes_per_launch": byts,
                          "avg_launch_us": round(region_s / steps * 1e6, 3),
                          "timing": "HIP events on the context stream around the timed region / launches"}}
 
 
-def run_lm_head_bench(args, H, V):
+def run_lm_head(steps, warmup, H=2880, V=201088):
     """The next row after the MoE path: dispatch_lm_head (moe_dispatch.rs:624-683), logits[V] =
     W[V, H] x in f32 with the reference's f32 weights (201 088 x 2880 = 2.32 GB), device-resident
     input and logits."""
-    from silentotithrandousha_amd import DeviceBuffer
     rng = np.random.default_rng(9)
     log(f"lm head: {V} x {H} f32 ({V * H * 4 / 1e9:.2f} GB)")
     w = rng.standard_normal((V, H), dtype=np.float32)
@@ -360,13 +391,13 @@ def run_lm_head_bench(args, H, V):
     del w
     x = DeviceBuffer.from_array(rng.standard_normal(H, dtype=np.float32))
     y = DeviceBuffer(V * 4)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         disp.dispatch_lm_head_device(x, V, y)
     disp.synchronize()
     region = StreamEvents(lib().moe_stream(disp.ctx))
     t0 = time.perf_counter()
     region.start()
-    for _ in range(args.steps):
+    for _ in range(steps):
         disp.dispatch_lm_head_device(x, V, y)
     region.stop()
     disp.synchronize()
@@ -374,18 +405,15 @@ def run_lm_head_bench(args, H, V):
     region_s = region.elapsed_ms() / 1e3
     region.close()
     byts = V * H * 4 + H * 4 + V * 4
-    gbs = byts * args.steps / el / 1e9
-    kgbs = byts * args.steps / region_s / 1e9  # one k_lm_head launch per step
+    kgbs = byts * steps / region_s / 1e9  # one k_lm_head launch per step
     disp.close()
-    return {"metric": "LM head f32 GEMV 201088x2880 GB/s", "value": round(gbs, 1), "unit": "GB/s",
-            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "ms_per_step": round(el * 1e3 / args.steps, 6), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "f32", "data": "synthetic (weights N(0,0.02), x N(0,1))",
+    return {"value": round(byts * steps / el / 1e9, 1), "unit": "GB/s", "steps": steps,
+            "warmup": warmup, "ms_per_step": round(el * 1e3 / steps, 6), "dtype": "f32",
             "config": {"workload": "lm head (next row) 201088x2880 f32", "vocab": V, "hidden": H},
             "roofline": {"bound": "hbm", "kernel": "k_lm_head", "achieved": round(kgbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
                          "traffic": None, "algorithmic_bytes_per_launch": byts,
-                         "avg_launch_us": round(region_s / args.steps * 1e6, 3),
+                         "avg_launch_us": round(region_s / steps * 1e6, 3),
                          "timing": "HIP events on the context stream around the timed region / launches"}}
 
 
@@ -403,44 +431,107 @@ def copy_calibration(mib):
 
 
 # ------------------------------------------------------------------ CPU baseline
+def host_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "cpus_available": affinity}
+
+
 def cpu_baseline(seconds, H, I, E, k):
-    """The reference's live CPU MoE block restated in C (oracle/): router + top-4, cold fp16
-    expert cache (MXFP4 -> fp16 decode of the 4 selected experts, session.rs:860-941) and
-    cpu_expert_ffn with the NEON matvec order, one thread per selected expert (rayon over
-    k slots, session.rs:953-972), then the combine. Bounded sample, rank 0, N=1 only."""
+    """The reference's live CPU MoE block restated in C (oracle/), on config 2's layer shape:
+    router + top-4, then per selected expert cpu_expert_ffn with the NEON-order fp16 x f32
+    matvec on k threads (rayon over the k slots, session.rs:953-972) and the slot-order combine.
+    Three legs, each a bounded sample of `seconds`:
+      cold  — fp16 expert cache missing every expert (random routing over 32 experts with the
+              reference's 4 cache slots): MXFP4 -> fp16 decode of the 4 experts per token
+              (session.rs:860-941) — the reference's live path on this workload, the headline;
+      warm  — every selected expert already in the fp16 cache (matvecs only), its best case;
+      fp32  — the reference's f32 helpers (weights.rs:350-423 decode + sequential f32 matvec,
+              session.rs:75-85), the oracle's own path, on the oracle's OpenMP threads."""
     from oracle import orc
     layers = [syn.make_layer(H, I, E, seed=500 + i) for i in range(2)]
     xs = syn.hidden(64, H, seed=501)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        lay = layers[n % 2]
-        x = xs[n % 64]
+    legs = {}
+
+    def route(lay, x):
         logits = orc.router_logits(lay["router_w"], lay["router_b"], x, E, H)
         idx, w, _, _ = orc.topk(logits, k)
-        orc.live_moe_token(x, lay, idx[0], w[0], k)
+        return idx[0], w[0]
+
+    # cold: decode on every token
+    n, t0 = 0, time.perf_counter()
+    while True:
+        lay, x = layers[n % 2], xs[n % 64]
+        idx, w = route(lay, x)
+        orc.live_moe_token(x, lay, idx, w, k)
         n += 1
         el = time.perf_counter() - t0
-        if (el >= seconds and n >= 3) or n >= 1000:
+        if (el >= seconds and n >= 3) or n >= 2000:
             break
-    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": k, "kind": "port",
-            "sample": f"{n} tokens of the config-2 layer (2 synthetic layers, cold fp16 expert "
-                      f"cache: MXFP4->fp16 dequant + fp16xf32 matvec in the reference's NEON "
-                      f"order, {k} threads as rayon over the top-{k} slots), {el:.1f} s"}
+    legs["cold"] = {"value": round(n / el, 3), "unit": "tokens/s", "threads": k,
+                    "sample": f"{n} tokens, {el:.1f} s"}
+    # warm: two tokens of one layer alternate, so at most 2k fp16 entries are built (outside
+    # the timed calls) and every timed token finds its experts cached
+    cache, n, el = {}, 0, 0.0
+    while True:
+        li = 0
+        lay, x = layers[li], xs[n % 2]
+        idx, w = route(lay, x)
+        for e in idx:
+            if (li, int(e)) not in cache:
+                cache[(li, int(e))] = orc.live_expert_f16(lay, int(e))
+        ents = [cache[(li, int(e))] for e in idx]
+        t0 = time.perf_counter()
+        route(lay, x)
+        orc.live_moe_token_warm(x, H, I, ents, w, k)
+        el += time.perf_counter() - t0
+        n += 1
+        if (el >= seconds / 2 and n >= 3) or n >= 2000:
+            break
+    legs["warm"] = {"value": round(n / el, 3), "unit": "tokens/s", "threads": k,
+                    "sample": f"{n} tokens (2 alternating, {len(cache)} cached fp16 experts), {el:.1f} s timed"}
+    del cache
+    # fp32 path
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.moe_layer(xs[n % 64][None], layers[n % 2], k)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds / 2 and n >= 3) or n >= 2000:
+            break
+    legs["fp32"] = {"value": round(n / el, 3), "unit": "tokens/s", "threads": orc.omp_threads(),
+                    "sample": f"{n} tokens, {el:.1f} s"}
+    return {"value": legs["cold"]["value"], "unit": "tokens/s", "cores": k, "kind": "port",
+            "sample": (f"config-2 layer shape, 2 synthetic layers x {E} experts, 64 tokens cycled; "
+                       f"cold fp16 expert cache (the reference's live path under random routing): "
+                       f"{legs['cold']['sample']} on {k} threads (rayon over the top-{k} slots)"),
+            "legs": legs, "host": host_info()}
 
 
+# ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="default: per workload")
+    ap.add_argument("--steps", type=int, default=None, help="headline steps (default: per workload)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode1",
-                    choices=["decode1", "decode64", "prefill", "matvec", "decode1_120b", "prefill_120b", "lm_head"])
+    ap.add_argument("--workload", default="all", choices=["all", "matvec", "lm_head"] + list(WORKLOADS))
     ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--layers-120b", type=int, default=6)
     ap.add_argument("--no-graph", dest="graph", action="store_false")
     ap.add_argument("--no-fused", dest="fused", action="store_false",
                     help="single-token steps through the multi-kernel path")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--gemm-shape", type=int, default=0, choices=range(8), help="grouped GEMM block shape (tuning)")
     ap.add_argument("--gemm-shape-down", type=int, default=0, choices=range(8),
@@ -454,37 +545,56 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
-    dsteps, dwarm = {"decode1": (4800, 480), "decode1_120b": (4800, 480), "matvec": (4800, 480),
-                     "decode64": (960, 96), "prefill": (8, 2), "prefill_120b": (48, 8),
-                     "lm_head": (40, 4)}[args.workload]
-    args.steps = dsteps if args.steps is None else args.steps
-    args.warmup = dwarm if args.warmup is None else args.warmup
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding of this path (expert parallel / row split) is a design note, not built.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
-    H = I = 2880
-    if args.workload == "matvec":
-        res = run_matvec_bench(args)
-    elif args.workload == "lm_head":
-        res = run_lm_head_bench(args, H, 201088)
-    elif args.workload == "decode1":
-        res = run_layer_bench(args, H, I, 32, 4, 1, args.layers, "config2 gpt-oss-20b moe layer decode b=1", "decode1")
-    elif args.workload == "decode64":
-        res = run_layer_bench(args, H, I, 32, 4, 64, args.layers, "config3 gpt-oss-20b moe layer decode b=64", "decode64")
-    elif args.workload == "prefill":
-        res = run_layer_bench(args, H, I, 32, 4, 4096, args.layers,
-                              "config4 gpt-oss-20b moe prefill 4096 tokens x 24 layers", "prefill",
-                              layers_per_step=args.layers, mfma_bound=True)
-    elif args.workload == "decode1_120b":
-        res = run_layer_bench(args, H, I, 128, 4, 1, args.layers, "config5 gpt-oss-120b moe layer decode b=1", "decode1_120b")
+    head = "decode1" if args.workload == "all" else args.workload
+    dsteps, dwarm = {"matvec": (4800, 480), "lm_head": (40, 4)}.get(head, WORKLOADS.get(head, (0,) * 6)[4:])
+    steps = dsteps if args.steps is None else args.steps
+    warmup = dwarm if args.warmup is None else args.warmup
+    common = {"metric": METRIC, "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None,
+              "data": ("synthetic (seeded, device-generated; nibbles uniform 0..15, E8M0 118..130, "
+                       "router N(0,0.02) bf16, biases N(0,0.01) bf16, x N(0,1))")}
+    if head == "matvec":
+        common["metric"] = "MXFP4 matvec 2880x2880 GB/s (config 1)"
+    elif head == "lm_head":
+        common["metric"] = "LM head GEMV 201088x2880 GB/s"
+    t_start = time.perf_counter()
+    if head == "matvec":
+        res = run_matvec(steps, warmup, args.graph)
+    elif head == "lm_head":
+        res = run_lm_head(steps, warmup)
     else:
-        res = run_layer_bench(args, H, I, 128, 4, 2048, args.layers, "config5 gpt-oss-120b moe layer 2048 tokens", "prefill_120b")
-    if args.cpu and rank == 0 and args.workload == "decode1":
+        E = WORKLOADS[head][1]
+        m = Model(H20, I20, E, args.layers if E == 32 else args.layers_120b, args)
+        res = run_layer(m, head, steps, warmup, args.graph, args.copy_mib, args.traffic_kib)
+        log(f"{head}: {res['value']} tokens/s ({res['ms_per_step']} ms/step)")
+        extras = {}
+        if args.workload == "all":
+            for w, key in (("decode64", "config3_decode64"), ("prefill", "config4_prefill_4096x24")):
+                extras[key] = run_layer(m, w, WORKLOADS[w][4], WORKLOADS[w][5], args.graph)
+                log(f"{w}: {extras[key]['value']} tokens/s")
+            m.close()
+            m = Model(H20, I20, 128, args.layers_120b, args)
+            for w, key in (("decode1_120b", "config5_120b_decode1"), ("prefill_120b", "config5_120b_2048")):
+                extras[key] = run_layer(m, w, WORKLOADS[w][4], WORKLOADS[w][5], args.graph)
+                log(f"{w}: {extras[key]['value']} tokens/s")
+            m.close()
+            extras["config1_matvec"] = run_matvec(4800, 480, args.graph)
+            log(f"matvec: {extras['config1_matvec']['value']} GB/s")
+            res["configs"] = extras
+        else:
+            m.close()
+    out = dict(common)
+    out.update(res)
+    if args.cpu and rank == 0 and head == "decode1":
         log("cpu baseline")
-        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, H, I, 32, 4)
-    print(json.dumps(res), flush=True)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, H20, I20, 32, 4)
+    log(f"done in {time.perf_counter() - t_start:.1f} s")
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -535,6 +535,18 @@ typedef struct live_job {
   float *out;
 } live_job;
 
+void orc_live_expert_f16(const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                         const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                         size_t H, size_t I, uint16_t *gu, uint16_t *gub, uint16_t *d, uint16_t *db) {
+  orc_dequant_gate_up_reordered_f16(gu_blocks, gu_scales, I, H, gu);
+  for (size_t i = 0; i < I; i++) {
+    gub[i] = orc_f32_to_f16_rne(gu_bias[2 * i]);
+    gub[I + i] = orc_f32_to_f16_rne(gu_bias[2 * i + 1]);
+  }
+  orc_dequant_down_f16(d_blocks, d_scales, H, I, d);
+  for (size_t i = 0; i < H; i++) db[i] = orc_f32_to_f16_rne(d_bias[i]);
+}
+
 /* One selected expert on the cache-miss path: MXFP4 -> fp16 (session.rs:875-899), then
  * cpu_expert_ffn (session.rs:959-970). */
 static void *live_worker(void *arg) {
@@ -546,17 +558,75 @@ static void *live_worker(void *arg) {
   uint16_t *db = (uint16_t *)malloc(H * 2);
   float *gbuf = (float *)malloc(2 * I * 4);
   float *hbuf = (float *)malloc(I * 4);
-  orc_dequant_gate_up_reordered_f16(j->gub, j->gus, I, H, gu);
-  for (size_t i = 0; i < I; i++) {
-    gub[i] = orc_f32_to_f16_rne(j->gubias[2 * i]);
-    gub[I + i] = orc_f32_to_f16_rne(j->gubias[2 * i + 1]);
-  }
-  orc_dequant_down_f16(j->db, j->ds, H, I, d);
-  for (size_t i = 0; i < H; i++) db[i] = orc_f32_to_f16_rne(j->dbias[i]);
+  orc_live_expert_f16(j->gub, j->gus, j->gubias, j->db, j->ds, j->dbias, H, I, gu, gub, d, db);
   orc_cpu_expert_ffn_f16(j->x, gu, gub, d, db, j->out, gbuf, hbuf, H, I);
   free(gu); free(gub); free(d); free(db); free(gbuf); free(hbuf);
   return NULL;
 }
+
+typedef struct warm_job {
+  const float *x;
+  size_t H, I;
+  const uint16_t *gu, *gub, *d, *db;
+  float *out;
+} warm_job;
+
+/* One selected expert on the cache-hit path: cpu_expert_ffn on the cached fp16 entry
+ * (session.rs:959-970). */
+static void *warm_worker(void *arg) {
+  warm_job *j = (warm_job *)arg;
+  float *gbuf = (float *)malloc(2 * j->I * 4);
+  float *hbuf = (float *)malloc(j->I * 4);
+  orc_cpu_expert_ffn_f16(j->x, j->gu, j->gub, j->d, j->db, j->out, gbuf, hbuf, j->H, j->I);
+  free(gbuf); free(hbuf);
+  return NULL;
+}
+
+/* Runs n jobs of `size` bytes at `jobs` with `worker`, at most n_threads at a time (rayon's
+ * par_iter_mut over the k slots, session.rs:953-972). */
+static void run_slots(void *jobs, size_t size, size_t n, int n_threads, void *(*worker)(void *)) {
+  pthread_t *th = (pthread_t *)malloc(n * sizeof(pthread_t));
+  if (n_threads < 1) n_threads = 1;
+  for (size_t s0 = 0; s0 < n; s0 += (size_t)n_threads) {
+    size_t s1 = s0 + (size_t)n_threads < n ? s0 + (size_t)n_threads : n;
+    for (size_t s = s0; s < s1; s++) {
+      void *a = (char *)jobs + s * size;
+      if (pthread_create(&th[s], NULL, worker, a) != 0) worker(a), th[s] = 0;
+    }
+    for (size_t s = s0; s < s1; s++)
+      if (th[s]) pthread_join(th[s], NULL);
+  }
+  free(th);
+}
+
+/* session.rs:974-980: sequential weighted accumulation in slot order */
+static void live_combine(const float *outs, const float *w, size_t n, size_t H, float *y) {
+  for (size_t d = 0; d < H; d++) {
+    float acc = 0.0f;
+    for (size_t s = 0; s < n; s++) acc = acc + w[s] * outs[s * H + d];
+    y[d] = acc;
+  }
+}
+
+int orc_live_moe_token_warm(const float *x, size_t H, size_t I, size_t n, const float *w,
+                            const uint16_t *const *gu, const uint16_t *const *gub,
+                            const uint16_t *const *d, const uint16_t *const *db, int n_threads,
+                            float *y) {
+  float *outs = (float *)malloc((n ? n : 1) * H * sizeof(float));
+  warm_job *jobs = (warm_job *)malloc((n ? n : 1) * sizeof(warm_job));
+  for (size_t s = 0; s < n; s++) jobs[s] = (warm_job){x, H, I, gu[s], gub[s], d[s], db[s], outs + s * H};
+  run_slots(jobs, sizeof(warm_job), n, n_threads, warm_worker);
+  live_combine(outs, w, n, H, y);
+  free(outs); free(jobs);
+  return 0;
+}
+
+#ifdef _OPENMP
+#include <omp.h>
+int orc_omp_max_threads(void) { return omp_get_max_threads(); }
+#else
+int orc_omp_max_threads(void) { return 1; }
+#endif
 
 int orc_live_moe_token(const float *x, size_t H, size_t I, size_t k, const int32_t *idx,
                        const float *w, const uint8_t *gu_blocks, const uint8_t *gu_scales,
@@ -565,29 +635,16 @@ int orc_live_moe_token(const float *x, size_t H, size_t I, size_t k, const int32
   size_t nbh = H / 32, nbi = I / 32;
   size_t n = 0;
   while (n < k && idx[n] >= 0) n++;
-  float *outs = (float *)malloc(n * H * sizeof(float));
-  live_job *jobs = (live_job *)malloc(n * sizeof(live_job));
-  pthread_t *th = (pthread_t *)malloc(n * sizeof(pthread_t));
+  float *outs = (float *)malloc((n ? n : 1) * H * sizeof(float));
+  live_job *jobs = (live_job *)malloc((n ? n : 1) * sizeof(live_job));
   for (size_t s = 0; s < n; s++) {
     size_t e = (size_t)idx[s];
     jobs[s] = (live_job){x, H, I, gu_blocks + e * 2 * I * nbh * 16, gu_scales + e * 2 * I * nbh,
                          d_blocks + e * H * nbi * 16, d_scales + e * H * nbi, gu_bias + e * 2 * I,
                          d_bias + e * H, outs + s * H};
   }
-  if (n_threads < 1) n_threads = 1;
-  for (size_t s0 = 0; s0 < n; s0 += (size_t)n_threads) {
-    size_t s1 = s0 + (size_t)n_threads < n ? s0 + (size_t)n_threads : n;
-    for (size_t s = s0; s < s1; s++)
-      if (pthread_create(&th[s], NULL, live_worker, &jobs[s]) != 0) live_worker(&jobs[s]), th[s] = 0;
-    for (size_t s = s0; s < s1; s++)
-      if (th[s]) pthread_join(th[s], NULL);
-  }
-  /* session.rs:974-980: sequential weighted accumulation in slot order */
-  for (size_t d = 0; d < H; d++) {
-    float acc = 0.0f;
-    for (size_t s = 0; s < n; s++) acc = acc + w[s] * outs[s * H + d];
-    y[d] = acc;
-  }
-  free(outs); free(jobs); free(th);
+  run_slots(jobs, sizeof(live_job), n, n_threads, live_worker);
+  live_combine(outs, w, n, H, y);
+  free(outs); free(jobs);
   return 0;
 }

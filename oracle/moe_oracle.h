@@ -151,6 +151,21 @@ int orc_live_moe_token(const float *x, size_t H, size_t I, size_t k, const int32
                        const float *w, const uint8_t *gu_blocks, const uint8_t *gu_scales,
                        const float *gu_bias, const uint8_t *d_blocks, const uint8_t *d_scales,
                        const float *d_bias, int n_threads, float *y);
+/* The reference's fp16 expert-cache entry for one expert (session.rs:126-136, filled on a miss
+ * at :875-899): gate/up de-interleaved to [gate I; up I] x H fp16 (weights.rs:641-660), biases
+ * rounded f32 -> fp16 (weights.rs:686-702), down H x I fp16. */
+void orc_live_expert_f16(const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                         const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                         size_t H, size_t I, uint16_t *gu, uint16_t *gub, uint16_t *d, uint16_t *db);
+/* One token on the live path with every selected expert already in the fp16 cache (the hit
+ * path of session.rs:851-941): cpu_expert_ffn per slot on up to n_threads threads
+ * (session.rs:953-972) and the slot-order combine (:974-980). gu[s] ... db[s]: slot s's entry. */
+int orc_live_moe_token_warm(const float *x, size_t H, size_t I, size_t n, const float *w,
+                            const uint16_t *const *gu, const uint16_t *const *gub,
+                            const uint16_t *const *d, const uint16_t *const *db, int n_threads,
+                            float *y);
+/* OpenMP threads the oracle's parallel loops use (the fp32 path's matmuls). */
+int orc_omp_max_threads(void);
 
 #ifdef __cplusplus
 }

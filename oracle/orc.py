@@ -75,6 +75,13 @@ def lib():
     L.orc_live_moe_token.argtypes = [_f32p, _sz, _sz, _sz, _i32p, _f32p, _u8p, _u8p, _f32p, _u8p,
                                      _u8p, _f32p, ctypes.c_int, _f32p]
     L.orc_live_moe_token.restype = ctypes.c_int
+    L.orc_live_expert_f16.argtypes = [_u8p, _u8p, _f32p, _u8p, _u8p, _f32p, _sz, _sz, _u16p, _u16p,
+                                      _u16p, _u16p]
+    L.orc_live_moe_token_warm.argtypes = [_f32p, _sz, _sz, _sz, _f32p, ctypes.c_void_p,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_int, _f32p]
+    L.orc_live_moe_token_warm.restype = ctypes.c_int
+    L.orc_omp_max_threads.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -244,3 +251,36 @@ def live_moe_token(x, layer, idx, w, n_threads):
                                   _c(layer["d_bias"], np.float32).reshape(-1), n_threads, y)
     assert rc == 0
     return y
+
+
+def live_expert_f16(layer, e):
+    """The fp16 expert-cache entry of expert e (session.rs:875-899): (gu, gu_bias, down,
+    down_bias) as uint16 arrays, gate/up de-interleaved."""
+    H, I = layer["H"], layer["I"]
+    gu = np.empty(2 * I * H, np.uint16)
+    gub = np.empty(2 * I, np.uint16)
+    d = np.empty(H * I, np.uint16)
+    db = np.empty(H, np.uint16)
+    lib().orc_live_expert_f16(_c(layer["gu_blocks"][e], np.uint8).reshape(-1),
+                              _c(layer["gu_scales"][e], np.uint8).reshape(-1),
+                              _c(layer["gu_bias"][e], np.float32).reshape(-1),
+                              _c(layer["d_blocks"][e], np.uint8).reshape(-1),
+                              _c(layer["d_scales"][e], np.uint8).reshape(-1),
+                              _c(layer["d_bias"][e], np.float32).reshape(-1), H, I, gu, gub, d, db)
+    return gu, gub, d, db
+
+
+def live_moe_token_warm(x, H, I, entries, w, n_threads):
+    """One token on the live path with the selected experts' fp16 entries (from
+    live_expert_f16, in slot order) already cached."""
+    n = len(entries)
+    ptrs = [(ctypes.c_void_p * max(n, 1))(*[ent[i].ctypes.data for ent in entries]) for i in range(4)]
+    y = np.empty(H, np.float32)
+    rc = lib().orc_live_moe_token_warm(_c(x, np.float32).reshape(-1), H, I, n, _c(w, np.float32),
+                                       ptrs[0], ptrs[1], ptrs[2], ptrs[3], n_threads, y)
+    assert rc == 0
+    return y
+
+
+def omp_threads():
+    return int(lib().orc_omp_max_threads())

@@ -47,17 +47,16 @@ int fail(int code, const char *fmt, ...) {
 struct DevBuf {
   void *p = nullptr;
   size_t cap = 0;
+  // Grows the buffer. The new allocation is made before the old one is freed, so a failed
+  // call leaves the buffer (and every pointer carved from it) as it was.
   int ensure(size_t bytes) {
     if (bytes <= cap) return MOE_OK;
+    const size_t want = std::max(bytes, (size_t)4096);
+    void *q = nullptr;
+    hipError_t e = hipMalloc(&q, want);
+    if (e != hipSuccess) return fail(MOE_ERR_OOM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
     if (p) (void)hipFree(p);
-    p = nullptr;
-    cap = 0;
-    size_t want = std::max(bytes, (size_t)4096);
-    hipError_t e = hipMalloc(&p, want);
-    if (e != hipSuccess) {
-      p = nullptr;
-      return fail(MOE_ERR_OOM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
-    }
+    p = q;
     cap = want;
     return MOE_OK;
   }
@@ -194,6 +193,8 @@ int collect_timing(moe_ctx *c) {
 
 size_t al(size_t v) { return align_up(v, 256); }
 
+constexpr size_t kMaxTokens = (size_t)1 << 20;  // tokens per path-level call
+
 // Router chain length per lane, rounded up to whole 16-byte loads (8 bf16).
 size_t router_kip(size_t H) { return ((H + 63) / 64 + 7) / 8 * 8; }
 size_t router_bytes(size_t H, size_t E) { return E * 64 * router_kip(H) * 2; }
@@ -310,6 +311,16 @@ int check_layer(moe_ctx *c, size_t layer, bool need_router, long expert = -1) {
   return MOE_OK;
 }
 
+// Token count and top-k of a path-level call on a loaded layer (checked before any workspace
+// is sized for them).
+int check_tokens(moe_ctx *c, size_t layer, size_t T, size_t k) {
+  const size_t E = c->layers[layer].n_experts;
+  if (k < 1 || k > (size_t)kMaxTopK || k > E)
+    return fail(MOE_ERR_INVALID, "top_k %zu outside [1, min(%d, %zu)]", k, kMaxTopK, E);
+  if (T > kMaxTokens) return fail(MOE_ERR_INVALID, "n_tokens %zu above %zu", T, kMaxTokens);
+  return MOE_OK;
+}
+
 // Expert sizes in the checkpoint layout.
 struct ExpertBytes {
   size_t gub, gus, gubias, db, ds, dbias;
@@ -397,9 +408,7 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
                 Ly.router_experts, E);
   if (T == 0) return MOE_OK;
   if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
-  if (k < 1 || k > (size_t)kMaxTopK || k > E)
-    return fail(MOE_ERR_INVALID, "top_k %zu outside [1, min(%d, %zu)]", k, kMaxTopK, E);
-  if (T > (size_t)1 << 20) return fail(MOE_ERR_INVALID, "n_tokens %zu too large", T);
+  RETURN_IF(check_tokens(c, layer, T, k));
   RETURN_IF(ensure_work(c, T, k, E));
   if (norm && !Ly.has_norm) return fail(MOE_ERR_STATE, "layer %zu has no RMSNorm weight", layer);
   const float *resid = nullptr;  // x for the residual add of the unfused paths
@@ -613,8 +622,12 @@ void moe_destroy(moe_ctx *c) {
   for (auto &l : c->layers) {
     l.experts.release();
     l.router.release();
+    l.norm.release();
   }
   c->work.release();
+  c->layer_sync.release();
+  c->route_ticket.release();
+  c->layer_h.release();
   c->scratch_experts.release();
   c->stage.release();
   c->mv_split.release();
@@ -645,6 +658,10 @@ static int preload_common(moe_ctx *c, size_t layer, size_t n_experts) {
   if (c->layers.size() <= layer) c->layers.resize(layer + 1);
   Layer &Ly = c->layers[layer];
   if (Ly.n_experts != n_experts) {  // a new expert count discards the layer's experts
+    // the layer is empty until the new records exist (a failed allocation leaves it empty)
+    Ly.n_experts = 0;
+    Ly.loaded.clear();
+    Ly.n_loaded = 0;
     if (Ly.experts.cap < n_experts * c->L.stride) Ly.experts.release();
     RETURN_IF(Ly.experts.ensure(n_experts * c->L.stride));
     Ly.n_experts = n_experts;
@@ -819,6 +836,7 @@ int moe_dispatch_experts_batched(moe_ctx *c, const float *input, size_t n,
 int moe_init_lm_head(moe_ctx *c, const float *weights, size_t vocab) {
   RETURN_IF(use_dev(c));
   if (!weights || !vocab) return fail(MOE_ERR_INVALID, "null weights or zero vocab");
+  c->lm_vocab = 0;  // not initialised until the new weights are resident
   if (c->lm_w.cap < vocab * c->H * 4) c->lm_w.release();
   RETURN_IF(c->lm_w.ensure(vocab * c->H * 4));
   RETURN_IF(c->lm_x.ensure(c->H * 4));
@@ -858,8 +876,9 @@ int moe_router_topk(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k
   if (!x || !idx || !weights) return fail(MOE_ERR_INVALID, "null argument");
   RETURN_IF(check_layer(c, layer, true));
   const size_t E = c->layers[layer].router_experts;
-  if (k < 1 || k > (size_t)kMaxTopK || k > E) return fail(MOE_ERR_INVALID, "bad top_k %zu", k);
   if (T == 0) return MOE_OK;
+  RETURN_IF(check_tokens(c, layer, T, k));
+  if (k > E) return fail(MOE_ERR_INVALID, "top_k %zu above the router's %zu experts", k, E);
   RETURN_IF(ensure_work(c, T, k, E));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
   RouteArgs ra{};
@@ -895,6 +914,7 @@ int moe_layer_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
   if (T == 0) return MOE_OK;
   RETURN_IF(check_layer(c, layer, true));
+  RETURN_IF(check_tokens(c, layer, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
   RETURN_IF(forward_device(c, layer, c->w.x, T, k, c->w.y, c->stream));
@@ -914,6 +934,7 @@ int moe_block_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   if (!x || !out) return fail(MOE_ERR_INVALID, "null x or out");
   if (T == 0) return MOE_OK;
   RETURN_IF(check_layer(c, layer, true));
+  RETURN_IF(check_tokens(c, layer, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
   RETURN_IF(forward_device(c, layer, c->w.x, T, k, c->w.y, c->stream, true));

@@ -174,7 +174,9 @@ struct Json {
     } while (lit(','));
     return lit(']') || fail_at("unterminated array");
   }
-  bool tensor(TensorInfo &t, uint64_t data0) {
+  // data0: file offset of the data section; data_len: its length (file size - data0). Offsets are
+  // checked against data_len before data0 is added, so no sum can wrap.
+  bool tensor(TensorInfo &t, uint64_t data0, uint64_t data_len) {
     if (!lit('{')) return fail_at("expected a tensor entry");
     bool have_d = false, have_s = false, have_o = false;
     if (!lit('}')) {
@@ -191,6 +193,7 @@ struct Json {
           std::vector<uint64_t> o;
           if (!uint_array(o)) return false;
           if (o.size() != 2 || o[1] < o[0]) return fail_at("data_offsets must be [begin, end]");
+          if (o[1] > data_len) return fail_at("data_offsets run past the end of the file");
           t.begin = data0 + o[0];
           t.end = data0 + o[1];
           have_o = true;
@@ -233,10 +236,8 @@ int open_shard(const char *path, Shard &sh) {
         continue;
       }
       TensorInfo t;
-      if (!(ok = j.tensor(t, data0))) break;
-      if (t.end > sh.size) {
-        j.err = "tensor " + name + " runs past the end of the file";
-        ok = false;
+      if (!(ok = j.tensor(t, data0, sh.size - data0))) {
+        j.err = "tensor " + name + ": " + j.err;
         break;
       }
       sh.tensors[name] = t;

@@ -606,6 +606,77 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
         assert np.array_equal(outs[0], o), f"shape {shape} down {down}"
 
 
+def _prefill_parity(orc, d, layer, T, seed, n_sample):
+    """A T-token layer through the default path (the 8-token router blocks, the 512-row x
+    64-entry grouped GEMM at the real K): top-k indices of every token exact against the
+    oracle's router; n_sample tokens (per-token outputs do not depend on the other tokens)
+    within the tolerance of the oracle; the whole output within 2e-4 of the GEMV path; the
+    other large-batch block shape and the 4-wavefront shapes bit-identical."""
+    E, k = layer["E"], 4
+    x = syn.hidden(T, H20, seed=seed)
+    logits = orc.router_logits(layer["router_w"], layer["router_b"], x, E, H20)
+    widx, _, _, _ = orc.topk(logits, k)
+    gidx, _ = d.router_topk(0, x, k)
+    assert np.array_equal(gidx, widx)
+    counts = np.bincount(widx.ravel(), minlength=E)
+    assert counts.mean() >= 48, "the default shape needs experts averaging 48+ entries"
+    d.set_batch_gemm(1)
+    d.set_gemm_shape(0)
+    got = d.layer_forward(0, x, k)
+    sample = np.random.default_rng(seed + 1).choice(T, n_sample, replace=False)
+    sample.sort()
+    want, _, idx_s, _ = orc.moe_layer(x[sample], layer, k)
+    assert np.array_equal(idx_s, widx[sample])
+    assert_rel_l2(got[sample], want, f"T={T} E={E} sampled tokens vs oracle")
+    d.set_batch_gemm(0)
+    ref = d.layer_forward(0, x, k)
+    d.set_batch_gemm(1)
+    e = rel_l2(got, ref)
+    assert e < 2e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
+    for shape, down in [(1, 0), (2, 2), (3, 3), (0, 4)]:
+        d.set_gemm_shape(shape, down)
+        o = d.layer_forward(0, x, k)
+        assert np.array_equal(got, o), f"T={T} E={E} shape {shape} down {down}"
+    d.set_gemm_shape(0)
+
+
+def test_prefill_4096_tokens_20b(orc, disp20, layer20):
+    """Config 4's layer shape: 4096 tokens of a 20B layer (32 experts, 512 entries each on
+    average)."""
+    _prefill_parity(orc, disp20, layer20, 4096, seed=450, n_sample=64)
+
+
+def test_prefill_2048_tokens_120b(orc):
+    """Config 5b: 2048 tokens of a 120B layer (128 experts, 64 entries each on average)."""
+    L = syn.make_layer(H20, I20, 128, seed=460)
+    d = GpuMoeDispatcher(H20, I20, 7.0)
+    try:
+        d.preload_layer(0, L)
+        _prefill_parity(orc, d, L, 2048, seed=461, n_sample=32)
+    finally:
+        d.close()
+
+
+def test_invalid_calls_leave_context_usable(orc, disp20, layer20):
+    """Calls refused for their arguments (top-k 0 or above the expert count, a layer never
+    loaded) change nothing: the next valid call of each size still matches the oracle."""
+    from silentotithrandousha_amd._ffi import MoeError
+    for T in (1, 64):
+        x = syn.hidden(T, H20, seed=470 + T)
+        for bad_k in (0, 33, 1 << 40):
+            with pytest.raises(MoeError, match="top_k"):
+                disp20.layer_forward(0, x, bad_k)
+        for bad_k in (0, 33):
+            with pytest.raises(MoeError, match="top_k"):
+                disp20.router_topk(0, x, bad_k)
+        with pytest.raises(MoeError):
+            disp20.layer_forward(5, x, 4)
+        want, _, idx, _ = orc.moe_layer(x, layer20, 4)
+        gidx, _ = disp20.router_topk(0, x, 4)
+        assert np.array_equal(gidx, idx)
+        assert_rel_l2(disp20.layer_forward(0, x, 4), want, f"after refused calls T={T}")
+
+
 @pytest.mark.parametrize("H,E", [(64, 8), (64, 32), (512, 128)])
 def test_batch_grouping_in_router_and_separate(orc, H, E):
     """The router's last block groups the entries by expert when its x staging holds the

@@ -292,6 +292,62 @@ def test_combine_order_and_skip(orc):
     assert ys[1] == 1.0 and ys[2] == 2.0
 
 
+# ---------------------------------------------------------------- fp32 MXFP4 matvec (weights.rs:350-371 + session.rs:75-85)
+
+def _seq_dot_f32(w_row, x):
+    """acc = 0; acc = fl(acc + fl(w[k] x[k])) for k = 0, 1, ... in float32 (no fused multiply-add)."""
+    acc = np.float32(0.0)
+    for wk, xk in zip(w_row.astype(np.float32), x.astype(np.float32)):
+        acc = np.float32(acc + np.float32(wk * xk))
+    return acc
+
+
+def test_oracle_mxfp4_matvec_brute_force(orc):
+    """4 x 64: every output equals the float32 sequential, separately rounded dot of the numpy
+    decode (np_ref) with x, bit for bit."""
+    rng = np.random.default_rng(31)
+    blocks = rng.integers(0, 256, size=(4, 2, 16), dtype=np.uint8)
+    scales = rng.integers(118, 131, size=(4, 2), dtype=np.uint8)
+    x = rng.normal(0, 1, 64).astype(np.float32)
+    W = np_ref.decode(blocks, scales)
+    want = np.array([_seq_dot_f32(W[r], x) for r in range(4)], np.float32)
+    assert_bit_exact(orc.mxfp4_matvec(blocks, scales, 4, 64, x), want, "4x64 matvec")
+
+
+def test_oracle_mxfp4_matvec_sequential_order(orc):
+    """Weights 1.0 (nibble 2, scale 127) and x = [2^24, 1, -2^24, 0 ...]: the sequential
+    order rounds 2^24 + 1 to 2^24 (tie to even) and returns 0; float64, a pairwise tree or a
+    fused multiply-add chain that reorders the terms returns 1."""
+    blocks = np.full((1, 1, 16), 0x22, np.uint8)
+    scales = np.full((1, 1), 127, np.uint8)
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[2] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    assert orc.mxfp4_matvec(blocks, scales, 1, 32, x)[0] == 0.0
+    x[2], x[1] = 1.0, -(2.0 ** 24)   # 2^24 + (-2^24) + 1 = 1 exactly in this order
+    assert orc.mxfp4_matvec(blocks, scales, 1, 32, x)[0] == 1.0
+
+
+def test_oracle_mxfp4_matvec_float64_bound(orc):
+    """Config 1 (2880 x 2880, nibbles uniform, scales 118..130, x ~ N(0,1)): every row within
+    the sequential-summation bound |y - y64| <= gamma_n sum_k |w_k x_k|, gamma_n = n u / (1 - n u),
+    u = 2^-24, n = cols + 1 (one rounding per product and per sum), of the float64 product of the
+    numpy decode; and close on average (rel-L2 < 1e-6)."""
+    rows = cols = 2880
+    rng = np.random.default_rng(32)
+    blocks = rng.integers(0, 256, size=(rows, cols // 32, 16), dtype=np.uint8)
+    scales = rng.integers(118, 131, size=(rows, cols // 32), dtype=np.uint8)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    W = np_ref.decode(blocks, scales)
+    y64 = W @ x.astype(np.float64)
+    got = orc.mxfp4_matvec(blocks, scales, rows, cols, x).astype(np.float64)
+    u = 2.0 ** -24
+    n = cols + 1
+    gamma = n * u / (1 - n * u)
+    bound = gamma * (np.abs(W) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(got - y64) <= bound)
+    assert rel_l2(got, y64) < 1e-6
+
+
 # ---------------------------------------------------------------- live CPU path (session.rs:16-124)
 
 def test_matvec_f16xf32_neon_order(orc):
@@ -321,6 +377,20 @@ def test_live_path_close_to_fp32_path(orc):
     outs = np.stack([orc.expert_ffn(x, *syn.expert_slice(L, e), H, I)[0] for e in idx[0]])
     y_f32 = orc.combine(outs, w[0])
     assert rel_l2(y_live, y_f32) < 5e-3   # fp16 biases and the NEON sum order
+
+
+def test_live_warm_cache_equals_cold(orc):
+    """The cache-hit path (fp16 entries built once) gives the cache-miss path's bits: the two
+    differ only in when the MXFP4 -> fp16 decode runs."""
+    H, I, E = 256, 128, 4
+    L = syn.make_layer(H, I, E, seed=17, scale_lo=116, scale_hi=122)
+    x = syn.hidden(1, H, seed=18)[0]
+    idx = np.array([2, 0, 3], np.int32)
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    cold = orc.live_moe_token(x, L, idx, w, 3)
+    entries = [orc.live_expert_f16(L, int(e)) for e in idx]
+    assert_bit_exact(orc.live_moe_token_warm(x, H, I, entries, w, 3), cold, "warm vs cold")
+    assert_bit_exact(orc.live_moe_token_warm(x, H, I, entries, w, 1), cold, "warm 1 thread")
 
 
 # ---------------------------------------------------------------- RMSNorm (session.rs:483-493)

@@ -43,7 +43,7 @@ def test_find_package_writer(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["missing_file", "short", "header_past_end", "bad_json", "range_past_end",
-                                  "float_shape", "missing_tensor"])
+                                  "float_shape", "missing_tensor", "wrapping_offsets"])
 def test_malformed(tmp_path, case):
     p = tmp_path / "bad.safetensors"
     good = {"t": ("U8", np.zeros(16, np.uint8), (16,))}
@@ -59,6 +59,17 @@ def test_malformed(tmp_path, case):
     elif case == "range_past_end":
         h = b'{"t": {"dtype": "U8", "shape": [64], "data_offsets": [0, 64]}}'
         p.write_bytes(len(h).to_bytes(8, "little") + h + bytes(16))
+    elif case == "wrapping_offsets":
+        # end = data0 + o1 wraps to 16 (inside the file) while begin = data0 + o0 stays near
+        # 2^64: end - begin is the right byte count for a 32-byte tensor, so only an overflow
+        # check on the offsets themselves refuses it
+        tmpl = '{"t": {"dtype": "U8", "shape": [32], "data_offsets": [%d, %d]}}'
+        n = len(tmpl % (2**64 - 1, 2**64 - 1))  # both offsets have 20 digits
+        data0 = 8 + n
+        o1 = 2**64 - data0 + 16
+        h = (tmpl % (o1 - 32, o1)).encode()
+        assert len(h) == n
+        p.write_bytes(len(h).to_bytes(8, "little") + h + bytes(64))
     elif case == "float_shape":
         h = b'{"t": {"dtype": "U8", "shape": [1.5], "data_offsets": [0, 16]}}'
         p.write_bytes(len(h).to_bytes(8, "little") + h + bytes(16))
