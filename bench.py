@@ -248,7 +248,7 @@ def run_layer(model, workload, steps, warmup, graph=True, copy_mib=0, traffic_ki
     y.close()
 
     ms_per_step = elapsed * 1e3 / steps
-    tokens_per_s = T * lps * steps / elapsed
+    tokens_per_s = T * steps / elapsed  # a step takes T tokens through all lps layers
     active = expected_active(E, k, T)
     traffic = layer_traffic(H, I, E, T, active) * lps
     flops = layer_flops(H, I, E, k, T) * lps

@@ -610,8 +610,13 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
     """A T-token layer through the default path (the 8-token router blocks, the 512-row x
     64-entry grouped GEMM at the real K): top-k indices of every token exact against the
     oracle's router; n_sample tokens (per-token outputs do not depend on the other tokens)
-    within the tolerance of the oracle; the whole output within 2e-4 of the GEMV path; the
-    other large-batch block shape and the 4-wavefront shapes bit-identical."""
+    within the tolerance of the oracle; the whole output within 6e-4 of the GEMV path; the
+    other large-batch block shape and the 4-wavefront shapes bit-identical.
+    The GEMV path is exact to 2^-17 and the grouped GEMM's 3 E2M3 terms to ~2^-14 of each
+    block maximum; on this synthetic layer the gate/up pre-activations reach hundreds against
+    the SwiGLU clamp of 7, so the x split's error is amplified where gate or up sits in the
+    SwiGLU's sloped range: a float64 model of the split on 16 of these tokens gives 3.1e-4
+    relative L2 on the layer output (x split alone 3.1e-4, h split alone 7e-6)."""
     E, k = layer["E"], 4
     x = syn.hidden(T, H20, seed=seed)
     logits = orc.router_logits(layer["router_w"], layer["router_b"], x, E, H20)
@@ -632,7 +637,7 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
     ref = d.layer_forward(0, x, k)
     d.set_batch_gemm(1)
     e = rel_l2(got, ref)
-    assert e < 2e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
+    assert e < 6e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
     for shape, down in [(1, 0), (2, 2), (3, 3), (0, 4)]:
         d.set_gemm_shape(shape, down)
         o = d.layer_forward(0, x, k)
