@@ -239,6 +239,18 @@ int moe_layer_forward(moe_ctx *ctx, size_t layer, const float *x, size_t n_token
 int moe_layer_forward_device(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens,
                              size_t top_k, float *y, void *stream);
 
+/* The same forward without allocating: no reference counterpart. For callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid it): the
+ * per-call workspace comes from a fixed 16 MiB device array that the library holds on every GPU
+ * it runs on until the process ends, so neither this call nor its first call allocates (the
+ * context's other device memory is allocated by moe_create and the preload calls). Calls whose
+ * workspace would exceed 16 MiB (about 110 tokens at top-4 for hidden = intermediate = 2880)
+ * return MOE_ERR_INVALID; timing must be off (MOE_ERR_STATE otherwise). Every context on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two contexts, two threads)
+ * race and must be serialised by the caller. Results are identical to moe_layer_forward_device. */
+int moe_layer_forward_device_noalloc(moe_ctx *ctx, size_t layer, const float *x, size_t n_tokens,
+                                     size_t top_k, float *y, void *stream);
+
 /* The MoE block with the post-attention RMSNorm before it and the residual add after it: the
  * router fusion of build_decode_output_proj_router (executables.rs:260-317: router(RMSNorm(h)))
  * in the fp32 form of session.rs:483-493, and the residual add of session.rs:982-994:

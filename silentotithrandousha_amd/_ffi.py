@@ -82,6 +82,7 @@ SIGNATURES = {
     "moe_router_topk": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp]),
     "moe_layer_forward": (_int, [_vp, _sz, _vp, _sz, _sz, _vp]),
     "moe_layer_forward_device": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _vp]),
+    "moe_layer_forward_device_noalloc": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _vp]),
     "moe_mxfp4_dequant_device": (_int, [_vp, _vp, _sz, _sz, _vp, _vp]),
     "moe_dequant_expert_device": (_int, [_vp, _sz, _sz, _int, _vp, _vp]),
     "moe_mxfp4_packed_size": (_sz, [_sz, _sz]),

@@ -166,4 +166,10 @@ hipError_t launch_rmsnorm(const float *x, size_t T, size_t H, const float *gamma
                           hipStream_t s);
 hipError_t launch_add_rows(float *y, const float *x, size_t n, hipStream_t s);
 
+// Allocation-free forward (noalloc.hip): bytes of each device's scratch array, its device address
+// (resolved once per device, with that device current), and a kernel that zeroes device memory.
+size_t noalloc_scratch_bytes();
+hipError_t noalloc_scratch_ptr(int dev, void **ptr);
+hipError_t launch_zero(void *p, size_t bytes, hipStream_t s);
+
 }  // namespace moe

@@ -85,6 +85,7 @@ struct Work {
   uint16_t *xsplit, *hsplit;
   uint8_t *xrec, *hrec;  // grouped GEMM activation records: tokens, entries (padding zero)
   int32_t *idx, *n_active, *active_ids, *active_off, *entry_src, *pos;
+  size_t hrec_bytes;     // bytes of hrec, which must hold zeros where no kernel writes
 };
 
 enum {
@@ -133,6 +134,7 @@ struct moe_ctx {
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
   int n_cu = 256;     // compute units of the device (the one-launch grid is sized to it)
   uint32_t spin_limit = 1u << 20;
+  void *scratch = nullptr;  // this device's scratch array (moe_layer_forward_device_noalloc)
   std::vector<TimingRec> recs;
   std::vector<hipEvent_t> pool;
   double acc_ms[K_COUNT] = {};
@@ -199,6 +201,37 @@ constexpr size_t kMaxTokens = (size_t)1 << 20;  // tokens per path-level call
 size_t router_kip(size_t H) { return ((H + 63) / 64 + 7) / 8 * 8; }
 size_t router_bytes(size_t H, size_t E) { return E * 64 * router_kip(H) * 2; }
 
+// Lays out the per-call workspace of T tokens, top-k k and E experts at `b` (nullptr: sizes
+// only) and returns its bytes. host_io adds the staging rows of host-pointer calls (x, y) and
+// the normalised rows of the unfused block forward (xn).
+size_t carve_work(Work &w, char *b, size_t T, size_t k, size_t E, size_t H, size_t I, bool host_io) {
+  const size_t N = T * k;
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char * {
+    const size_t o = off;
+    off = al(off + bytes);
+    return b && bytes ? b + o : nullptr;
+  };
+  w.x = (float *)take(host_io ? T * H * 4 : 0);
+  w.y = (float *)take(host_io ? T * H * 4 : 0);
+  w.xn = (float *)take(host_io ? T * H * 4 : 0);
+  w.logits = (float *)take(T * E * 4);
+  w.wts = (float *)take(N * 4);
+  w.o = (float *)take(N * H * 4);
+  w.xsplit = (uint16_t *)take(T * 2 * H * 2);
+  w.hsplit = (uint16_t *)take(N * 2 * I * 2);
+  w.idx = (int32_t *)take(N * 4);
+  w.n_active = (int32_t *)take(4);
+  w.active_ids = (int32_t *)take(E * 4);
+  w.active_off = (int32_t *)take((E + 1) * 4);
+  w.entry_src = (int32_t *)take(N * 4);
+  w.pos = (int32_t *)take(N * 4);
+  w.xrec = (uint8_t *)take(T * GemmRec::kBytes);
+  w.hrec_bytes = N * GemmRec::kBytes;
+  w.hrec = (uint8_t *)take(w.hrec_bytes);
+  return off;
+}
+
 int ensure_work(moe_ctx *c, size_t T, size_t k, size_t E) {
   if (T <= c->work_T && k <= c->work_k && E <= c->work_E) return MOE_OK;
   if (c->capturing)
@@ -206,77 +239,46 @@ int ensure_work(moe_ctx *c, size_t T, size_t k, size_t E) {
   T = std::max(T, c->work_T);
   k = std::max(k, c->work_k);
   E = std::max({E, c->work_E, (size_t)kMaxExperts});
-  const size_t H = c->H, I = c->I, N = T * k;
-  size_t off = 0;
-  size_t o_x = off; off = al(off + T * H * 4);
-  size_t o_y = off; off = al(off + T * H * 4);
-  size_t o_xn = off; off = al(off + T * H * 4);
-  size_t o_lg = off; off = al(off + T * E * 4);
-  size_t o_wt = off; off = al(off + N * 4);
-  size_t o_o = off; off = al(off + N * H * 4);
-  size_t o_xs = off; off = al(off + T * 2 * H * 2);
-  size_t o_hs = off; off = al(off + N * 2 * I * 2);
-  size_t o_idx = off; off = al(off + N * 4);
-  size_t o_na = off; off = al(off + 4);
-  size_t o_ai = off; off = al(off + E * 4);
-  size_t o_ao = off; off = al(off + (E + 1) * 4);
-  size_t o_es = off; off = al(off + N * 4);
-  size_t o_pos = off; off = al(off + N * 4);
-  size_t o_xr = off; off = al(off + T * GemmRec::kBytes);
-  size_t o_hr = off; off = al(off + N * GemmRec::kBytes);
-  RETURN_IF(c->work.ensure(off));
-  char *b = (char *)c->work.p;
+  Work w{};
+  RETURN_IF(c->work.ensure(carve_work(w, nullptr, T, k, E, c->H, c->I, true)));
+  carve_work(w, (char *)c->work.p, T, k, E, c->H, c->I, true);
   // h records are written block by block; their padding past I must read as zeros
-  HIP_TRY(hipMemset(b + o_hr, 0, N * GemmRec::kBytes));
-  c->w.xrec = (uint8_t *)(b + o_xr);
-  c->w.hrec = (uint8_t *)(b + o_hr);
-  c->w.x = (float *)(b + o_x);
-  c->w.y = (float *)(b + o_y);
-  c->w.xn = (float *)(b + o_xn);
-  c->w.logits = (float *)(b + o_lg);
-  c->w.wts = (float *)(b + o_wt);
-  c->w.o = (float *)(b + o_o);
-  c->w.xsplit = (uint16_t *)(b + o_xs);
-  c->w.hsplit = (uint16_t *)(b + o_hs);
-  c->w.idx = (int32_t *)(b + o_idx);
-  c->w.n_active = (int32_t *)(b + o_na);
-  c->w.active_ids = (int32_t *)(b + o_ai);
-  c->w.active_off = (int32_t *)(b + o_ao);
-  c->w.entry_src = (int32_t *)(b + o_es);
-  c->w.pos = (int32_t *)(b + o_pos);
+  HIP_TRY(hipMemset(w.hrec, 0, w.hrec_bytes));
+  c->w = w;
   c->work_T = T;
   c->work_k = k;
   c->work_E = E;
   return MOE_OK;
 }
 
-GemvArgs gemv_args(moe_ctx *c, const uint8_t *base, bool gate_up) {
+GemvArgs gemv_args(moe_ctx *c, const Work &w, const uint8_t *base, bool gate_up) {
   GemvArgs a{};
   a.base = base;
   a.stride = c->L.stride;
   a.mat_off = gate_up ? c->L.gu_off : c->L.dn_off;
   a.bias_off = gate_up ? c->L.gub_off : c->L.dnb_off;
   a.d = gate_up ? c->L.gu : c->L.dn;
-  a.n_active = c->w.n_active;
-  a.active_ids = c->w.active_ids;
-  a.active_off = c->w.active_off;
+  a.n_active = w.n_active;
+  a.active_ids = w.active_ids;
+  a.active_off = w.active_off;
   a.limit = c->clamp;
   return a;
 }
 
 // gate_up -> down for the expert list already in the workspace; outputs in w.o[entry].
-int run_experts(moe_ctx *c, const uint8_t *base, int max_active, int max_entries, hipStream_t s) {
-  GemvArgs gu = gemv_args(c, base, true);
-  gu.entry_src = c->w.entry_src;
-  gu.bsrc = c->w.xsplit;
-  gu.out = c->w.hsplit;
+int run_experts(moe_ctx *c, const Work &w, const uint8_t *base, int max_active, int max_entries,
+                hipStream_t s) {
+  GemvArgs gu = gemv_args(c, w, base, true);
+  gu.entry_src = w.entry_src;
+  gu.bsrc = w.xsplit;
+  gu.out = w.hsplit;
   gu.max_active = max_active;
   gu.max_entries_per_expert = max_entries;
   RETURN_IF(timed(c, K_GATE_UP, s, [&] { return launch_gemv(GEMV_GATE_UP, gu, s); }));
-  GemvArgs dn = gemv_args(c, base, false);
+  GemvArgs dn = gemv_args(c, w, base, false);
   dn.entry_src = nullptr;
-  dn.bsrc = c->w.hsplit;
-  dn.out = c->w.o;
+  dn.bsrc = w.hsplit;
+  dn.out = w.o;
   dn.max_active = max_active;
   dn.max_entries_per_expert = max_entries;
   RETURN_IF(timed(c, K_DOWN, s, [&] { return launch_gemv(GEMV_DOWN, dn, s); }));
@@ -398,8 +400,10 @@ int set_single_token_list(moe_ctx *c, size_t n, const int32_t *ids) {
 
 // norm: the block forward (RMSNorm of x before, x + result after); the one-launch decode fuses
 // both, the other paths run k_rmsnorm into the workspace first and k_add_rows last.
-int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k, float *y,
-                   hipStream_t s, bool norm = false) {
+// w: the workspace, sized for (T, k, E) by the caller (ensure_work, or the scratch array of the
+// allocation-free entry point).
+int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size_t T, size_t k,
+                   float *y, hipStream_t s, bool norm = false) {
   RETURN_IF(check_layer(c, layer, true));
   Layer &Ly = c->layers[layer];
   const size_t E = Ly.n_experts;
@@ -409,17 +413,16 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
   if (T == 0) return MOE_OK;
   if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
   RETURN_IF(check_tokens(c, layer, T, k));
-  RETURN_IF(ensure_work(c, T, k, E));
   if (norm && !Ly.has_norm) return fail(MOE_ERR_STATE, "layer %zu has no RMSNorm weight", layer);
   const float *resid = nullptr;  // x for the residual add of the unfused paths
   if (norm) {
     const bool fused = T == 1 && c->decode_mode == 2;
     if (!fused || (reinterpret_cast<uintptr_t>(x) & 15)) {
       RETURN_IF(timed(c, K_NORM, s, [&] {
-        return launch_rmsnorm(x, T, c->H, (const float *)Ly.norm.p, Ly.eps, c->w.xn, s);
+        return launch_rmsnorm(x, T, c->H, (const float *)Ly.norm.p, Ly.eps, w.xn, s);
       }));
       resid = x;
-      x = c->w.xn;
+      x = w.xn;
       norm = false;
     }
   }
@@ -449,10 +452,10 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     da.top2_mass = c->ad_top2;
     da.x = x;
     da.y = y;
-    da.logits = c->w.logits;
-    da.idx = c->w.idx;
-    da.wts = c->w.wts;
-    da.hsplit = c->w.hsplit;
+    da.logits = w.logits;
+    da.idx = w.idx;
+    da.wts = w.wts;
+    da.hsplit = w.hsplit;
     da.n_gu_wg_per_slot = (int)((c->L.gu.tiles + 3) / 4);
     LayerArgs la{};
     la.d = da;
@@ -468,10 +471,10 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
       return timed(c, K_DECODE_LAYER, s, [&] { return launch_decode_layer(la, s); });
     if (norm) {  // the fused kernel refused the shape: normalise first, add the residual last
       RETURN_IF(timed(c, K_NORM, s, [&] {
-        return launch_rmsnorm(x, T, c->H, (const float *)Ly.norm.p, Ly.eps, c->w.xn, s);
+        return launch_rmsnorm(x, T, c->H, (const float *)Ly.norm.p, Ly.eps, w.xn, s);
       }));
       resid = x;
-      x = c->w.xn;
+      x = w.xn;
       da.x = x;
     }
     if (decode_supported(da)) {
@@ -494,30 +497,30 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
   ra.top1_min = c->ad_top1;
   ra.margin_min = c->ad_margin;
   ra.top2_mass = c->ad_top2;
-  ra.logits = c->w.logits;
-  ra.idx = c->w.idx;
-  ra.wts = c->w.wts;
+  ra.logits = w.logits;
+  ra.idx = w.idx;
+  ra.wts = w.wts;
   // the grouped GEMM (16- to 64-entry column tiles) pays off once experts average a few
   // entries; smaller batches stream each weight tile through the GEMV kernels, which read the
   // bf16 hi + lo split of x that the router writes
   const bool use_gemm = c->batch_gemm && T > 1 && (c->batch_gemm == 2 || T * k >= 4 * E) &&
                         c->L.gu.ns <= (uint32_t)kGemmNs && c->L.dn.ns <= (uint32_t)kGemmNs &&
                         (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-  ra.xsplit = use_gemm ? nullptr : c->w.xsplit;
-  ra.xrec = use_gemm ? c->w.xrec : nullptr;  // the router writes the GEMM's activation records
+  ra.xsplit = use_gemm ? nullptr : w.xsplit;
+  ra.xrec = use_gemm ? w.xrec : nullptr;  // the router writes the GEMM's activation records
   ra.fuse_bucket = T == 1;
-  ra.n_active = c->w.n_active;
-  ra.active_ids = c->w.active_ids;
-  ra.active_off = c->w.active_off;
-  ra.entry_src = c->w.entry_src;
-  ra.pos = c->w.pos;
+  ra.n_active = w.n_active;
+  ra.active_ids = w.active_ids;
+  ra.active_off = w.active_off;
+  ra.entry_src = w.entry_src;
+  ra.pos = w.pos;
   const bool fuse_bucket = T > 1 && route_bucket_fits((int)c->H, (int)E);
   ra.bucket_ticket = fuse_bucket ? (uint32_t *)c->route_ticket.p : nullptr;
   RETURN_IF(timed(c, K_ROUTE, s, [&] { return launch_route(ra, s); }));
   if (T > 1 && !fuse_bucket)
     RETURN_IF(timed(c, K_BUCKET, s, [&] {
-      return launch_bucket(c->w.idx, (int)T, (int)k, (int)E, c->w.n_active, c->w.active_ids,
-                           c->w.active_off, c->w.entry_src, c->w.pos, s);
+      return launch_bucket(w.idx, (int)T, (int)k, (int)E, w.n_active, w.active_ids,
+                           w.active_off, w.entry_src, w.pos, s);
     }));
   const int max_active = (int)std::min(E, T * k);
   if (use_gemm) {
@@ -525,9 +528,9 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     GemmArgs ga{};
     ga.base = (const uint8_t *)Ly.experts.p;
     ga.stride = c->L.stride;
-    ga.n_active = c->w.n_active;
-    ga.active_ids = c->w.active_ids;
-    ga.active_off = c->w.active_off;
+    ga.n_active = w.n_active;
+    ga.active_ids = w.active_ids;
+    ga.active_off = w.active_off;
     ga.limit = c->clamp;
     ga.max_active = max_active;
     ga.n_entries = N;
@@ -537,9 +540,9 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     gu.mat_off = c->L.gu_off;
     gu.bias_off = c->L.gub_off;
     gu.d = c->L.gu;
-    gu.entry_src = c->w.entry_src;
-    gu.brec = c->w.xrec;
-    gu.out = c->w.hrec;
+    gu.entry_src = w.entry_src;
+    gu.brec = w.xrec;
+    gu.out = w.hrec;
     RETURN_IF(timed(c, K_GATE_UP, s, [&] { return launch_gemm_fp8(GEMV_GATE_UP, gu, s); }));
     GemmArgs dn = ga;
     if (!c->gemm_band) dn.band = 1;
@@ -548,14 +551,14 @@ int forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
     dn.bias_off = c->L.dnb_off;
     dn.d = c->L.dn;
     dn.entry_src = nullptr;
-    dn.brec = c->w.hrec;
-    dn.out = c->w.o;
+    dn.brec = w.hrec;
+    dn.out = w.o;
     RETURN_IF(timed(c, K_DOWN, s, [&] { return launch_gemm_fp8(GEMV_DOWN, dn, s); }));
   } else {
-    RETURN_IF(run_experts(c, (const uint8_t *)Ly.experts.p, max_active, (int)std::min(T, (size_t)1 << 30), s));
+    RETURN_IF(run_experts(c, w, (const uint8_t *)Ly.experts.p, max_active, (int)std::min(T, (size_t)1 << 30), s));
   }
   RETURN_IF(timed(c, K_COMBINE, s, [&] {
-    return launch_combine(c->w.o, c->w.pos, c->w.wts, (int)T, (int)k, (int)c->H, 0, y, s);
+    return launch_combine(w.o, w.pos, w.wts, (int)T, (int)k, (int)c->H, 0, y, s);
   }));
   if (resid) RETURN_IF(timed(c, K_NORM, s, [&] { return launch_add_rows(y, resid, T * c->H, s); }));
   return MOE_OK;
@@ -598,6 +601,13 @@ int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ct
   if (e != hipSuccess) {
     delete c;
     return fail(MOE_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  // this device's copy of the allocation-free forward's scratch array (resolved once per device)
+  e = noalloc_scratch_ptr(dev, &c->scratch);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return fail(MOE_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
   }
   const size_t sb = layer_sync_bytes(), hb = layer_hterm_bytes();
   if (c->layer_sync.ensure(sb) != MOE_OK || hipMemset(c->layer_sync.p, 0, sb) != hipSuccess ||
@@ -775,7 +785,7 @@ int moe_dispatch_expert_preloaded(moe_ctx *c, const float *input, size_t layer, 
   HIP_TRY(launch_split(c->w.x, 1, c->H, c->w.xsplit, c->stream));
   const int32_t id = (int32_t)expert;
   RETURN_IF(set_single_token_list(c, 1, &id));
-  RETURN_IF(run_experts(c, (const uint8_t *)c->layers[layer].experts.p, 1, 1, c->stream));
+  RETURN_IF(run_experts(c, c->w, (const uint8_t *)c->layers[layer].experts.p, 1, 1, c->stream));
   HIP_TRY(hipMemcpyAsync(output, c->w.o, c->H * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return MOE_OK;
@@ -794,7 +804,7 @@ int moe_dispatch_expert(moe_ctx *c, const float *input, const uint8_t *gub, size
   HIP_TRY(hipMemcpyAsync(c->w.x, input, c->H * 4, hipMemcpyHostToDevice, c->stream));
   HIP_TRY(launch_split(c->w.x, 1, c->H, c->w.xsplit, c->stream));
   RETURN_IF(set_single_token_list(c, 1, nullptr));
-  RETURN_IF(run_experts(c, (const uint8_t *)c->scratch_experts.p, 1, 1, c->stream));
+  RETURN_IF(run_experts(c, c->w, (const uint8_t *)c->scratch_experts.p, 1, 1, c->stream));
   HIP_TRY(hipMemcpyAsync(output, c->w.o, c->H * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return MOE_OK;
@@ -826,7 +836,7 @@ int moe_dispatch_experts_batched(moe_ctx *c, const float *input, size_t n,
   std::vector<float> wts(n);
   for (size_t i = 0; i < n; i++) wts[i] = ex[i].weight;
   HIP_TRY(hipMemcpyAsync(c->w.wts, wts.data(), n * 4, hipMemcpyHostToDevice, c->stream));
-  RETURN_IF(run_experts(c, base, (int)n, 1, c->stream));
+  RETURN_IF(run_experts(c, c->w, base, (int)n, 1, c->stream));
   HIP_TRY(launch_combine(c->w.o, c->w.pos, c->w.wts, 1, (int)n, (int)c->H, 1, c->w.y, c->stream));
   HIP_TRY(hipMemcpyAsync(output, c->w.y, c->H * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
@@ -917,7 +927,7 @@ int moe_layer_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   RETURN_IF(check_tokens(c, layer, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
-  RETURN_IF(forward_device(c, layer, c->w.x, T, k, c->w.y, c->stream));
+  RETURN_IF(forward_device(c, c->w, layer, c->w.x, T, k, c->w.y, c->stream));
   HIP_TRY(hipMemcpyAsync(y, c->w.y, T * c->H * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return check_layer_sync(c);
@@ -926,7 +936,36 @@ int moe_layer_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
 int moe_layer_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
                              float *y, void *stream) {
   RETURN_IF(use_dev(c));
-  return forward_device(c, layer, x, T, k, y, pick(c, stream));
+  RETURN_IF(check_layer(c, layer, true));
+  if (T == 0) return MOE_OK;
+  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
+  return forward_device(c, c->w, layer, x, T, k, y, pick(c, stream));
+}
+
+int moe_layer_forward_device_noalloc(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k,
+                                     float *y, void *stream) {
+  RETURN_IF(use_dev(c));
+  if (c->timing)
+    return fail(MOE_ERR_STATE, "the allocation-free forward runs with timing off (timing creates events)");
+  RETURN_IF(check_layer(c, layer, true));
+  if (T == 0) return MOE_OK;
+  if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
+  RETURN_IF(check_tokens(c, layer, T, k));
+  if (!c->scratch) return fail(MOE_ERR_STATE, "no scratch array address for device %d", c->dev);
+  const size_t E = c->layers[layer].n_experts;
+  Work w{};
+  const size_t need = carve_work(w, nullptr, T, k, E, c->H, c->I, false);
+  if (need > noalloc_scratch_bytes())
+    return fail(MOE_ERR_INVALID,
+                "%zu tokens at top-%zu over %zu experts need %zu bytes of workspace; the allocation-free "
+                "forward's scratch holds %zu (use moe_layer_forward_device)",
+                T, k, E, need, noalloc_scratch_bytes());
+  carve_work(w, (char *)c->scratch, T, k, E, c->H, c->I, false);
+  const hipStream_t s = pick(c, stream);
+  // the array keeps the previous call's contents: the h records' padding must read as zeros
+  HIP_TRY(launch_zero(w.hrec, w.hrec_bytes, s));
+  return forward_device(c, w, layer, x, T, k, y, s);
 }
 
 int moe_block_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k, float *out) {
@@ -937,7 +976,7 @@ int moe_block_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   RETURN_IF(check_tokens(c, layer, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
-  RETURN_IF(forward_device(c, layer, c->w.x, T, k, c->w.y, c->stream, true));
+  RETURN_IF(forward_device(c, c->w, layer, c->w.x, T, k, c->w.y, c->stream, true));
   HIP_TRY(hipMemcpyAsync(out, c->w.y, T * c->H * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return check_layer_sync(c);
@@ -947,7 +986,11 @@ int moe_block_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T,
                              float *out, void *stream) {
   RETURN_IF(use_dev(c));
   if (x == out) return fail(MOE_ERR_INVALID, "out must not alias x");
-  return forward_device(c, layer, x, T, k, out, pick(c, stream), true);
+  RETURN_IF(check_layer(c, layer, true));
+  if (T == 0) return MOE_OK;
+  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
+  return forward_device(c, c->w, layer, x, T, k, out, pick(c, stream), true);
 }
 
 int moe_preload_norm(moe_ctx *c, size_t layer, const float *gamma, float eps) {
