@@ -51,6 +51,17 @@ __device__ __forceinline__ void lds_dma4(const void *g, const void *lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
+// The same with a wavefront-uniform 64-bit base in SGPRs and a 32-bit per-lane offset
+// (global address = sbase + voff): one VGPR per lane instead of a 64-bit pointer.
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void *sbase, const void *lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(la) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4_s(uint32_t voff, const void *sbase, const void *lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(la) : "memory", "m0");
+}
+
 // Block shape: WR x WC wavefronts; wavefront (wr, wc) owns RT tiles of 16 weight rows (row
 // group wr) x CGW column groups of 16 entries (entry group wc). Every operand goes through LDS by
 // LDS-DMA (global_load_lds) into a ring of D K-steps: per step, the B records of the block's
@@ -68,7 +79,10 @@ struct GemmShape {
   static constexpr int kTilesA = WR * RT;                    // A tiles of the block
   static constexpr int kDmaA = kTilesA / W;                  // A tiles (and scale words) per wavefront
   static_assert(kTilesA % W == 0, "A tiles shared evenly");
-  static constexpr int kBufB = kDma * W * 1024;              // one step of B (+ the pieces past kGroups)
+  // one wavefront per SIMD with 16+ row tiles (B-stationary steps): B holds exactly kGroups pieces
+  // and the pieces past them land in a dummy area; otherwise the slot also holds those pieces
+  static constexpr bool kBStat = RT >= 16;
+  static constexpr int kBufB = (kBStat ? kGroups : kDma * W) * 1024;
   static constexpr int kBufA = kTilesA * 1024;               // A chunks of one step
   static constexpr int kBufS = kTilesA * 256;                // A-scale words of one step
   static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
@@ -82,6 +96,25 @@ struct GemmB {
   i32x8 v[kGemmTerms];
   uint32_t sc[kGemmTerms];
 };
+
+// The same as one 16-byte and one 8-byte LDS read per term: the 24 bytes of lane group g start at
+// 24 g, so even groups read 16 + 8 and odd groups 8 + 16 bytes, the 16-byte part 16-byte aligned.
+// Eight lanes of one group read 16-byte parts 304 bytes apart (19 j mod 8 distinct), so the
+// 16-byte reads are free of bank conflicts.
+__device__ __forceinline__ void gemm_read_b_t(GemmB &b, const uint8_t *eb, int g, int t) {
+  const uint8_t *q = eb + t * G::kTermBytes + 24 * g;
+  uint32_t d[6];
+  if ((g & 1) == 0) {
+    const uint4 x = *reinterpret_cast<const uint4 *>(q);
+    const uint2 y = *reinterpret_cast<const uint2 *>(q + 16);
+    d[0] = x.x; d[1] = x.y; d[2] = x.z; d[3] = x.w; d[4] = y.x; d[5] = y.y;
+  } else {
+    const uint2 y = *reinterpret_cast<const uint2 *>(q);
+    const uint4 x = *reinterpret_cast<const uint4 *>(q + 8);
+    d[0] = y.x; d[1] = y.y; d[2] = x.x; d[3] = x.y; d[4] = x.z; d[5] = x.w;
+  }
+  b.v[t] = i32x8{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], 0, 0};
+}
 
 __device__ __forceinline__ void gemm_read_b(GemmB &b, const uint8_t *eb, int g) {
 #pragma unroll
@@ -133,6 +166,76 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *
   }
 }
 
+// MFMAs of one K-step for a wavefront with many row tiles (one wavefront per SIMD): the B
+// operands of all CG column groups are read once and held for the step; row tiles go in pairs,
+// the A chunks of the next pair read while the MFMAs of this pair run (8 independent
+// accumulators between two MFMAs into the same one). Per output the terms still accumulate in
+// order t = 0, 1, 2 (the order of gemm_step, so every shape gives the same bits). FULL: every
+// row tile of the wavefront is inside the matrix (no test in the loop); otherwise row pairs from
+// nrt_valid on issue no MFMAs (a pair straddling the end computes its second tile on a clamped
+// tile, not stored).
+template <int RT, int CGW, int WR, int WC, int D, bool FULL>
+__device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uint8_t *slot, int wr, int wc,
+                                                int lane, int sh, int nrt_valid) {
+  using S = GemmShape<RT, CGW, WR, WC, D>;
+  static_assert(RT % 2 == 0, "row tiles in pairs");
+  constexpr int CG = CGW;
+  const int j = lane & 15, g = lane >> 4;
+  const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024,
+                *sb = slot + S::kBufB + S::kBufA + wr * RT * 256;
+  // the first pair's A, then B term by term: the first MFMAs (term 0 of every column group) can
+  // start before the other terms have arrived
+  uint4 a0 = *reinterpret_cast<const uint4 *>(ab + 16 * lane);
+  uint4 a1 = *reinterpret_cast<const uint4 *>(ab + 1024 + 16 * lane);
+  uint32_t s0 = *reinterpret_cast<const uint32_t *>(sb + 4 * lane) >> sh;
+  uint32_t s1 = *reinterpret_cast<const uint32_t *>(sb + 256 + 4 * lane) >> sh;
+  GemmB b[CG];
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+#pragma unroll
+    for (int c = 0; c < CG; c++) gemm_read_b_t(b[c], bb + 16 * c * kEntryStep, g, t);
+  }
+#pragma unroll
+  for (int c = 0; c < CG; c++) {
+    const uint4 sc = *reinterpret_cast<const uint4 *>(bb + 16 * c * kEntryStep + kGemmTerms * G::kTermBytes);
+    b[c].sc[0] = sc.x >> (8 * g);
+    b[c].sc[1] = sc.y >> (8 * g);
+    b[c].sc[2] = sc.z >> (8 * g);
+  }
+#pragma unroll
+  for (int r = 0; r < RT; r += 2) {
+    uint4 n0 = a0, n1 = a1;
+    uint32_t t0s = s0, t1s = s1;
+    if (r + 2 < RT) {
+      n0 = *reinterpret_cast<const uint4 *>(ab + (r + 2) * 1024 + 16 * lane);
+      n1 = *reinterpret_cast<const uint4 *>(ab + (r + 3) * 1024 + 16 * lane);
+      t0s = *reinterpret_cast<const uint32_t *>(sb + (r + 2) * 256 + 4 * lane) >> sh;
+      t1s = *reinterpret_cast<const uint32_t *>(sb + (r + 3) * 256 + 4 * lane) >> sh;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the next pair's A reads issue before this pair's MFMAs
+    if (FULL || r < nrt_valid) {
+      const i32x8 A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, 0, 0, 0, 0};
+      const i32x8 A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w, 0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < kGemmTerms; t++) {
+#pragma unroll
+        for (int c = 0; c < CG; c++) {
+          // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
+          acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A0, b[c].v[t], acc[r][c], 4, 2, 0, (int)s0, 0,
+                                                                       (int)b[c].sc[t]);
+          acc[r + 1][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A1, b[c].v[t], acc[r + 1][c], 4, 2, 0,
+                                                                           (int)s1, 0, (int)b[c].sc[t]);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    a0 = n0;
+    a1 = n1;
+    s0 = t0s;
+    s1 = t1s;
+  }
+}
+
 template <int MODE, int RT, int CGW, int WR, int WC, int D>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
   using S = GemmShape<RT, CGW, WR, WC, D>;
@@ -143,7 +246,10 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   __shared__ __attribute__((aligned(1024))) uint8_t s_r1[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
   constexpr int kBiasTiles = RT < 4 ? 4 : RT;  // the bias DMA moves 64 rows (4 tiles) per wavefront load
-  __shared__ __attribute__((aligned(16))) float s_bias[W * kBiasTiles * 16];  // per wavefront: its rows' bias
+  // per wavefront: its rows' bias (the B-stationary shape reads its bias from global memory in the
+  // epilogue, and its B pieces past the step's kGroups land in s_dummy)
+  __shared__ __attribute__((aligned(16))) float s_bias[S::kBStat ? 4 : W * kBiasTiles * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_dummy[S::kBStat && S::kDma * W > S::kGroups ? 1024 : 16];
   __shared__ int s_tile[4];  // expert record index, first entry, entry count, row block
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wr = wv % WR, wc = wv / WR;
@@ -213,9 +319,11 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     }
   }
   __syncthreads();
-  const int ex = s_tile[0], beg = s_tile[1], ncol = s_tile[2];
+  // block-uniform (read from LDS, so made scalar explicitly: the bounds below then branch on SGPRs)
+  const int ex = __builtin_amdgcn_readfirstlane(s_tile[0]), beg = __builtin_amdgcn_readfirstlane(s_tile[1]),
+            ncol = __builtin_amdgcn_readfirstlane(s_tile[2]);
   if (ex < 0) return;
-  const int rblk = s_tile[3];
+  const int rblk = __builtin_amdgcn_readfirstlane(s_tile[3]);
   const int tb = rblk * S::kRows / 16;  // first 16-row tile of the block
   const int t0 = tb + wr * RT;           // first 16-row tile of the wavefront
   const uint8_t *rec = a.base + (size_t)ex * a.stride;
@@ -231,39 +339,71 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   //      scale byte is 0 (the packer zero-fills them) while the B records hold zeros there, so
   //      it adds exact zeros. Every lane of every DMA runs, so each wavefront issues exactly
   //      kIssue VMEM operations per step, which the vmcnt waits count on.
-  const uint8_t *bsrc[S::kDma];
+  const uint8_t *bsrc[S::kBStat ? 1 : S::kDma];
+  uint32_t boff[S::kBStat ? S::kDma : 1];  // B-stationary shape: offsets from a.brec (records < 4 GB)
 #pragma unroll
   for (int i = 0; i < S::kDma; i++) {
     const int c = min(64 * (W * i + wv) + lane, S::kStepChunks - 1);
     const int e = c / kChunks, part = c % kChunks;
     const int ge = beg + min(e, ncol - 1);
     const int row = a.entry_src ? a.entry_src[ge] : ge;
-    bsrc[i] = a.brec + (size_t)row * G::kBytes + 16 * part;
+    if constexpr (S::kBStat)
+      boff[i] = (uint32_t)row * (uint32_t)G::kBytes + 16u * part;
+    else
+      bsrc[i] = a.brec + (size_t)row * G::kBytes + 16 * part;
   }
   const uint8_t *asrc[S::kDmaA];  // the wavefront's share of the block's A tiles: W i + wv
   const uint8_t *ssrc[S::kDmaA];
   const size_t last_chunk = (size_t)d.rows * d.nb - 1;
+  const int wvu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
   for (int i = 0; i < S::kDmaA; i++) {
-    const int tl = min(tb + W * i + wv, (int)d.tiles - 1);
-    asrc[i] = mat + (size_t)tl * 16 * d.nb * 16;
-    ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
+    const int tl = min(tb + W * i + wvu, (int)d.tiles - 1);
+    if constexpr (S::kBStat) {  // tile bases (wavefront-uniform); the lane part is added per step
+      asrc[i] = mat + (size_t)tl * 16 * d.nb * 16;
+      ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256;
+    } else {
+      asrc[i] = mat + (size_t)tl * 16 * d.nb * 16;
+      ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
+    }
   }
+  // B-stationary shape: the last 16-byte chunk of a tile (a lane's chunk past it, in the last
+  // step, is clamped into the tile: its scale byte is 0 and its B values are 0, so it adds 0)
+  const uint32_t a_last = 16u * d.nb * 16u - 16u;
   bool tv[RT];
 #pragma unroll
   for (int r = 0; r < RT; r++) tv[r] = t0 + r < (int)d.tiles;
+  // wavefront-uniform bound of the B-stationary step: its row tiles inside the matrix
+  const int nrt_valid = __builtin_amdgcn_readfirstlane(min(RT, (int)d.tiles - t0));
   const uint8_t *alast = mat + last_chunk * 16;
+#define GEMM_LOAD_S(step, sl)                                                                       \
+  do {                                                                                              \
+    const uint8_t *bb_ = a.brec + (size_t)(step) * G::kStep;                                        \
+    _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                           \
+      lds_dma16_s(boff[i], bb_, W * i + wvu >= S::kGroups ? s_dummy : (sl) + 1024 * (W * i + wvu)); \
+    }                                                                                               \
+    const uint32_t ao_ = min((uint32_t)(step) * 1024u + 16u * lane, a_last);                        \
+    _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                            \
+      lds_dma16_s(ao_, asrc[i], (sl) + S::kBufB + (W * i + wvu) * 1024);                           \
+    const uint32_t so_ = (uint32_t)((step) >> 2) * 256u + 4u * lane;                                 \
+    _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                            \
+      lds_dma4_s(so_, ssrc[i], (sl) + S::kBufB + S::kBufA + (W * i + wvu) * 256);                  \
+  } while (0)
 #define GEMM_LOAD(step, sl)                                                                         \
   do {                                                                                              \
-    _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                           \
-      lds_dma16(bsrc[i] + (size_t)(step) * G::kStep, (sl) + 1024 * (W * i + wv));                  \
+    if constexpr (S::kBStat) {                                                                      \
+      GEMM_LOAD_S(step, sl);                                                                        \
+    } else {                                                                                        \
+      _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                         \
+        lds_dma16(bsrc[S::kBStat ? 0 : i] + (size_t)(step) * G::kStep, (sl) + 1024 * (W * i + wv)); \
+      }                                                                                             \
+      _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++) {                                        \
+        const uint8_t *src = asrc[i] + (size_t)(step) * 1024 + 16 * lane;                           \
+        lds_dma16(src < alast ? src : alast, (sl) + S::kBufB + (W * i + wv) * 1024);                \
+      }                                                                                             \
+      _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                          \
+        lds_dma4(ssrc[i] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (W * i + wv) * 256); \
     }                                                                                               \
-    _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++) {                                          \
-      const uint8_t *src = asrc[i] + (size_t)(step) * 1024 + 16 * lane;                             \
-      lds_dma16(src < alast ? src : alast, (sl) + S::kBufB + (W * i + wv) * 1024);                  \
-    }                                                                                               \
-    _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                            \
-      lds_dma4(ssrc[i] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (W * i + wv) * 256); \
   } while (0)
 
   f32x4 acc[RT][CG];
@@ -274,8 +414,8 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 
   // ---- bias of the wavefront's rows into LDS by DMA before the K loop (complete at the first
   //      wait), read in the epilogue
-  {
-    const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
+  const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
+  if constexpr (!S::kBStat) {
 #pragma unroll
     for (int k = 0; k < kBiasTiles / 4; k++)
       lds_dma4(bias + min(t0 * 16 + 64 * k + lane, (int)d.rows - 1), s_bias + (wv * kBiasTiles + 4 * k) * 16);
@@ -293,7 +433,10 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   do {                                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     GEMM_LOAD(min((st) + D - 1, ns - 1), nxt);                                                      \
-    gemm_step<RT, CGW, WR, WC, D>(acc, cur, wr, wc, lane, 8 * ((st) & 3));                          \
+    if constexpr (S::kBStat)                                                                        \
+      gemm_step_bstat<RT, CGW, WR, WC, D, false>(acc, cur, wr, wc, lane, 8 * ((st) & 3), nrt_valid); \
+    else                                                                                            \
+      gemm_step<RT, CGW, WR, WC, D>(acc, cur, wr, wc, lane, 8 * ((st) & 3));                        \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));                                  \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
@@ -320,11 +463,17 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   }
 #undef GEMM_STEP
 #undef GEMM_LOAD
+#undef GEMM_LOAD_S
 
   // ---- epilogue
   float4 bv[RT];
 #pragma unroll
-  for (int r = 0; r < RT; r++) bv[r] = *reinterpret_cast<const float4 *>(s_bias + (wv * kBiasTiles + r) * 16 + 4 * g);
+  for (int r = 0; r < RT; r++) {
+    if constexpr (S::kBStat)
+      bv[r] = *reinterpret_cast<const float4 *>(bias + min(t0 + r, (int)d.tiles - 1) * 16 + 4 * g);
+    else
+      bv[r] = *reinterpret_cast<const float4 *>(s_bias + (wv * kBiasTiles + r) * 16 + 4 * g);
+  }
   if constexpr (MODE == GEMV_GATE_UP) {
     // every 4 row tiles (64 rows) of the wavefront = h block hb (h values 32 hb .. 32 hb + 31)
     // of its entries. The SwiGLU values are staged in the (now free) ring as f32 [entry][32];
@@ -460,6 +609,7 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3>(a, s);
   if (a.shape == 6) return launch_gemm_shape<MODE, 4, 1, 1, 1, 3>(a, s);
   if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3>(a, s);
+  if (a.shape == 8) return launch_gemm_shape<MODE, 16, 4, 2, 2, 2>(a, s);
   if (mean >= 48)
     return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2>(a, s);
   if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3>(a, s);

@@ -565,7 +565,8 @@ def test_batch_gemm_matches_oracle_and_gemv(orc, shape):
 
 
 def test_batch_gemm_block_shapes_identical(orc):
-    """Every block shape (large-batch 8 wavefronts as 4 x 2 or 8 x 1; forced 256-row x 32- and
+    """Every block shape (large-batch 8 wavefronts as 4 x 2 or 8 x 1; the 512 x 128 block of 4
+    wavefronts of 256 rows x 64 entries; forced 256-row x 32- and
     16-entry blocks; 128-row blocks of 4 or 2 wavefronts, the 2-row-tile one for down only)
     accumulates every output in the same K and term order: identical results."""
     H, I, E, k, T = 512, 512, 16, 4, 300
@@ -575,7 +576,8 @@ def test_batch_gemm_block_shapes_identical(orc):
     x = syn.hidden(T, H, seed=411)
     d.set_batch_gemm(2)
     outs = []
-    shapes = [(0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (0, 4), (2, 5), (5, 4), (7, 6)]
+    shapes = [(0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (8, 0), (0, 4), (2, 5), (5, 4),
+              (7, 6), (8, 8)]
     for shape, down in shapes:
         d.set_gemm_shape(shape, down)
         outs.append(d.layer_forward(0, x, k))
@@ -638,7 +640,7 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
     d.set_batch_gemm(1)
     e = rel_l2(got, ref)
     assert e < 6e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
-    for shape, down in [(1, 0), (2, 2), (3, 3), (0, 4)]:
+    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4)]:
         d.set_gemm_shape(shape, down)
         o = d.layer_forward(0, x, k)
         assert np.array_equal(got, o), f"T={T} E={E} shape {shape} down {down}"
