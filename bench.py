@@ -10,8 +10,9 @@ distinct tokens, so every step streams its experts from HBM.
 The default run (`--workload all`) also times the other configurations in the same process and
 reports each under `configs` with its own dominant-kernel roofline: config 1 (one 2880x2880
 MXFP4 matvec), config 3 (64 tokens through one layer), config 4 (4096 tokens through all 24
-layers), config 5 (a 120B-shaped layer, 128 experts, at 1 and 2048 tokens). Those use their own
-step counts (in each entry); --steps / --warmup apply to the headline.
+layers), config 5 (a 120B-shaped layer, 128 experts, at 1 and 2048 tokens), and the next row
+beside the path (the bf16 LM head). Those use their own step counts (in each entry); --steps /
+--warmup apply to the headline.
 
 Prints ONE JSON line. `--workload <name>` runs one configuration alone (for profiling).
 """
@@ -417,6 +418,48 @@ def run_lm_head(steps, warmup, H=2880, V=201088):
                          "timing": "HIP events on the context stream around the timed region / launches"}}
 
 
+def run_lm_head_bf16(steps, warmup, H=2880, V=201088):
+    """The LM head from the checkpoint's bf16 lm_head.weight (lm_head_dot, weights.rs:73-82):
+    201 088 x 2880 bf16 = 1.16 GB streamed per call, device-resident input and logits; weights
+    generated on the device (bf16 of N(0, 0.02))."""
+    L = lib()
+    log(f"lm head bf16: {V} x {H} ({V * H * 2 / 1e9:.2f} GB)")
+    disp = GpuMoeDispatcher(H, H, 7.0)
+    wd = DeviceBuffer(V * H * 2)
+    check(L.moe_synth_fill_device(wd.ptr, V * H, 1, 77, 0.02, 0, None))
+    disp.init_lm_head_bf16_device(wd, V)
+    wd.close()
+    x = DeviceBuffer(H * 4)
+    check(L.moe_synth_fill_device(x.ptr, H, 2, 78, 1.0, 0, None))
+    y = DeviceBuffer(V * 4)
+    for _ in range(warmup):
+        disp.dispatch_lm_head_device(x, V, y)
+    disp.synchronize()
+    region = StreamEvents(L.moe_stream(disp.ctx))
+    t0 = time.perf_counter()
+    region.start()
+    for _ in range(steps):
+        disp.dispatch_lm_head_device(x, V, y)
+    region.stop()
+    disp.synchronize()
+    el = time.perf_counter() - t0
+    region_s = region.elapsed_ms() / 1e3
+    region.close()
+    for b in (x, y):
+        b.close()
+    disp.close()
+    byts = V * H * 2 + H * 4 + V * 4
+    kgbs = byts * steps / region_s / 1e9  # one k_lm_head_bf16 launch per step
+    return {"value": round(byts * steps / el / 1e9, 1), "unit": "GB/s", "steps": steps,
+            "warmup": warmup, "ms_per_step": round(el * 1e3 / steps, 6), "dtype": "bf16 x f32, f32 acc",
+            "config": {"workload": "lm head (next row) 201088x2880 bf16 (checkpoint dtype)", "vocab": V, "hidden": H},
+            "roofline": {"bound": "hbm", "kernel": "k_lm_head_bf16", "achieved": round(kgbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes_per_launch": byts,
+                         "avg_launch_us": round(region_s / steps * 1e6, 3),
+                         "timing": "HIP events on the context stream around the timed region / launches"}}
+
+
 def copy_calibration(mib):
     """One plain device-to-device copy of `mib` MiB (the runtime's blit kernel,
     __amd_rocclr_copyBuffer): under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch
@@ -525,7 +568,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="headline steps (default: per workload)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="all", choices=["all", "matvec", "lm_head"] + list(WORKLOADS))
+    ap.add_argument("--workload", default="all", choices=["all", "matvec", "lm_head", "lm_head_bf16"] + list(WORKLOADS))
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--layers-120b", type=int, default=6)
     ap.add_argument("--no-graph", dest="graph", action="store_false")
@@ -551,7 +594,8 @@ def main():
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
     head = "decode1" if args.workload == "all" else args.workload
-    dsteps, dwarm = {"matvec": (4800, 480), "lm_head": (40, 4)}.get(head, WORKLOADS.get(head, (0,) * 6)[4:])
+    dsteps, dwarm = {"matvec": (4800, 480), "lm_head": (40, 4), "lm_head_bf16": (80, 8)}.get(
+        head, WORKLOADS.get(head, (0,) * 6)[4:])
     steps = dsteps if args.steps is None else args.steps
     warmup = dwarm if args.warmup is None else args.warmup
     common = {"metric": METRIC, "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
@@ -560,13 +604,15 @@ def main():
                        "router N(0,0.02) bf16, biases N(0,0.01) bf16, x N(0,1))")}
     if head == "matvec":
         common["metric"] = "MXFP4 matvec 2880x2880 GB/s (config 1)"
-    elif head == "lm_head":
+    elif head in ("lm_head", "lm_head_bf16"):
         common["metric"] = "LM head GEMV 201088x2880 GB/s"
     t_start = time.perf_counter()
     if head == "matvec":
         res = run_matvec(steps, warmup, args.graph)
     elif head == "lm_head":
         res = run_lm_head(steps, warmup)
+    elif head == "lm_head_bf16":
+        res = run_lm_head_bf16(steps, warmup)
     else:
         E = WORKLOADS[head][1]
         m = Model(H20, I20, E, args.layers if E == 32 else args.layers_120b, args)
@@ -585,6 +631,8 @@ def main():
             m.close()
             extras["config1_matvec"] = run_matvec(4800, 480, args.graph)
             log(f"matvec: {extras['config1_matvec']['value']} GB/s")
+            extras["next_lm_head_bf16"] = run_lm_head_bf16(80, 8)
+            log(f"lm head bf16: {extras['next_lm_head_bf16']['value']} GB/s")
             res["configs"] = extras
         else:
             m.close()

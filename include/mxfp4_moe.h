@@ -214,6 +214,14 @@ int moe_dispatch_experts_batched(moe_ctx *ctx, const float *input, size_t n,
 
 /* GpuMoeDispatcher::init_lm_head — moe_dispatch.rs:611-621. weights [vocab, H] f32. */
 int moe_init_lm_head(moe_ctx *ctx, const float *weights, size_t vocab_size);
+/* The LM head from the checkpoint's BF16 lm_head.weight [vocab, H] (weights.rs:56, loaded at
+ * :251) — the live path's form: ModelWeights::lm_head_dot (weights.rs:73-82, bf16 widened exactly
+ * to f32, f32 accumulation) and the bf16 chunks of session.rs:425-450; half the bytes of the f32
+ * form. Replaces an earlier init (f32 or bf16); dispatch_lm_head(_device) then reads these rows.
+ * Needs H % 8 == 0 and H <= 3072. The _device form copies from device memory on `stream`. */
+int moe_init_lm_head_bf16(moe_ctx *ctx, const uint16_t *weights_bf16, size_t vocab_size);
+int moe_init_lm_head_bf16_device(moe_ctx *ctx, const uint16_t *weights_bf16, size_t vocab_size,
+                                 void *stream);
 /* GpuMoeDispatcher::dispatch_lm_head — moe_dispatch.rs:624-683. logits[vocab] = W input.
  * Returns MOE_ERR_STATE where the reference panics ("call init_lm_head first"). */
 int moe_dispatch_lm_head(moe_ctx *ctx, const float *input, size_t vocab_size, float *logits);

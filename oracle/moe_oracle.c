@@ -648,3 +648,17 @@ int orc_live_moe_token(const float *x, size_t H, size_t I, size_t k, const int32
   free(outs); free(jobs);
   return 0;
 }
+
+/* ------------------------------------------------------------------ LM head (bf16 rows) */
+
+/* ModelWeights::lm_head_dot (weights.rs:73-82) for every row: w = bf16 -> f32 (exact),
+ * acc = 0; acc += w * x[i] (separate product and sum, sequential in i). */
+void orc_lm_head_bf16(const uint16_t *w_bf16, const float *x, size_t vocab, size_t H, float *y) {
+#pragma omp parallel for schedule(static)
+  for (long v = 0; v < (long)vocab; v++) {
+    const uint16_t *row = w_bf16 + (size_t)v * H;
+    float acc = 0.0f;
+    for (size_t i = 0; i < H; i++) acc = acc + orc_bf16_to_f32(row[i]) * x[i];
+    y[v] = canon(acc);
+  }
+}

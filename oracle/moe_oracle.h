@@ -164,6 +164,8 @@ int orc_live_moe_token_warm(const float *x, size_t H, size_t I, size_t n, const 
                             const uint16_t *const *gu, const uint16_t *const *gub,
                             const uint16_t *const *d, const uint16_t *const *db, int n_threads,
                             float *y);
+/* ModelWeights::lm_head_dot (weights.rs:73-82) for all rows of a bf16 [vocab, H] LM head. */
+void orc_lm_head_bf16(const uint16_t *w_bf16, const float *x, size_t vocab, size_t H, float *y);
 /* OpenMP threads the oracle's parallel loops use (the fp32 path's matmuls). */
 int orc_omp_max_threads(void);
 

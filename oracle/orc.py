@@ -82,6 +82,7 @@ def lib():
                                           ctypes.c_int, _f32p]
     L.orc_live_moe_token_warm.restype = ctypes.c_int
     L.orc_omp_max_threads.restype = ctypes.c_int
+    L.orc_lm_head_bf16.argtypes = [_u16p, _f32p, _sz, _sz, _f32p]
     _lib = L
     return L
 
@@ -284,3 +285,12 @@ def live_moe_token_warm(x, H, I, entries, w, n_threads):
 
 def omp_threads():
     return int(lib().orc_omp_max_threads())
+
+
+def lm_head_bf16(w_bf16, x):
+    """weights.rs:73-82 lm_head_dot over every row: bf16 [V, H] bits, x [H] -> f32 [V]."""
+    w = _c(w_bf16, np.uint16)
+    V, H = w.shape
+    y = np.empty(V, np.float32)
+    lib().orc_lm_head_bf16(w.reshape(-1), _c(x, np.float32).reshape(-1), V, H, y)
+    return y

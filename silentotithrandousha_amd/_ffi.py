@@ -77,6 +77,8 @@ SIGNATURES = {
                                    _vp, _sz, _vp]),
     "moe_dispatch_experts_batched": (_int, [_vp, _vp, _sz, _vp, _vp]),
     "moe_init_lm_head": (_int, [_vp, _vp, _sz]),
+    "moe_init_lm_head_bf16": (_int, [_vp, _vp, _sz]),
+    "moe_init_lm_head_bf16_device": (_int, [_vp, _vp, _sz, _vp]),
     "moe_dispatch_lm_head": (_int, [_vp, _vp, _sz, _vp]),
     "moe_dispatch_lm_head_device": (_int, [_vp, _vp, _sz, _vp, _vp]),
     "moe_router_topk": (_int, [_vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp]),

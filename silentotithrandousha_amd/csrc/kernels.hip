@@ -16,6 +16,8 @@
 // in f32 inside the MFMA.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -800,6 +802,65 @@ __global__ __launch_bounds__(256) void k_lm_head(const float *w, const float *x,
   if (lane == 0) y[row] = acc;
 }
 
+// logits[v] = sum_i bf16_to_f32(W[v, i]) x[i] with the checkpoint's bf16 rows (lm_head_dot,
+// weights.rs:73-82: bf16 widened exactly, f32 accumulation). A wavefront walks rows v = wave,
+// wave + n_waves, ... two at a time; lane l keeps x[8 (l + 64 q) .. + 7] (q < kLmQ) in registers
+// for all its rows and accumulates its 16-byte pieces of a row with fused multiply-adds in q
+// order, then a xor butterfly over the 64 lanes. Weights are streamed with non-temporal loads.
+constexpr int kLmQ = 6;  // 16-byte pieces per lane per row: H <= 64 * 8 * kLmQ = 3072
+__global__ __launch_bounds__(256) void k_lm_head_bf16(const uint16_t *w, const float *x, size_t vocab, int H,
+                                                      float *y) {
+  const int lane = threadIdx.x & 63;
+  const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6), n_waves = (size_t)gridDim.x * 4;
+  const int nq = H / 8;  // 16-byte pieces per row
+  float xr[kLmQ][8];
+#pragma unroll
+  for (int q = 0; q < kLmQ; q++) {
+    const int p = lane + 64 * q;
+    if (p < nq) {
+      const float4 a = reinterpret_cast<const float4 *>(x)[2 * p];
+      const float4 b = reinterpret_cast<const float4 *>(x)[2 * p + 1];
+      xr[q][0] = a.x; xr[q][1] = a.y; xr[q][2] = a.z; xr[q][3] = a.w;
+      xr[q][4] = b.x; xr[q][5] = b.y; xr[q][6] = b.z; xr[q][7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) xr[q][i] = 0.0f;
+    }
+  }
+  for (size_t v0 = wave * 2; v0 < vocab; v0 += 2 * n_waves) {
+    const size_t v1 = v0 + 1 < vocab ? v0 + 1 : v0;  // an odd last row is computed twice, stored once
+    u32x4 wv[2][kLmQ];
+#pragma unroll
+    for (int q = 0; q < kLmQ; q++) {
+      const int p = lane + 64 * q;
+      wv[0][q] = p < nq ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + v0 * H) + p) : u32x4{0, 0, 0, 0};
+      wv[1][q] = p < nq ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + v1 * H) + p) : u32x4{0, 0, 0, 0};
+    }
+    float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+#pragma unroll
+      for (int q = 0; q < kLmQ; q++) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+          const uint32_t u = wv[r][q][h];
+          acc[r] = __builtin_fmaf(__uint_as_float(u << 16), xr[q][2 * h], acc[r]);
+          acc[r] = __builtin_fmaf(__uint_as_float(u & 0xFFFF0000u), xr[q][2 * h + 1], acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      acc[0] = acc[0] + __shfl_xor(acc[0], o);
+      acc[1] = acc[1] + __shfl_xor(acc[1], o);
+    }
+    if (lane == 0) {
+      y[v0] = acc[0];
+      if (v1 != v0) y[v1] = acc[1];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ RMSNorm and residual
 
 // n[t] = (x[t] * inv_rms) * gamma, one wavefront per row (session.rs:483-493, the sum of squares
@@ -859,6 +920,18 @@ __global__ __launch_bounds__(256) void k_add_rows(float *y, const float *x, size
 hipError_t launch_add_rows(float *y, const float *x, size_t n, hipStream_t s) {
   if (!n) return hipSuccess;
   hipLaunchKernelGGL(k_add_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, x, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_head_bf16(const uint16_t *w, const float *x, size_t vocab, size_t H, float *y, int n_cu,
+                               hipStream_t s) {
+  if (H % 8 || H > 64 * 8 * kLmQ || !vocab || (reinterpret_cast<uintptr_t>(x) & 15) ||
+      (reinterpret_cast<uintptr_t>(w) & 15))
+    return hipErrorInvalidValue;
+  // four blocks (16 wavefronts) per CU, each wavefront a grid-stride walk over row pairs
+  const size_t pairs_blocks = (vocab + 7) / 8;
+  const unsigned blocks = (unsigned)std::min<size_t>(pairs_blocks, (size_t)4 * (n_cu > 0 ? n_cu : 256));
+  hipLaunchKernelGGL(k_lm_head_bf16, dim3(blocks), dim3(256), 0, s, w, x, vocab, (int)H, y);
   return hipGetLastError();
 }
 

@@ -161,6 +161,8 @@ hipError_t launch_matvec_fp4(const uint8_t *packed, size_t rows, size_t cols, co
                              float *y, hipStream_t s);
 hipError_t launch_lm_head(const float *w, const float *x, size_t vocab, size_t H, float *y,
                           hipStream_t s);
+hipError_t launch_lm_head_bf16(const uint16_t *w, const float *x, size_t vocab, size_t H, float *y, int n_cu,
+                               hipStream_t s);
 // Post-attention RMSNorm of T rows (rms_inv_wave's order) and the residual add y += x.
 hipError_t launch_rmsnorm(const float *x, size_t T, size_t H, const float *gamma, float eps, float *n,
                           hipStream_t s);

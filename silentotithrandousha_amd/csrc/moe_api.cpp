@@ -119,6 +119,7 @@ struct moe_ctx {
   void *mv_list_at = nullptr;  // mv_split.p when its list was written
   DevBuf lm_w, lm_x, lm_y;
   size_t lm_vocab = 0;
+  bool lm_bf16 = false;  // lm_w holds the checkpoint's bf16 rows (else f32)
   bool timing = false;
   bool capturing = false;
   // single-token forwards: 0 = the batch path, 1 = two decode kernels, 2 = one launch
@@ -843,17 +844,49 @@ int moe_dispatch_experts_batched(moe_ctx *c, const float *input, size_t n,
   return MOE_OK;
 }
 
+static int init_lm_head_common(moe_ctx *c, const void *weights, size_t vocab, size_t elem,
+                               hipMemcpyKind kind, hipStream_t s);
+
 int moe_init_lm_head(moe_ctx *c, const float *weights, size_t vocab) {
+  if (!c) return fail(MOE_ERR_INVALID, "null context");
+  return init_lm_head_common(c, weights, vocab, 4, hipMemcpyHostToDevice, c->stream);
+}
+
+// LM head weights [vocab, H] into lm_w: f32 or the checkpoint's bf16 rows; kind of the source
+// pointer given by `kind`.
+static int init_lm_head_common(moe_ctx *c, const void *weights, size_t vocab, size_t elem,
+                               hipMemcpyKind kind, hipStream_t s) {
   RETURN_IF(use_dev(c));
   if (!weights || !vocab) return fail(MOE_ERR_INVALID, "null weights or zero vocab");
+  if (vocab > ((size_t)1 << 40) / c->H) return fail(MOE_ERR_INVALID, "vocab_size %zu too large", vocab);
   c->lm_vocab = 0;  // not initialised until the new weights are resident
-  if (c->lm_w.cap < vocab * c->H * 4) c->lm_w.release();
-  RETURN_IF(c->lm_w.ensure(vocab * c->H * 4));
+  if (c->lm_w.cap < vocab * c->H * elem) c->lm_w.release();
+  RETURN_IF(c->lm_w.ensure(vocab * c->H * elem));
   RETURN_IF(c->lm_x.ensure(c->H * 4));
   RETURN_IF(c->lm_y.ensure(vocab * 4));
-  HIP_TRY(hipMemcpy(c->lm_w.p, weights, vocab * c->H * 4, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpyAsync(c->lm_w.p, weights, vocab * c->H * elem, kind, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  c->lm_bf16 = elem == 2;
   c->lm_vocab = vocab;
   return MOE_OK;
+}
+
+int moe_init_lm_head_bf16(moe_ctx *c, const uint16_t *weights_bf16, size_t vocab) {
+  if (!c) return fail(MOE_ERR_INVALID, "null context");
+  if (c->H % 8 || c->H > 3072) return fail(MOE_ERR_INVALID, "bf16 LM head needs hidden %% 8 == 0 and <= 3072");
+  return init_lm_head_common(c, weights_bf16, vocab, 2, hipMemcpyHostToDevice, c->stream);
+}
+
+int moe_init_lm_head_bf16_device(moe_ctx *c, const uint16_t *weights_bf16, size_t vocab, void *stream) {
+  if (!c) return fail(MOE_ERR_INVALID, "null context");
+  if (c->H % 8 || c->H > 3072) return fail(MOE_ERR_INVALID, "bf16 LM head needs hidden %% 8 == 0 and <= 3072");
+  return init_lm_head_common(c, weights_bf16, vocab, 2, hipMemcpyDeviceToDevice, pick(c, stream));
+}
+
+static hipError_t lm_head_launch(moe_ctx *c, const float *x, size_t vocab, float *y, hipStream_t s) {
+  if (c->lm_bf16)
+    return launch_lm_head_bf16((const uint16_t *)c->lm_w.p, x, vocab, c->H, y, c->n_cu, s);
+  return launch_lm_head((const float *)c->lm_w.p, x, vocab, c->H, y, s);
 }
 
 int moe_dispatch_lm_head(moe_ctx *c, const float *input, size_t vocab, float *logits) {
@@ -863,8 +896,7 @@ int moe_dispatch_lm_head(moe_ctx *c, const float *input, size_t vocab, float *lo
   if (vocab > c->lm_vocab)
     return fail(MOE_ERR_INVALID, "vocab_size %zu exceeds the initialised %zu", vocab, c->lm_vocab);
   HIP_TRY(hipMemcpyAsync(c->lm_x.p, input, c->H * 4, hipMemcpyHostToDevice, c->stream));
-  HIP_TRY(launch_lm_head((const float *)c->lm_w.p, (const float *)c->lm_x.p, vocab, c->H,
-                         (float *)c->lm_y.p, c->stream));
+  HIP_TRY(lm_head_launch(c, (const float *)c->lm_x.p, vocab, (float *)c->lm_y.p, c->stream));
   HIP_TRY(hipMemcpyAsync(logits, c->lm_y.p, vocab * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return MOE_OK;
@@ -876,7 +908,7 @@ int moe_dispatch_lm_head_device(moe_ctx *c, const float *input, size_t vocab, fl
   if (!input || !logits) return fail(MOE_ERR_INVALID, "null input or logits");
   if (vocab > c->lm_vocab)
     return fail(MOE_ERR_INVALID, "vocab_size %zu exceeds the initialised %zu", vocab, c->lm_vocab);
-  HIP_TRY(launch_lm_head((const float *)c->lm_w.p, input, vocab, c->H, logits, pick(c, stream)));
+  HIP_TRY(lm_head_launch(c, input, vocab, logits, pick(c, stream)));
   return MOE_OK;
 }
 

@@ -233,6 +233,17 @@ class GpuMoeDispatcher:
         check(lib().moe_init_lm_head(self._ctx, _p(w), vocab_size))
         self.lm_vocab = vocab_size
 
+    def init_lm_head_bf16(self, weights_bf16, vocab_size):
+        """The checkpoint's BF16 lm_head.weight as bf16 bits [vocab, H] (weights.rs:56, 251;
+        lm_head_dot weights.rs:73-82)."""
+        w = _c(weights_bf16, np.uint16)
+        check(lib().moe_init_lm_head_bf16(self._ctx, _p(w), vocab_size))
+        self.lm_vocab = vocab_size
+
+    def init_lm_head_bf16_device(self, weights_dev, vocab_size, stream=None):
+        check(lib().moe_init_lm_head_bf16_device(self._ctx, _dp(weights_dev), vocab_size, stream))
+        self.lm_vocab = vocab_size
+
     def dispatch_lm_head(self, x, vocab_size):
         y = np.empty(vocab_size, np.float32)
         check(lib().moe_dispatch_lm_head(self._ctx, _p(_c(x, np.float32)), vocab_size, _p(y)))

@@ -196,6 +196,40 @@ def test_lm_head_host_and_device():
     d.close()
 
 
+@pytest.mark.parametrize("H,V", [(2880, 50001), (64, 37)])
+def test_lm_head_bf16(orc, H, V):
+    """The checkpoint's bf16 LM head (lm_head_dot, weights.rs:73-82): every logit within the
+    sum-of-products bound gamma_n sum |w x| of the float64 dot (n = H + 8: the kernel's fused
+    lane chains and its 64-lane butterfly) and so of the oracle's sequential restatement; 50 001
+    rows make every wavefront walk several row pairs and leave an odd last row. The host and
+    device initialisations give the same bits; an f32 init after a bf16 one switches back."""
+    from silentotithrandousha_amd import DeviceBuffer
+    rng = np.random.default_rng(61)
+    w = syn.bf16_bits((rng.standard_normal((V, H)) * 0.02).astype(np.float32))
+    x = rng.standard_normal(H).astype(np.float32)
+    d = GpuMoeDispatcher(H, H, 7.0)
+    d.init_lm_head_bf16(w, V)
+    got = d.dispatch_lm_head(x, V).astype(np.float64)
+    W = syn.bf16_to_f32(w).astype(np.float64)
+    y64 = W @ x.astype(np.float64)
+    u = 2.0 ** -24
+    n = H + 8
+    bound = n * u / (1 - n * u) * (np.abs(W) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(got - y64) <= bound)
+    want = orc.lm_head_bf16(w, x).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2 * bound)
+    assert rel_l2(got, y64) < 1e-6
+    wd, xd, yd = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), DeviceBuffer(V * 4)
+    d.init_lm_head_bf16_device(wd, V)
+    d.dispatch_lm_head_device(xd, V, yd)
+    d.synchronize()
+    assert np.array_equal(yd.download(np.float32, (V,)), got.astype(np.float32))
+    wf = syn.bf16_to_f32(w[:8])
+    d.init_lm_head(wf, 8)
+    assert rel_l2(d.dispatch_lm_head(x, 8), wf.astype(np.float64) @ x.astype(np.float64)) < 1e-5
+    d.close()
+
+
 # ---------------------------------------------------------------- router + top-k
 
 def test_router_logits_and_topk_bit_exact(orc, disp20, layer20):

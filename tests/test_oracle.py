@@ -348,6 +348,30 @@ def test_oracle_mxfp4_matvec_float64_bound(orc):
     assert rel_l2(got, y64) < 1e-6
 
 
+# ---------------------------------------------------------------- LM head (weights.rs:73-82)
+
+def test_oracle_lm_head_bf16_brute_force_and_bound(orc):
+    """lm_head_dot: brute force (float32 sequential, separately rounded) on 3 x 40 rows bit for
+    bit; an order-sensitive row (2^24, 1, -2^24 -> 0); 257 x 2880 within the sequential-sum
+    bound of the float64 dot of the exactly widened bf16 values."""
+    rng = np.random.default_rng(41)
+    w = syn.bf16_bits(rng.normal(0, 0.05, size=(3, 40)).astype(np.float32))
+    x = rng.normal(0, 1, 40).astype(np.float32)
+    wf = syn.bf16_to_f32(w)
+    want = np.array([_seq_dot_f32(wf[r], x) for r in range(3)], np.float32)
+    assert_bit_exact(orc.lm_head_bf16(w, x), want, "3 x 40 lm head")
+    w1 = syn.bf16_bits(np.array([[1.0, 1.0, 1.0, 0.0]], np.float32))
+    assert orc.lm_head_bf16(w1, np.array([2.0 ** 24, 1.0, -(2.0 ** 24), 0.0], np.float32))[0] == 0.0
+    V, H = 257, 2880
+    w = syn.bf16_bits(rng.normal(0, 0.02, size=(V, H)).astype(np.float32))
+    x = rng.normal(0, 1, H).astype(np.float32)
+    W = syn.bf16_to_f32(w).astype(np.float64)
+    y64 = W @ x.astype(np.float64)
+    u = 2.0 ** -24
+    gamma = (H + 1) * u / (1 - (H + 1) * u)
+    assert np.all(np.abs(orc.lm_head_bf16(w, x) - y64) <= gamma * (np.abs(W) @ np.abs(x.astype(np.float64))))
+
+
 # ---------------------------------------------------------------- live CPU path (session.rs:16-124)
 
 def test_matvec_f16xf32_neon_order(orc):
