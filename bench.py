@@ -460,6 +460,52 @@ def run_lm_head_bf16(steps, warmup, H=2880, V=201088):
                          "timing": "HIP events on the context stream around the timed region / launches"}}
 
 
+def run_beaver32(steps, warmup, n=5, t=1, count=50_000_000):
+    """The Beaver-triple generator (§8's last row; the reference's GpuTripleGen32,
+    gpu/mod.rs:511-1012): `count` triples of one party per call with device-resident seeds and
+    outputs — the reference's kernel-only throughput path (dispatch_kernel_only, mod.rs:915-938,
+    timed at 50M triples in beaver.rs:3576-3610, n = 5, t = 1)."""
+    from silentotithrandousha_amd import GpuTripleGen32
+    L = lib()
+    g = GpuTripleGen32(n, t)
+    rounds = g.num_rounds(count)
+    seeds = DeviceBuffer(rounds * 4)
+    check(L.moe_synth_fill_device(seeds.ptr, rounds * 4, 0, 91, 0, 255, None))
+    outs = [DeviceBuffer(count * 4) for _ in range(3)]
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    stream = ctypes.c_void_p()
+    if hip.hipStreamCreate(ctypes.byref(stream)):
+        raise RuntimeError("hipStreamCreate failed")
+    for _ in range(warmup):
+        g.generate_device(0, count, seeds, *outs, stream=stream)
+    hip.hipStreamSynchronize(stream)
+    region = StreamEvents(stream.value)  # events on the stream the kernels run on
+    t0 = time.perf_counter()
+    region.start()
+    for _ in range(steps):
+        g.generate_device(0, count, seeds, *outs, stream=stream)
+    region.stop()
+    hip.hipStreamSynchronize(stream)
+    el = time.perf_counter() - t0
+    region_s = region.elapsed_ms() / 1e3
+    region.close()
+    hip.hipStreamDestroy(stream)
+    for b in outs + [seeds]:
+        b.close()
+    g.close()
+    byts = count * 12 + rounds * 4  # a, b, c words written + the round seeds read
+    return {"value": round(count * steps / el, 1), "unit": "triples/s", "steps": steps, "warmup": warmup,
+            "ms_per_step": round(el * 1e3 / steps, 6), "dtype": "u32 (mod 2^31 - 1)",
+            "config": {"workload": "beaver triples p = 2^31 - 1, one party, 50M per call", "n": n, "t": t,
+                       "count": count},
+            "roofline": {"bound": "hbm", "kernel": "k_beaver32", "achieved": round(byts * steps / region_s / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(byts * steps / region_s / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes_per_launch": byts,
+                         "avg_launch_us": round(region_s / steps * 1e6, 3),
+                         "timing": "HIP events on the launch stream around the timed region / launches"}}
+
+
 def copy_calibration(mib):
     """One plain device-to-device copy of `mib` MiB (the runtime's blit kernel,
     __amd_rocclr_copyBuffer): under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch
@@ -568,7 +614,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="headline steps (default: per workload)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="all", choices=["all", "matvec", "lm_head", "lm_head_bf16"] + list(WORKLOADS))
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "matvec", "lm_head", "lm_head_bf16", "beaver32"] + list(WORKLOADS))
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--layers-120b", type=int, default=6)
     ap.add_argument("--no-graph", dest="graph", action="store_false")
@@ -594,7 +641,7 @@ def main():
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
     head = "decode1" if args.workload == "all" else args.workload
-    dsteps, dwarm = {"matvec": (4800, 480), "lm_head": (40, 4), "lm_head_bf16": (80, 8)}.get(
+    dsteps, dwarm = {"matvec": (4800, 480), "lm_head": (40, 4), "lm_head_bf16": (80, 8), "beaver32": (20, 3)}.get(
         head, WORKLOADS.get(head, (0,) * 6)[4:])
     steps = dsteps if args.steps is None else args.steps
     warmup = dwarm if args.warmup is None else args.warmup
@@ -606,6 +653,8 @@ def main():
         common["metric"] = "MXFP4 matvec 2880x2880 GB/s (config 1)"
     elif head in ("lm_head", "lm_head_bf16"):
         common["metric"] = "LM head GEMV 201088x2880 GB/s"
+    elif head == "beaver32":
+        common["metric"] = "Beaver triples/s, p = 2^31 - 1, n = 5, t = 1"
     t_start = time.perf_counter()
     if head == "matvec":
         res = run_matvec(steps, warmup, args.graph)
@@ -613,6 +662,8 @@ def main():
         res = run_lm_head(steps, warmup)
     elif head == "lm_head_bf16":
         res = run_lm_head_bf16(steps, warmup)
+    elif head == "beaver32":
+        res = run_beaver32(steps, warmup)
     else:
         E = WORKLOADS[head][1]
         m = Model(H20, I20, E, args.layers if E == 32 else args.layers_120b, args)
@@ -633,6 +684,8 @@ def main():
             log(f"matvec: {extras['config1_matvec']['value']} GB/s")
             extras["next_lm_head_bf16"] = run_lm_head_bf16(80, 8)
             log(f"lm head bf16: {extras['next_lm_head_bf16']['value']} GB/s")
+            extras["next_beaver32"] = run_beaver32(20, 3)
+            log(f"beaver32: {extras['next_beaver32']['value']} triples/s")
             res["configs"] = extras
         else:
             m.close()

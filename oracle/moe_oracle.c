@@ -662,3 +662,91 @@ void orc_lm_head_bf16(const uint16_t *w_bf16, const float *x, size_t vocab, size
     y[v] = canon(acc);
   }
 }
+
+/* ------------------------------------------------------------------ Beaver triples, p = 2^31 - 1 */
+
+/* Field ops and hash of shader32.metal:4-33 (fmul folds 2^31 = 1; every result in [0, p)). */
+#define ORC_P32 0x7FFFFFFFu
+uint32_t orc_m31_mul(uint32_t a, uint32_t b) {
+  uint64_t x = (uint64_t)a * (uint64_t)b;
+  uint32_t lo = (uint32_t)(x & ORC_P32), hi = (uint32_t)(x >> 31);
+  uint32_t r = lo + hi;
+  r = (r >> 31) + (r & ORC_P32);
+  return r >= ORC_P32 ? r - ORC_P32 : r;
+}
+uint32_t orc_m31_add(uint32_t a, uint32_t b) {
+  uint32_t r = a + b;
+  return r >= ORC_P32 ? r - ORC_P32 : r;
+}
+uint32_t orc_chash32(uint32_t seed, uint32_t idx) {
+  uint32_t x = seed ^ (idx * 0x9e3779b9u);
+  x ^= x >> 16;
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  x &= 0x7FFFFFFFu;
+  return x >= ORC_P32 ? x - ORC_P32 : x;
+}
+
+/* beaver_triple_gen_32 (party < 0) / beaver_triple_gen_single_party_32 (party >= 0),
+ * shader32.metal:75-167, run as the Metal dispatch runs it (gpu/mod.rs:975-1000): one thread
+ * per round, threadgroups of w = min(32, num_rounds) threads, one SIMD group of 32 lanes per
+ * threadgroup, lane = index in the threadgroup. Lanes past the last round do not exist; a
+ * shuffle from a lane that does not exist is taken as 0 (the Metal result there is undefined).
+ * him[j][i] = (i + 1)^j for j < spr (mod.rs:606-612), eval_raw[p] = p + 1 (mod.rs:561). */
+void orc_beaver32(size_t n, size_t spr, long party, size_t count, const uint32_t *seeds,
+                  uint32_t *a_out, uint32_t *b_out, uint32_t *c_out) {
+  size_t rounds = (count + spr - 1) / spr;
+  size_t w = rounds < 32 ? rounds : 32;
+  uint32_t him[3][8], ev[8];
+  for (size_t i = 0; i < 8; i++) ev[i] = (uint32_t)(i + 1);
+  for (size_t j = 0; j < 3; j++)
+    for (size_t i = 0; i < 8; i++) {
+      uint32_t v = 1;
+      for (size_t e = 0; e < j; e++) v = orc_m31_mul(v, (uint32_t)(i + 1));
+      him[j][i] = v;
+    }
+  for (size_t g0 = 0; g0 < rounds; g0 += w) {
+    size_t lanes = rounds - g0 < w ? rounds - g0 : w;
+    uint32_t rt[32] = {0};
+    int exists[32] = {0};
+    for (size_t l = 0; l < lanes; l++) {
+      exists[l] = 1;
+      uint32_t i = (uint32_t)(l % n);
+      rt[l] = l < n ? orc_chash32(seeds[g0 + l], i * 3u) : 0u;
+    }
+    for (size_t l = 0; l < lanes; l++) {
+      size_t round = g0 + l, base = round * spr;
+      for (size_t j = 0; j < spr && base + j < count; j++) {
+        /* simd_fadd_reduce over xor 1, 2, 4: the aligned group of 8 lanes holding l */
+        uint32_t bt = 0;
+        for (size_t q = l & ~(size_t)7; q < (l & ~(size_t)7) + 8; q++) {
+          if (!exists[q]) continue;
+          uint32_t m = q < n ? him[j][q % n] : 0u;
+          bt = orc_m31_add(bt, orc_m31_mul(m, rt[q]));
+        }
+        uint32_t seed = seeds[round];
+        uint32_t a0 = orc_chash32(seed, (uint32_t)(n * 3 + spr * 2 + j * 2));
+        uint32_t b0 = orc_chash32(seed, (uint32_t)(n * 3 + spr * 2 + j * 2 + 1));
+        uint32_t ca = orc_chash32(seed, (uint32_t)(n * 3 + j * 2));
+        uint32_t cb = orc_chash32(seed, (uint32_t)(n * 3 + j * 2 + 1));
+        size_t out = base + j;
+        if (party >= 0) {
+          uint32_t x = ev[party];
+          a_out[out] = orc_m31_add(a0, orc_m31_mul(ca, x));
+          b_out[out] = orc_m31_add(b0, orc_m31_mul(cb, x));
+          c_out[out] = orc_m31_add(orc_m31_mul(a0, b0), orc_m31_mul(x, bt));
+        } else {
+          for (size_t p = 0; p < n; p++) {
+            uint32_t x = ev[p];
+            size_t d = p * count + out;
+            a_out[d] = orc_m31_add(a0, orc_m31_mul(ca, x));
+            b_out[d] = orc_m31_add(b0, orc_m31_mul(cb, x));
+            c_out[d] = orc_m31_add(orc_m31_mul(a0, b0), orc_m31_mul(x, bt));
+          }
+        }
+      }
+    }
+  }
+}

@@ -166,6 +166,13 @@ int orc_live_moe_token_warm(const float *x, size_t H, size_t I, size_t n, const 
                             float *y);
 /* ModelWeights::lm_head_dot (weights.rs:73-82) for all rows of a bf16 [vocab, H] LM head. */
 void orc_lm_head_bf16(const uint16_t *w_bf16, const float *x, size_t vocab, size_t H, float *y);
+/* Beaver triples over p = 2^31 - 1 (shader32.metal:4-167 as dispatched by gpu/mod.rs:975-1000):
+ * field ops, the hash, and both kernels (party < 0: every party, outputs [n][count]). */
+uint32_t orc_m31_mul(uint32_t a, uint32_t b);
+uint32_t orc_m31_add(uint32_t a, uint32_t b);
+uint32_t orc_chash32(uint32_t seed, uint32_t idx);
+void orc_beaver32(size_t n, size_t spr, long party, size_t count, const uint32_t *seeds,
+                  uint32_t *a_out, uint32_t *b_out, uint32_t *c_out);
 /* OpenMP threads the oracle's parallel loops use (the fp32 path's matmuls). */
 int orc_omp_max_threads(void);
 

@@ -83,6 +83,14 @@ def lib():
     L.orc_live_moe_token_warm.restype = ctypes.c_int
     L.orc_omp_max_threads.restype = ctypes.c_int
     L.orc_lm_head_bf16.argtypes = [_u16p, _f32p, _sz, _sz, _f32p]
+    _u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+    L.orc_m31_mul.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    L.orc_m31_mul.restype = ctypes.c_uint32
+    L.orc_m31_add.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    L.orc_m31_add.restype = ctypes.c_uint32
+    L.orc_chash32.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    L.orc_chash32.restype = ctypes.c_uint32
+    L.orc_beaver32.argtypes = [_sz, _sz, ctypes.c_long, _sz, _u32p, _u32p, _u32p, _u32p]
     _lib = L
     return L
 
@@ -294,3 +302,15 @@ def lm_head_bf16(w_bf16, x):
     y = np.empty(V, np.float32)
     lib().orc_lm_head_bf16(w.reshape(-1), _c(x, np.float32).reshape(-1), V, H, y)
     return y
+
+
+def beaver32(n, t, count, seeds, party=-1):
+    """shader32.metal's triple kernels as dispatched by gpu/mod.rs: party >= 0 -> (a, b, c) of
+    that party [count]; party = -1 -> every party's, each [n, count]."""
+    spr = n - 2 * t
+    seeds = _c(seeds, np.uint32)
+    assert seeds.size >= (count + spr - 1) // spr
+    shape = (count,) if party >= 0 else (n, count)
+    a, b, c = (np.empty(shape, np.uint32) for _ in range(3))
+    lib().orc_beaver32(n, spr, party, count, seeds, a.reshape(-1), b.reshape(-1), c.reshape(-1))
+    return a, b, c

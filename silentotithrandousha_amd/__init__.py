@@ -8,6 +8,7 @@ does, and fails loudly without the library or a gfx950 device.
 from ._ffi import LIB_PATH, MoeError, lib  # noqa: F401
 from .dispatcher import (DeviceBuffer, GpuMoeDispatcher, mxfp4_dequant, mxfp4_matvec,  # noqa: F401
                          mxfp4_pack, safetensors_find)
+from .beaver import GpuTripleGen32  # noqa: F401
 
 (KERNEL_ROUTE, KERNEL_BUCKET, KERNEL_GATE_UP, KERNEL_DOWN, KERNEL_COMBINE, KERNEL_DECODE_GATE_UP,
  KERNEL_DECODE_DOWN, KERNEL_DECODE_LAYER, KERNEL_RESERVED, KERNEL_NORM) = range(10)

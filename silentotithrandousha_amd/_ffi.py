@@ -9,6 +9,8 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp4moe.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "mxfp4_moe.h")
+# every header of the library's C ABI: the MoE path and the Beaver-triple generator
+HEADER_PATHS = [HEADER_PATH, os.path.join(os.path.dirname(_HERE), "include", "beaver32.h")]
 
 MOE_OK = 0
 MOE_ERR_INVALID = 1
@@ -107,6 +109,14 @@ SIGNATURES = {
     "moe_get_timing": (_int, [_vp, _int, ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_uint64)]),
     "moe_reset_timing": (_int, [_vp]),
+    # include/beaver32.h
+    "beaver32_create": (_int, [_sz, _sz, ctypes.POINTER(_vp)]),
+    "beaver32_destroy": (None, [_vp]),
+    "beaver32_spr": (_sz, [_vp]),
+    "beaver32_generate": (_int, [_vp, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "beaver32_generate_single_party": (_int, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "beaver32_generate_device": (_int, [_vp, ctypes.c_long, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "beaver32_synchronize": (_int, [_vp]),
 }
 
 _lib = None

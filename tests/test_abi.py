@@ -12,9 +12,11 @@ HEADER = _ffi.HEADER_PATH
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    names = re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text)
+    names = []
+    for h in _ffi.HEADER_PATHS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b((?:moe|beaver32)_[a-z0-9_]+)\s*\(", text)
     return sorted(set(names))
 
 
@@ -50,6 +52,11 @@ def test_host_side_validation_without_gpu():
     assert L.moe_create(2880, 2880, float("nan"), ctypes.byref(ctx)) == _ffi.MOE_ERR_INVALID
     assert L.moe_dispatch_lm_head(None, None, 1, None) == _ffi.MOE_ERR_INVALID
     assert L.moe_version().startswith(b"mxfp4_moe")
+    # GpuTripleGen32::new's parameter checks (gpu/mod.rs:525-536) come before any device query
+    for n, t, msg in ((4, 2, b"n > 2t"), (9, 1, b"n <= 8"), (8, 1, b"HIM table")):
+        assert L.beaver32_create(n, t, ctypes.byref(ctx)) == _ffi.MOE_ERR_INVALID
+        assert msg in L.moe_last_error()
+    assert L.beaver32_generate(None, 1, None, None, None, None, None) == _ffi.MOE_ERR_INVALID
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is visible")
