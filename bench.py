@@ -621,6 +621,9 @@ def main():
     ap.add_argument("--no-graph", dest="graph", action="store_false")
     ap.add_argument("--no-fused", dest="fused", action="store_false",
                     help="single-token steps through the multi-kernel path")
+    ap.add_argument("--decode-mode", type=int, default=None, choices=(0, 1, 2),
+                    help="single-token path: 2 one launch (default), 1 two launches (bf16 MFMA on decoded "
+                         "weights), 0 the five-kernel batch path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--gemm-shape", type=int, default=0, choices=range(9), help="grouped GEMM block shape (tuning)")
@@ -635,6 +638,8 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
+    if args.decode_mode is not None:
+        args.fused = args.decode_mode if args.decode_mode != 2 else True
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "sharding of this path (expert parallel / row split) is a design note, not built.", file=sys.stderr)
