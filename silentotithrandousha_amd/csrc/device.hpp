@@ -859,10 +859,8 @@ __device__ __forceinline__ void rec_split_half(const float (&v)[16], int p, uint
   const int b = p >> 1, h = p & 1, st = b >> 2, i = b & 3;
 #pragma unroll
   for (int t = 0; t < kGemmTerms; t++) {
-    uint32_t *dst = reinterpret_cast<uint32_t *>(r + GemmRec::half(st, t, i, h));
-    dst[0] = d[t][0];
-    dst[1] = d[t][1];
-    dst[2] = d[t][2];
+#pragma unroll
+    for (int u = 0; u < 3; u++) *reinterpret_cast<uint32_t *>(r + GemmRec::dword(st, t, i, 3 * h + u)) = d[t][u];
   }
   if (h == 0) {
 #pragma unroll

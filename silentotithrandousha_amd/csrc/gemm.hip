@@ -27,9 +27,10 @@ using G = GemmRec;  // step-major activation record (kernels.hpp)
 // The batch path's activations are kGemmTerms E2M3 terms (exact to about 2^-13 of each block's
 // maximum, well inside the 1e-3 tolerance): the fp4 x fp6 MFMA issues in 16 cycles where fp4 x
 // fp8 takes 32, and a K-step of a record is 304 bytes instead of 400 for three fp8 terms.
-constexpr int kEntryStep = G::kStep;                // LDS bytes of one entry's K-step (a record step)
-static_assert(kEntryStep % 16 == 0, "entry stride: 16-byte aligned");
-constexpr int kChunks = kEntryStep / 16;            // 16-byte chunks per entry K-step (19)
+// B in LDS, per K-step: the entries' record steps one after the other (kEntryStep bytes each, as
+// the LDS-DMA copies them: each DMA reads whole record steps, a few rows per instruction).
+constexpr int kEntryStep = G::kStep;             // LDS bytes of one entry's K-step (a record step)
+constexpr int kChunks = G::kChunks;              // 16-byte chunks per entry K-step (19)
 
 // s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
 // outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima).
@@ -84,7 +85,16 @@ struct GemmShape {
   static constexpr bool kBStat = RT >= 16;
   static constexpr int kBufB = (kBStat ? kGroups : kDma * W) * 1024;
   static constexpr int kBufA = kTilesA * 1024;               // A chunks of one step
-  static constexpr int kBufS = kTilesA * 256;                // A-scale words of one step
+  // D = 2 (each step waits for all of its DMAs, so their number may vary): the A-scale words
+  // (one byte per step) go once per 4 steps into a pair of buffers outside the ring, and B
+  // pieces past kGroups are not loaded: 11 of the 64 KB a 512 x 64 step moved were such repeats
+  static constexpr bool kScale4 = !kBStat && D == 2;
+  // two steps in flight (operands read into registers, then the slot refilled), for column
+  // groups narrow enough to hold a step's operands
+  static constexpr bool kTwoAhead = kScale4 && CGW <= 2;
+  // DMA addresses as wavefront-uniform bases plus 32-bit lane offsets (fewer VGPRs)
+  static constexpr bool kSAddr = kBStat || kTwoAhead;
+  static constexpr int kBufS = kScale4 ? 0 : kTilesA * 256;  // A-scale words of one step
   static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
   static constexpr int kLds = D * kSlot;
   static constexpr int kIssue = kDma + 2 * kDmaA;            // VMEM operations per wavefront per step
@@ -97,47 +107,45 @@ struct GemmB {
   uint32_t sc[kGemmTerms];
 };
 
-// The same as one 16-byte and one 8-byte LDS read per term: the 24 bytes of lane group g start at
-// 24 g, so even groups read 16 + 8 and odd groups 8 + 16 bytes, the 16-byte part 16-byte aligned.
-// Eight lanes of one group read 16-byte parts 304 bytes apart (19 j mod 8 distinct), so the
-// 16-byte reads are free of bank conflicts.
+// Term t of lane (j, g) from entry j's record step at eb: the first 16 bytes of block g (chunk
+// 6t + g) and the last 8 (half g & 1 of chunk 6t + 4 + g / 2). Both are 16-byte reads (twice the
+// bytes per cycle of 8-byte reads): the pair chunk is read whole by both lanes of a pair, so 16
+// lanes share one address pair-wise and the reads of a 32-lane half have no bank conflicts; the
+// first-16-byte reads (records 304 bytes apart) take two passes where 8-byte reads took two each.
 __device__ __forceinline__ void gemm_read_b_t(GemmB &b, const uint8_t *eb, int g, int t) {
-  const uint8_t *q = eb + t * G::kTermBytes + 24 * g;
-  uint32_t d[6];
-  if ((g & 1) == 0) {
-    const uint4 x = *reinterpret_cast<const uint4 *>(q);
-    const uint2 y = *reinterpret_cast<const uint2 *>(q + 16);
-    d[0] = x.x; d[1] = x.y; d[2] = x.z; d[3] = x.w; d[4] = y.x; d[5] = y.y;
-  } else {
-    const uint2 y = *reinterpret_cast<const uint2 *>(q);
-    const uint4 x = *reinterpret_cast<const uint4 *>(q + 8);
-    d[0] = y.x; d[1] = y.y; d[2] = x.x; d[3] = x.y; d[4] = x.z; d[5] = x.w;
-  }
-  b.v[t] = i32x8{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], 0, 0};
+  const uint4 x = *reinterpret_cast<const uint4 *>(eb + (6 * t + g) * 16);
+  const uint4 y = *reinterpret_cast<const uint4 *>(eb + (6 * t + 4 + (g >> 1)) * 16);
+  const bool odd = (g & 1) != 0;
+  b.v[t] = i32x8{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)(odd ? y.z : y.x), (int)(odd ? y.w : y.y), 0, 0};
+}
+
+// The scale words of the terms (chunk kChunks - 1 of the record step; byte g is the lane's block).
+__device__ __forceinline__ void gemm_read_sc(GemmB &b, const uint8_t *eb, int g) {
+  static_assert(kGemmTerms == 3, "three scale words per chunk");
+  const uint4 sc = *reinterpret_cast<const uint4 *>(eb + (kChunks - 1) * 16);
+  b.sc[0] = sc.x >> (8 * g);
+  b.sc[1] = sc.y >> (8 * g);
+  b.sc[2] = sc.z >> (8 * g);
 }
 
 __device__ __forceinline__ void gemm_read_b(GemmB &b, const uint8_t *eb, int g) {
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-    const uint2 *q = reinterpret_cast<const uint2 *>(eb + t * G::kTermBytes + 24 * g);
-    const uint2 d0 = q[0], d1 = q[1], d2 = q[2];
-    b.v[t] = i32x8{(int)d0.x, (int)d0.y, (int)d1.x, (int)d1.y, (int)d2.x, (int)d2.y, 0, 0};
-    b.sc[t] = *reinterpret_cast<const uint32_t *>(eb + kGemmTerms * G::kTermBytes + 4 * t) >> (8 * g);
-  }
+  for (int t = 0; t < kGemmTerms; t++) gemm_read_b_t(b, eb, g, t);
+  gemm_read_sc(b, eb, g);
 }
 
 // MFMAs of one K-step for a wavefront: RT row tiles x CG column groups x kGemmTerms terms, all
-// operands from the step's ring slot; sh = 8 * (s % 4) selects the step's byte of the A-scale
-// words. The B operands of column group c + 1 are read while the MFMAs of group c run. Column
-// groups past the block's entries compute on repeated entries (not stored).
+// operands from the step's ring slot (sb: the step's A-scale words); sh = 8 * (s % 4) selects the
+// step's byte of them. The B operands of column group c + 1 are read while the MFMAs of group c
+// run. Column groups past the block's entries compute on repeated entries (not stored).
 template <int RT, int CGW, int WR, int WC, int D>
-__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *slot, int wr, int wc, int lane,
-                                          int sh) {
+__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *slot, const uint8_t *sb, int wr,
+                                          int wc, int lane, int sh) {
   using S = GemmShape<RT, CGW, WR, WC, D>;
   constexpr int CG = CGW;
   const int j = lane & 15, g = lane >> 4;
-  const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024,
-                *sb = slot + S::kBufB + S::kBufA + wr * RT * 256;
+  const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024;
+  sb += wr * RT * 256;
   uint4 ar[RT];
   uint32_t sw[RT];
 #pragma unroll
@@ -164,6 +172,101 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *
     __builtin_amdgcn_sched_barrier(0);
     if (c + 1 < CG) bc = bn;
   }
+}
+
+// All operands of one K-step for a wavefront (gemm_step's, read up front): the A chunks and scale
+// words of its RT row tiles and the B operands of its CG column groups.
+template <int RT, int CG>
+struct GemmOps {
+  uint4 ar[RT];
+  uint32_t sw[RT];
+  GemmB b[CG];
+};
+
+// One column group's B as read (both 16-byte chunks of each term, the scale chunk), before
+// gemm_read_b_t's half selection: reads issued early, selected once they are needed.
+struct GemmBRaw {
+  uint4 x[kGemmTerms], y[kGemmTerms], sc;
+};
+__device__ __forceinline__ void gemm_read_b_raw(GemmBRaw &b, const uint8_t *eb, int g) {
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    b.x[t] = *reinterpret_cast<const uint4 *>(eb + (6 * t + g) * 16);
+    b.y[t] = *reinterpret_cast<const uint4 *>(eb + (6 * t + 4 + (g >> 1)) * 16);
+  }
+  b.sc = *reinterpret_cast<const uint4 *>(eb + (kChunks - 1) * 16);
+}
+__device__ __forceinline__ void gemm_select_b(GemmB &b, const GemmBRaw &r, int g) {
+  static_assert(kGemmTerms == 3, "three scale words per chunk");
+  const bool odd = (g & 1) != 0;
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    const uint4 &x = r.x[t], &y = r.y[t];
+    b.v[t] = i32x8{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)(odd ? y.z : y.x), (int)(odd ? y.w : y.y), 0, 0};
+  }
+  b.sc[0] = r.sc.x >> (8 * g);
+  b.sc[1] = r.sc.y >> (8 * g);
+  b.sc[2] = r.sc.z >> (8 * g);
+}
+
+// The A operands and the B operands of column groups [0, C1) (selected); C1 < CGW: the later
+// groups are read with gemm_read_b_raw and selected by the caller.
+template <int RT, int CGW, int WR, int WC, int D, int C1 = CGW>
+__device__ __forceinline__ void gemm_read_ops(GemmOps<RT, CGW> &o, const uint8_t *slot, const uint8_t *sb, int wr,
+                                              int wc, int lane, int sh) {
+  using S = GemmShape<RT, CGW, WR, WC, D>;
+  const int j = lane & 15, g = lane >> 4;
+  const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024;
+  sb += wr * RT * 256;
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    o.ar[r] = *reinterpret_cast<const uint4 *>(ab + r * 1024 + 16 * lane);
+    o.sw[r] = *reinterpret_cast<const uint32_t *>(sb + r * 256 + 4 * lane) >> sh;
+  }
+#pragma unroll
+  for (int c = 0; c < C1; c++) gemm_read_b(o.b[c], bb + 16 * c * kEntryStep, g);
+}
+
+// The MFMAs of gemm_step for column groups [C0, C1) on operands already in registers (per output
+// the terms t = 0, 1, 2 in turn, as gemm_step, so both give the same bits), with dma(0) before
+// them (it may branch) and dma(1 .. NI - 1) spread over them (they must not branch, or the MFMAs
+// move out of order): the CU's memory pipeline accepts about 64 bytes per cycle, so issuing a
+// step's ~60 KB of LDS-DMA takes about as long as the MFMAs, which run meanwhile. The empty asm
+// at the end takes the groups' accumulators as operands, so their MFMAs stay before the barrier
+// that follows (the compiler otherwise moved them past it, where they ran after every other part
+// of the step).
+template <int RT, int CGW, int C0, int C1, int NI, typename F>
+__device__ __forceinline__ void gemm_mfma_ops(f32x4 (&acc)[RT][CGW], const GemmOps<RT, CGW> &o, F &&dma) {
+  constexpr int NM = (C1 - C0) * kGemmTerms * RT;
+  if constexpr (NI > 0) dma(0);
+  __builtin_amdgcn_sched_barrier(0);  // (a branch in dma(0) ends the block here)
+#pragma unroll
+  for (int c = C0; c < C1; c++) {
+#pragma unroll
+    for (int t = 0; t < kGemmTerms; t++) {
+#pragma unroll
+      for (int r = 0; r < RT; r++) {
+        const i32x8 A = {(int)o.ar[r].x, (int)o.ar[r].y, (int)o.ar[r].z, (int)o.ar[r].w, 0, 0, 0, 0};
+        // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
+        acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, o.b[c].v[t], acc[r][c], 4, 2, 0, (int)o.sw[r], 0,
+                                                                     (int)o.b[c].sc[t]);
+        const int m = ((c - C0) * kGemmTerms + t) * RT + r;
+#pragma unroll
+        for (int i = 1; i < NI; i++) {
+          if (m == (i * NM) / NI - 1) {
+            __builtin_amdgcn_sched_barrier(0);
+            dma(i);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int c = C0; c < C1; c++) asm volatile("" : "+v"(acc[r][c]));
 }
 
 // MFMAs of one K-step for a wavefront with many row tiles (one wavefront per SIMD): the B
@@ -196,12 +299,7 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
     for (int c = 0; c < CG; c++) gemm_read_b_t(b[c], bb + 16 * c * kEntryStep, g, t);
   }
 #pragma unroll
-  for (int c = 0; c < CG; c++) {
-    const uint4 sc = *reinterpret_cast<const uint4 *>(bb + 16 * c * kEntryStep + kGemmTerms * G::kTermBytes);
-    b[c].sc[0] = sc.x >> (8 * g);
-    b[c].sc[1] = sc.y >> (8 * g);
-    b[c].sc[2] = sc.z >> (8 * g);
-  }
+  for (int c = 0; c < CG; c++) gemm_read_sc(b[c], bb + 16 * c * kEntryStep, g);
 #pragma unroll
   for (int r = 0; r < RT; r += 2) {
     uint4 n0 = a0, n1 = a1;
@@ -245,6 +343,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   __shared__ __attribute__((aligned(1024))) uint8_t s_r0[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r1[S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_sc[2][S::kScale4 ? S::kTilesA * 256 : 16];
   constexpr int kBiasTiles = RT < 4 ? 4 : RT;  // the bias DMA moves 64 rows (4 tiles) per wavefront load
   // per wavefront: its rows' bias (the B-stationary shape reads its bias from global memory in the
   // epilogue, and its B pieces past the step's kGroups land in s_dummy)
@@ -339,15 +438,15 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   //      scale byte is 0 (the packer zero-fills them) while the B records hold zeros there, so
   //      it adds exact zeros. Every lane of every DMA runs, so each wavefront issues exactly
   //      kIssue VMEM operations per step, which the vmcnt waits count on.
-  const uint8_t *bsrc[S::kBStat ? 1 : S::kDma];
-  uint32_t boff[S::kBStat ? S::kDma : 1];  // B-stationary shape: offsets from a.brec (records < 4 GB)
+  const uint8_t *bsrc[S::kSAddr ? 1 : S::kDma];
+  uint32_t boff[S::kSAddr ? S::kDma : 1];  // offsets from a.brec (records < 4 GB)
 #pragma unroll
   for (int i = 0; i < S::kDma; i++) {
     const int c = min(64 * (W * i + wv) + lane, S::kStepChunks - 1);
     const int e = c / kChunks, part = c % kChunks;
     const int ge = beg + min(e, ncol - 1);
     const int row = a.entry_src ? a.entry_src[ge] : ge;
-    if constexpr (S::kBStat)
+    if constexpr (S::kSAddr)
       boff[i] = (uint32_t)row * (uint32_t)G::kBytes + 16u * part;
     else
       bsrc[i] = a.brec + (size_t)row * G::kBytes + 16 * part;
@@ -359,7 +458,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 #pragma unroll
   for (int i = 0; i < S::kDmaA; i++) {
     const int tl = min(tb + W * i + wvu, (int)d.tiles - 1);
-    if constexpr (S::kBStat) {  // tile bases (wavefront-uniform); the lane part is added per step
+    if constexpr (S::kSAddr) {  // tile bases (wavefront-uniform); the lane part is added per step
       asrc[i] = mat + (size_t)tl * 16 * d.nb * 16;
       ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256;
     } else {
@@ -367,8 +466,8 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256 + 4 * lane;
     }
   }
-  // B-stationary shape: the last 16-byte chunk of a tile (a lane's chunk past it, in the last
-  // step, is clamped into the tile: its scale byte is 0 and its B values are 0, so it adds 0)
+  // the last 16-byte chunk of a tile (with kSAddr, a lane's chunk past it, in the last step, is
+  // clamped into the tile: its scale byte is 0 and its B values are 0, so it adds 0)
   const uint32_t a_last = 16u * d.nb * 16u - 16u;
   bool tv[RT];
 #pragma unroll
@@ -389,20 +488,29 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                            \
       lds_dma4_s(so_, ssrc[i], (sl) + S::kBufB + S::kBufA + (W * i + wvu) * 256);                  \
   } while (0)
-#define GEMM_LOAD(step, sl)                                                                         \
+// fresh: step is the next step to load (not the repeat of the last one past the end)
+#define GEMM_LOAD(step, sl, fresh)                                                                  \
   do {                                                                                              \
     if constexpr (S::kBStat) {                                                                      \
       GEMM_LOAD_S(step, sl);                                                                        \
-    } else {                                                                                        \
+    } else if constexpr (!S::kTwoAhead) {                                                           \
       _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                         \
-        lds_dma16(bsrc[S::kBStat ? 0 : i] + (size_t)(step) * G::kStep, (sl) + 1024 * (W * i + wv)); \
+        if (!S::kScale4 || W * i + wvu < S::kGroups)                                                \
+          lds_dma16(bsrc[S::kSAddr ? 0 : i] + (size_t)(step) * G::kStep, (sl) + 1024 * (W * i + wv)); \
       }                                                                                             \
       _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++) {                                        \
         const uint8_t *src = asrc[i] + (size_t)(step) * 1024 + 16 * lane;                           \
         lds_dma16(src < alast ? src : alast, (sl) + S::kBufB + (W * i + wv) * 1024);                \
       }                                                                                             \
-      _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                          \
-        lds_dma4(ssrc[i] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (W * i + wv) * 256); \
+      if constexpr (S::kScale4) {                                                                   \
+        if ((fresh) && ((step) & 3) == 0) {                                                         \
+          _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                      \
+            lds_dma4(ssrc[i] + (size_t)((step) >> 2) * 256, s_sc[((step) >> 2) & 1] + (W * i + wv) * 256); \
+        }                                                                                           \
+      } else {                                                                                      \
+        _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                        \
+          lds_dma4(ssrc[i] + (size_t)((step) >> 2) * 256, (sl) + S::kBufB + S::kBufA + (W * i + wv) * 256); \
+      }                                                                                             \
     }                                                                                               \
   } while (0)
 
@@ -432,19 +540,106 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 #define GEMM_STEP(st, cur, nxt)                                                                     \
   do {                                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                              \
-    GEMM_LOAD(min((st) + D - 1, ns - 1), nxt);                                                      \
+    GEMM_LOAD(min((st) + D - 1, ns - 1), nxt, (st) + D - 1 < ns);                                   \
     if constexpr (S::kBStat)                                                                        \
       gemm_step_bstat<RT, CGW, WR, WC, D, false>(acc, cur, wr, wc, lane, 8 * ((st) & 3), nrt_valid); \
     else                                                                                            \
-      gemm_step<RT, CGW, WR, WC, D>(acc, cur, wr, wc, lane, 8 * ((st) & 3));                        \
+      gemm_step<RT, CGW, WR, WC, D>(acc, cur, S::kScale4 ? s_sc[((st) >> 2) & 1] : (cur) + S::kBufB + S::kBufA, \
+                                    wr, wc, lane, 8 * ((st) & 3));                                  \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));                                  \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
     __builtin_amdgcn_s_barrier();                                                                   \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
   } while (0)
-  GEMM_LOAD(0, s_r0);
-  if (D == 3) GEMM_LOAD(min(1, ns - 1), s_r1);
+  if constexpr (S::kTwoAhead) {
+    // ---- two steps in flight in the 2-slot ring: step s reads all of its operands from slot
+    //      s % 2 into registers, a barrier frees the slot, the slot receives the DMA of step
+    //      s + 2 while the MFMAs of step s run, and the step ends when this wavefront's DMA of
+    //      step s + 1 is complete (then a barrier: slot (s + 1) % 2 is whole). A step's loads miss
+    //      the L2 often enough that one step of prefetch left every step waiting for a miss.
+    //      The DMAs of a step, per wavefront: nb B pieces (kDma, or kDma - 1 for the wavefronts
+    //      past the step's kGroups pieces), kDmaA A tiles, and kDmaA scale words every 4 steps.
+    static_assert(W * (S::kDma - 1) < S::kGroups, "only the last B piece can fall past the step");
+    constexpr int kCSplit = CGW / 2;  // column groups computed before the slot is released
+    const bool fullb = W * (S::kDma - 1) + wvu < S::kGroups;
+    // DMA k of step ld into ring slot sl: 0 = the last B piece (only wavefronts inside kGroups),
+    // 1 .. kDma - 1 = the other B pieces, then the A tiles, then the A-scale words (issued only
+    // for steps that are multiples of 4, into s_sc)
+    auto dma2 = [&](int k, int ld, uint8_t *sl) {
+      if (k == 0) {
+        if (fullb) lds_dma16_s(boff[S::kDma - 1], a.brec + (size_t)ld * G::kStep, sl + 1024 * (W * (S::kDma - 1) + wvu));
+      } else if (k < S::kDma) {
+        lds_dma16_s(boff[(k - 1) % S::kDma], a.brec + (size_t)ld * G::kStep, sl + 1024 * (W * (k - 1) + wvu));
+      } else if (k < S::kDma + S::kDmaA) {
+        const int i = (k - S::kDma) % S::kDmaA;
+        lds_dma16_s(min((uint32_t)ld * 1024u + 16u * lane, a_last), asrc[i], sl + S::kBufB + (W * i + wvu) * 1024);
+      } else {
+        const int i = (k - S::kDma - S::kDmaA) % S::kDmaA;
+        lds_dma4_s((uint32_t)(ld >> 2) * 256u + 4u * lane, ssrc[i], s_sc[(ld >> 2) & 1] + (W * i + wvu) * 256);
+      }
+    };
+#define GEMM_VM_WAIT(extra)                                                                         \
+  do {                                                                                              \
+    if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + (extra)));                         \
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + (extra)));                           \
+  } while (0)
+#define GEMM_BARRIER()                                                                              \
+  do {                                                                                              \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
+    __builtin_amdgcn_s_barrier();                                                                   \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
+  } while (0)
+#define GEMM_STEP2(st, cur, jj)                                                                     \
+  do {                                                                                              \
+    GemmOps<RT, CGW> ops_;                                                                          \
+    gemm_read_ops<RT, CGW, WR, WC, D, kCSplit>(ops_, cur, s_sc[((st) >> 2) & 1], wr, wc, lane, 8 * (jj)); \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    /* the first column groups' MFMAs run while the other groups' operands arrive */               \
+    GemmBRaw raw_[CGW - kCSplit];                                                                   \
+    _Pragma("unroll") for (int c_ = kCSplit; c_ < CGW; c_++)                                        \
+      gemm_read_b_raw(raw_[c_ - kCSplit], cur + (16 * CGW * wc + (lane & 15) + 16 * c_) * kEntryStep, lane >> 4); \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    gemm_mfma_ops<RT, CGW, 0, kCSplit, 0>(acc, ops_, [](int) {});                                   \
+    _Pragma("unroll") for (int c_ = kCSplit; c_ < CGW; c_++)                                        \
+      gemm_select_b(ops_.b[c_], raw_[c_ - kCSplit], lane >> 4);                                     \
+    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));                                                   \
+    GEMM_BARRIER();                                                                                 \
+    const int ld_ = (st) + 2;                                                                       \
+    auto dma_ = [&](int k_) { dma2(k_, ld_, cur); };                                                \
+    if ((st) + 2 < ns)                                                                              \
+      gemm_mfma_ops<RT, CGW, kCSplit, CGW, S::kDma + S::kDmaA + ((jj) == 2 ? S::kDmaA : 0)>(acc, ops_, dma_); \
+    else                                                                                            \
+      gemm_mfma_ops<RT, CGW, kCSplit, CGW, 0>(acc, ops_, dma_);                                     \
+    const bool more_ = (st) + 2 < ns;                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    if (more_) GEMM_VM_WAIT(S::kDmaA + ((jj) == 2 ? S::kDmaA : 0));                                 \
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));                                               \
+    GEMM_BARRIER();                                                                                 \
+  } while (0)
+    constexpr int kAll = S::kDma + 2 * S::kDmaA;  // the DMAs of a step whose scale words load
+#pragma unroll
+    for (int k = 0; k < kAll; k++) dma2(k, 0, s_r0);
+    if (ns > 1) {
+#pragma unroll
+      for (int k = 0; k < kAll - S::kDmaA; k++) dma2(k, 1, s_r1);
+      GEMM_VM_WAIT(S::kDmaA);
+    } else {
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+    }
+    GEMM_BARRIER();
+    for (int s = 0; s < ns; s += 4) {
+      GEMM_STEP2(s, s_r0, 0);
+      if (s + 1 < ns) GEMM_STEP2(s + 1, s_r1, 1);
+      if (s + 2 < ns) GEMM_STEP2(s + 2, s_r0, 2);
+      if (s + 3 < ns) GEMM_STEP2(s + 3, s_r1, 3);
+    }
+#undef GEMM_STEP2
+#undef GEMM_BARRIER
+#undef GEMM_VM_WAIT
+  } else {
+  GEMM_LOAD(0, s_r0, true);
+  if (D == 3) GEMM_LOAD(min(1, ns - 1), s_r1, true);
   __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
@@ -460,6 +655,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       if (s + 1 < ns) GEMM_STEP(s + 1, s_r1, s_r0);
       if (s + 2 < ns) GEMM_STEP(s + 2, s_r2, s_r1);
     }
+  }
   }
 #undef GEMM_STEP
 #undef GEMM_LOAD
@@ -539,10 +735,8 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
           uint8_t *hr = hout + (size_t)(beg + e0 + e) * G::kBytes;
 #pragma unroll
           for (int t = 0; t < kGemmTerms; t++) {
-            uint32_t *dst = reinterpret_cast<uint32_t *>(hr + G::half(st, t, i, h));
-            dst[0] = dq[t][0];
-            dst[1] = dq[t][1];
-            dst[2] = dq[t][2];
+#pragma unroll
+            for (int u = 0; u < 3; u++) *reinterpret_cast<uint32_t *>(hr + G::dword(st, t, i, 3 * h + u)) = dq[t][u];
           }
           if (h == 0) {
 #pragma unroll

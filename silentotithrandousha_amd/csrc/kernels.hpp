@@ -51,22 +51,28 @@ struct GemvArgs {
 constexpr int kTerms = 4;
 
 // Step-major activation record of one row (token or entry) for the grouped GEMM (gemm.hip):
-// kGemmTerms fp6 (E2M3) terms per value, rows of up to 4 * kGemmNs 32-value blocks. K-step s
-// holds, per term t, 96 bytes in MFMA B-operand order: block 4s + b at 24 b, value u of the block
-// at bits 6u (the 6 dwords lane group b of the fp6 MFMA operand takes: K = 32 b + u); then
-// [term t][4 scale bytes, byte i = E8M0 of block 4s+i] (12 bytes) and 4 pad bytes. Blocks past
-// the row are zero.
+// kGemmTerms fp6 (E2M3) terms per value, rows of up to 4 * kGemmNs 32-value blocks. The B operand
+// of block 4s + b (b = 0..3, the MFMA lane group b: K = 32 b + u, value u at bits 6u) is 6 dwords;
+// K-step s holds, per term t, 96 bytes: dwords 0-3 of blocks 0..3 (16 bytes each, block b at 16 b),
+// then dwords 4-5 of blocks 0..3 (8 bytes each, at 64 + 8 b); then [term t][4 scale bytes, byte
+// i = E8M0 of block 4s+i] (12 bytes) and 4 pad bytes. A step is kChunks 16-byte chunks: chunk
+// 6t + b = the first 16 bytes of block b, chunk 6t + 4 + (b >> 1) = the last 8 bytes of blocks b
+// and b ^ 1, chunk 18 = the scales (the grouped GEMM stages them chunk by chunk). Blocks past the
+// row are zero.
 constexpr int kGemmNs = 24;
 constexpr int kGemmTerms = 3;
 struct GemmRec {
   static constexpr int kTermBytes = 96;
   static constexpr int kStep = kGemmTerms * kTermBytes + 16;
+  static constexpr int kChunks = kStep / 16;
   static constexpr int kBytes = kGemmNs * kStep;
-  MOE_HD static constexpr int data(int s, int t) { return s * kStep + t * kTermBytes; }
-  // byte offset of the 12-byte half h (values 16h .. 16h + 15) of block b (0..3) of step s, term t
-  MOE_HD static constexpr int half(int s, int t, int b, int h) { return data(s, t) + 24 * b + 12 * h; }
+  // byte offset of dword d (0..5) of the B operand of block b (0..3) of step s, term t
+  MOE_HD static constexpr int dword(int s, int t, int b, int d) {
+    return s * kStep + t * kTermBytes + (d < 4 ? 16 * b + 4 * d : 64 + 8 * b + 4 * (d - 4));
+  }
   MOE_HD static constexpr int scale(int s, int t) { return s * kStep + kGemmTerms * kTermBytes + 4 * t; }
 };
+static_assert(GemmRec::kStep % 16 == 0 && GemmRec::kChunks == 6 * kGemmTerms + 1, "record chunks");
 
 struct GemmArgs {
   const uint8_t *base;       // expert records of the layer
