@@ -361,11 +361,16 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   //      tile by column tile. The orders differ by a few percent, by matrix (measured).
   //      Wavefront 0 finds the expert of tile cl: lanes read 64 experts' entry ranges at once,
   //      a prefix sum of their tile counts places cl.
+  // Workgroup p of the launch's a.n_blocks: the two-ahead shapes run a persistent grid (one
+  // workgroup per CU, each taking p = blockIdx.x, + gridDim.x, ...: the same XCD for every p,
+  // p % 8); the others one workgroup per p.
+  for (int p = (int)blockIdx.x; p < a.n_blocks; p += S::kTwoAhead ? (int)gridDim.x : a.n_blocks) {
+  if (p != (int)blockIdx.x) __syncthreads();  // the previous tile's LDS reads are done
   int cl, rblk_l;
   {
     const int C = (a.n_tiles + 7) / 8;
-    const int L = a.band ? ((int)blockIdx.x % 8) * C + (int)blockIdx.x / 8 : (int)blockIdx.x;
-    if (L >= a.n_tiles) return;
+    const int L = a.band ? (p % 8) * C + p / 8 : p;
+    if (L >= a.n_tiles) continue;
     const int nrb = a.n_row_blocks, nct = a.n_tiles / nrb, RB = a.band ? min(a.band, nrb) : nrb, full = nrb / RB;
     if (L < full * RB * nct) {
       const int band = L / (RB * nct), r = L - band * RB * nct;
@@ -421,7 +426,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   // block-uniform (read from LDS, so made scalar explicitly: the bounds below then branch on SGPRs)
   const int ex = __builtin_amdgcn_readfirstlane(s_tile[0]), beg = __builtin_amdgcn_readfirstlane(s_tile[1]),
             ncol = __builtin_amdgcn_readfirstlane(s_tile[2]);
-  if (ex < 0) return;
+  if (ex < 0) continue;
   const int rblk = __builtin_amdgcn_readfirstlane(s_tile[3]);
   const int tb = rblk * S::kRows / 16;  // first 16-row tile of the block
   const int t0 = tb + wr * RT;           // first 16-row tile of the wavefront
@@ -767,6 +772,20 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       }
     }
   }
+  }  // workgroup p
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+    cus[dev] = n / 8 * 8;
+  }
+  return cus[dev];
 }
 
 template <int MODE, int RT, int CGW, int WR, int WC, int D>
@@ -780,7 +799,10 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   if (tiles > (size_t)INT32_MAX - 8) return hipErrorInvalidValue;
   a.n_tiles = (int)tiles;
   const size_t blocks = a.band ? (tiles + 7) / 8 * 8 : tiles;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D>), dim3((unsigned)blocks), dim3(S::kThreads), 0, s, a);
+  a.n_blocks = (int)blocks;
+  // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
+  const size_t grid = S::kTwoAhead ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 

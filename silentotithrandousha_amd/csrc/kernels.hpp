@@ -89,6 +89,7 @@ struct GemmArgs {
   int band;                  // row blocks per band of the XCD-local tile order (0: workgroup order)
   int n_row_blocks;          // set by launch_gemm_fp8: row blocks of the launch
   int n_tiles;               //                         row blocks x column tiles
+  int n_blocks;              //                         workgroups of the tile order (>= n_tiles)
 };
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
 
