@@ -840,6 +840,41 @@ __device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool 
 }
 
 
+// split16_fp6 for a whole 32-value block in one lane (x[u] = value u, m = its maximum |x|): the
+// conversions take all 32 values at once, and term t's codes are the 6 dwords of the block's
+// B operand (value u at bits 6u). Same codes and scales as two split16_fp6 halves.
+__device__ __forceinline__ void split32_fp6(const float (&x)[32], float m, bool bad, uint32_t (&d)[kGemmTerms][6],
+                                            uint32_t &sb) {
+  int E = 0;
+  if (m > 0.0f && isfinite(m)) frexpf(m, &E);
+  float r[32];
+#pragma unroll
+  for (int i = 0; i < 32; i++) r[i] = bad ? 0.0f : x[i];
+  sb = 0;
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    const int se = max(E - 2 - 5 * t, -126);
+    sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
+    const float sc = __builtin_amdgcn_ldexpf(1.0f, se);
+    f32x16v a, b;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      a[i] = r[2 * i];
+      b[i] = r[2 * i + 1];
+    }
+    u32x6v c;
+    asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(c) : "v"(a), "v"(b), "v"(sc));
+#pragma unroll
+    for (int k = 0; k < 6; k++) d[t][k] = c[k];
+    if (t + 1 < kGemmTerms) {  // the residual feeds the next term (the last term needs none)
+      f32x32v q;
+      asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
+#pragma unroll
+      for (int i = 0; i < 32; i++) r[i] = r[i] - q[i];
+    }
+  }
+}
+
 // Thread p (< 8 kGemmNs writes; every lane of the pair must run it) of a row's split: half
 // p & 1 (values 16 h .. 16 h + 15) of 32-value block p >> 1, given in v, into the row's GemmRec
 // record r: the kGemmTerms E2M3 terms of the half (block maximum and finiteness shared with the

@@ -334,6 +334,10 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
   }
 }
 
+// The shapes that run a persistent grid.
+template <int MODE, typename S>
+constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP; }
+
 template <int MODE, int RT, int CGW, int WR, int WC, int D>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
   using S = GemmShape<RT, CGW, WR, WC, D>;
@@ -361,16 +365,20 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   //      tile by column tile. The orders differ by a few percent, by matrix (measured).
   //      Wavefront 0 finds the expert of tile cl: lanes read 64 experts' entry ranges at once,
   //      a prefix sum of their tile counts places cl.
-  // Workgroup p of the launch's a.n_blocks: the two-ahead shapes run a persistent grid (one
-  // workgroup per CU, each taking p = blockIdx.x, + gridDim.x, ...: the same XCD for every p,
-  // p % 8); the others one workgroup per p.
-  for (int p = (int)blockIdx.x; p < a.n_blocks; p += S::kTwoAhead ? (int)gridDim.x : a.n_blocks) {
+  // Workgroup p of the launch's a.n_blocks: the two-ahead gate_up shape runs a persistent grid
+  // (one workgroup per CU, each taking p = blockIdx.x, + gridDim.x, ...: the same XCD for every
+  // p, p % 8); the others one workgroup per p (for the down shape the loop cost 8 %, measured).
+  constexpr bool kPersist = gemm_persistent<MODE, S>();
+  for (int p = (int)blockIdx.x; p < a.n_blocks; p += (int)gridDim.x) {
   if (p != (int)blockIdx.x) __syncthreads();  // the previous tile's LDS reads are done
   int cl, rblk_l;
   {
     const int C = (a.n_tiles + 7) / 8;
     const int L = a.band ? (p % 8) * C + p / 8 : p;
-    if (L >= a.n_tiles) continue;
+    if (L >= a.n_tiles) {
+      if constexpr (kPersist) continue;
+      else return;
+    }
     const int nrb = a.n_row_blocks, nct = a.n_tiles / nrb, RB = a.band ? min(a.band, nrb) : nrb, full = nrb / RB;
     if (L < full * RB * nct) {
       const int band = L / (RB * nct), r = L - band * RB * nct;
@@ -426,7 +434,10 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   // block-uniform (read from LDS, so made scalar explicitly: the bounds below then branch on SGPRs)
   const int ex = __builtin_amdgcn_readfirstlane(s_tile[0]), beg = __builtin_amdgcn_readfirstlane(s_tile[1]),
             ncol = __builtin_amdgcn_readfirstlane(s_tile[2]);
-  if (ex < 0) continue;
+  if (ex < 0) {
+    if constexpr (kPersist) continue;
+    else return;
+  }
   const int rblk = __builtin_amdgcn_readfirstlane(s_tile[3]);
   const int tb = rblk * S::kRows / 16;  // first 16-row tile of the block
   const int t0 = tb + wr * RT;           // first 16-row tile of the wavefront
@@ -694,9 +705,71 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
     uint8_t *hout = reinterpret_cast<uint8_t *>(a.out);
-    float *stage = reinterpret_cast<float *>((wv < 4 ? s_r0 : s_r1) + (wv & 3) * kWaveCols * 128);
     const int e0 = kWaveCols * wc;                                     // first entry of the wavefront
     const int nloc = max(0, min(kWaveCols, ncol - e0));                // its entries in the tile
+    // All of the wavefront's h blocks staged at once when they fit (rows of 36 floats: the
+    // 16-byte reads of 16 consecutive rows then hit distinct banks), then one lane per (h block,
+    // entry) splits the whole 32-value block (split32_fp6: a third fewer instructions than two
+    // 16-value halves) and stores each term's 24 bytes as one 16- and one 8-byte store.
+    constexpr int NHB = RT / 4;                        // h blocks of the wavefront
+    constexpr int kRow = 36;                           // staging row stride (floats)
+    constexpr int kStageW = NHB * kWaveCols * kRow * 4;  // staging bytes per wavefront
+    constexpr int kHalf = W > 1 ? W / 2 : 1;           // wavefronts per ring slot
+    if constexpr (kHalf * kStageW <= S::kSlot && NHB * kWaveCols <= 64) {  // one lane pass
+      float *st32 = reinterpret_cast<float *>((wv < kHalf ? s_r0 : s_r1) + (wv % kHalf) * kStageW);
+#pragma unroll
+      for (int hbk = 0; hbk < NHB; hbk++) {
+        if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
+#pragma unroll
+        for (int c = 0; c < CG; c++) {
+          if (16 * c >= nloc) break;
+          float *se = st32 + (hbk * kWaveCols + 16 * c + j) * kRow;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {  // h values 8r + 2g, 8r + 2g + 1 of the block
+            const f32x4 &av = acc[4 * hbk + r][c];
+            const float4 &b4 = bv[4 * hbk + r];
+            *reinterpret_cast<float2 *>(se + 8 * r + 2 * g) =
+                make_float2(swiglu_fast(av[0] + b4.x, av[1] + b4.y, a.limit), swiglu_fast(av[2] + b4.z, av[3] + b4.w, a.limit));
+          }
+        }
+      }
+      constexpr int kPairs = NHB * kWaveCols;
+#pragma unroll
+      for (int pass = 0; pass < (kPairs + 63) / 64; pass++) {
+        const int idx = 64 * pass + lane, hbk = min(idx / kWaveCols, NHB - 1), e = idx % kWaveCols;
+        const bool valid = idx < kPairs && tv[4 * hbk] && e < nloc;
+        const float *row = st32 + (valid ? hbk * kWaveCols + e : 0) * kRow;
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const float4 x = *reinterpret_cast<const float4 *>(row + 4 * q);
+          v[4 * q] = x.x;
+          v[4 * q + 1] = x.y;
+          v[4 * q + 2] = x.z;
+          v[4 * q + 3] = x.w;
+        }
+        float m = 0.0f;
+        bool bad = false;
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+          m = fmaxf(m, fabsf(v[k]));
+          bad = bad || !isfinite(v[k]);
+        }
+        uint32_t dq[kGemmTerms][6], sb;
+        split32_fp6(v, m, bad, dq, sb);
+        if (valid) {
+          const int hb = t0 / 4 + hbk, st = hb >> 2, i = hb & 3;
+          uint8_t *hr = hout + (size_t)(beg + e0 + e) * G::kBytes;
+#pragma unroll
+          for (int t = 0; t < kGemmTerms; t++) {
+            *reinterpret_cast<uint4 *>(hr + G::dword(st, t, i, 0)) = make_uint4(dq[t][0], dq[t][1], dq[t][2], dq[t][3]);
+            *reinterpret_cast<uint2 *>(hr + G::dword(st, t, i, 4)) = make_uint2(dq[t][4], dq[t][5]);
+            hr[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+          }
+        }
+      }
+    } else {
+    float *stage = reinterpret_cast<float *>((wv < 4 ? s_r0 : s_r1) + (wv & 3) * kWaveCols * 128);
 #pragma unroll
     for (int hbk = 0; hbk < RT / 4; hbk++) {
       if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
@@ -751,6 +824,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       }
       __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));  // staging reads done before the next h block
     }
+    }
   } else {
     float *out = reinterpret_cast<float *>(a.out);
     const int R = (int)d.rows;
@@ -772,6 +846,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       }
     }
   }
+    if constexpr (!kPersist) break;  // (no loop at all in the other shapes' code)
   }  // workgroup p
 }
 
@@ -801,7 +876,7 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   const size_t blocks = a.band ? (tiles + 7) / 8 * 8 : tiles;
   a.n_blocks = (int)blocks;
   // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
-  const size_t grid = S::kTwoAhead ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
+  const size_t grid = gemm_persistent<MODE, S>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
   hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
