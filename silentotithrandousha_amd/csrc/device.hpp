@@ -903,6 +903,27 @@ __device__ __forceinline__ void rec_split_half(const float (&v)[16], int p, uint
   }
 }
 
+// Block blk (values 32 blk .. 32 blk + 31, in v; 0 <= blk < 4 kGemmNs) of a row into the row's
+// GemmRec record r: one lane per block (split32_fp6), the same bytes as rec_split_half's pair.
+__device__ __forceinline__ void rec_split_block(const float (&v)[32], int blk, uint8_t *r) {
+  float m = 0.0f;
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    m = fmaxf(m, fabsf(v[i]));
+    bad = bad || !isfinite(v[i]);
+  }
+  uint32_t d[kGemmTerms][6], sb;
+  split32_fp6(v, m, bad, d, sb);
+  const int st = blk >> 2, i = blk & 3;
+#pragma unroll
+  for (int t = 0; t < kGemmTerms; t++) {
+    *reinterpret_cast<uint4 *>(r + GemmRec::dword(st, t, i, 0)) = make_uint4(d[t][0], d[t][1], d[t][2], d[t][3]);
+    *reinterpret_cast<uint2 *>(r + GemmRec::dword(st, t, i, 4)) = make_uint2(d[t][4], d[t][5]);
+    r[GemmRec::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+  }
+}
+
 // tile_mfma_f8 over steps [s0, s0 + NS) of a tile whose chunks for those steps are in raw[] (zeros
 // past the tile) and whose scale words are all in sw[]; rec, bsw as for tile_mfma_f8. One
 // accumulator: a quarter of a tile's steps is a short chain.

@@ -28,6 +28,38 @@ namespace moe {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteTokens = 8;  // tokens per block for large batches: the router weights load once per block
 
+// Wavefront 0 of a block: from the per-expert entry counts cnt[0..E), the active experts in
+// ascending id (active_ids, active_off, *n_active; the entries of active expert i are
+// [active_off[i], active_off[i + 1])) and every expert's first entry base[e], by wave prefix
+// sums over 64 experts at a time.
+__device__ __forceinline__ void expert_list_wave(const int *cnt, int E, int lane, int *base, int32_t *active_ids,
+                                                 int32_t *active_off, int32_t *n_active) {
+  int off = 0, na = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e < E ? cnt[e] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o);
+      if (lane >= o) incl += u;
+    }
+    const uint64_t act = __ballot(c > 0);
+    const int slot = na + __popcll(act & ((1ull << lane) - 1ull));
+    if (e < E) base[e] = off + incl - c;
+    if (c > 0) {
+      active_ids[slot] = e;
+      active_off[slot] = off + incl - c;
+    }
+    off += __shfl(incl, 63);
+    na += __popcll(act);
+  }
+  if (lane == 0) {
+    active_off[na] = off;
+    *n_active = na;
+  }
+}
+
 // Groups the T*k (token, slot) entries by expert, in one block of 1024 threads. Active
 // experts are listed in ascending id; entries of one expert are ordered by t*k + slot.
 // pos[t*k + slot] = entry index (or -1). LDS: s_count[E], s_base[E], s_wave[16][E].
@@ -53,20 +85,7 @@ __device__ __forceinline__ void bucket_block(const int32_t *idx, int T, int k, i
       if (ev[i] >= 0) atomicAdd(&s_count[ev[i]], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int na = 0, off = 0;
-    for (int e = 0; e < E; e++) {
-      s_base[e] = off;
-      if (s_count[e] > 0) {
-        active_ids[na] = e;
-        active_off[na] = off;
-        off += s_count[e];
-        na++;
-      }
-    }
-    active_off[na] = off;
-    *n_active = na;
-  }
+  if (wv == 0) expert_list_wave(s_count, E, lane, s_base, active_ids, active_off, n_active);
   __syncthreads();
   int e_next = tid < N ? ld_idx(tid) : -1;
   for (int c0 = 0; c0 < N; c0 += 1024) {
@@ -137,9 +156,10 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
   const int nq = ((H + 63) / 64 + 7) / 8;  // uint4 per lane chain
   const int Hp = route_hp(H);
   extern __shared__ float s_x[];  // TB * Hp floats
-  // the wavefront's first expert's weights, in flight while x is staged (then one expert ahead)
+  // one token per block: the weights of the wavefront's first expert, in flight while x is
+  // staged (with 8 tokens they would stay live through the records' split and spill)
   uint4 v[KI > 0 ? KI : 1];
-  if (KI > 0 && wv < E) {
+  if (KI > 0 && TB == 1 && wv < E) {
     const uint4 *wq = reinterpret_cast<const uint4 *>(a.w + (size_t)wv * nq * 512) + lane;
 #pragma unroll
     for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
@@ -178,46 +198,64 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
       for (int k = threadIdx.x; k < Hp; k += kRouteThreads) stage(tb, k, k < H ? a.x[(size_t)(t0 + tb) * H + k] : 0.0f);
   }
   __syncthreads();
-  if (a.xrec) {  // the grouped GEMM's activation records of the block's tokens (rec_split_half)
-    for (int u = threadIdx.x; u < nt * 256; u += kRouteThreads) {  // whole wavefronts
-      const int tb = u >> 8, p = u & 255, k0 = 32 * (p >> 1) + 16 * (p & 1);
+  if (a.xrec) {  // the grouped GEMM's activation records of the block's tokens: a lane per block
+    constexpr int kRecBlocks = 4 * kGemmNs;
+    for (int u = threadIdx.x; u < nt * kRecBlocks; u += kRouteThreads) {
+      const int tb = u / kRecBlocks, blk = u - tb * kRecBlocks, k0 = 32 * blk;
       const float *xt = s_x + tb * Hp;
-      float xv[16];
+      float xv[32];
 #pragma unroll
-      for (int i = 0; i < 16; i++) xv[i] = p < 8 * kGemmNs && k0 + i < H ? xt[k0 + i] : 0.0f;
-      rec_split_half(xv, p, a.xrec + (size_t)(t0 + tb) * GemmRec::kBytes);
+      for (int q = 0; q < 8; q++) {  // the staging row holds zeros from H to Hp; 16-byte reads there
+        const float4 x4 = k0 + 4 * q + 3 < Hp ? *reinterpret_cast<const float4 *>(xt + k0 + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[4 * q] = k0 + 4 * q < H ? x4.x : 0.0f;
+        xv[4 * q + 1] = k0 + 4 * q + 1 < H ? x4.y : 0.0f;
+        xv[4 * q + 2] = k0 + 4 * q + 2 < H ? x4.z : 0.0f;
+        xv[4 * q + 3] = k0 + 4 * q + 3 < H ? x4.w : 0.0f;
+      }
+      rec_split_block(xv, blk, a.xrec + (size_t)(t0 + tb) * GemmRec::kBytes);
     }
   }
-  for (int e = wv; e < E; e += nw) {
-    const uint16_t *w_e = a.w + (size_t)e * nq * 512;
-    if (KI > 0) {
-      uint4 cur[KI > 0 ? KI : 1];
+  if constexpr (KI > 0) {
+    // experts in pairs (e, e + nw): each x value is read from LDS once for both chains (the
+    // reads, not the FMAs, bound this loop); each chain keeps router_dot's order
+    for (int e = wv; e < E; e += 2 * nw) {
+      const int e1 = e + nw;
+      uint4 wa[KI], wb[KI];
+      const uint4 *qa = reinterpret_cast<const uint4 *>(a.w + (size_t)e * nq * 512) + lane;
+      const uint4 *qb = reinterpret_cast<const uint4 *>(a.w + (size_t)min(e1, E - 1) * nq * 512) + lane;
 #pragma unroll
-      for (int q = 0; q < KI; q++) cur[q] = v[q];
-      if (e + nw < E) {  // the next expert's weights load during this one's dot products
-        const uint4 *wq = reinterpret_cast<const uint4 *>(a.w + (size_t)(e + nw) * nq * 512) + lane;
-#pragma unroll
-        for (int q = 0; q < KI; q++) v[q] = wq[q * 64];
+      for (int q = 0; q < KI; q++) {
+        wa[q] = TB == 1 && e == wv ? v[q] : qa[q * 64];  // (the first expert's loaded at the start)
+        wb[q] = qb[q * 64];
       }
-#pragma unroll
-      for (int tb = 0; tb < TB; tb++) {
-        if (tb < nt) {
+#pragma unroll 1
+      for (int tb = 0; tb < nt; tb++) {  // (one token at a time: the chains' registers fit)
+        {
           const float *xt = s_x + tb * Hp;
-          float p = 0.0f;
+          float pa = 0.0f, pb = 0.0f;
 #pragma unroll
           for (int q = 0; q < KI; q++) {
-            const uint32_t u[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+            const uint32_t ua[4] = {wa[q].x, wa[q].y, wa[q].z, wa[q].w};
+            const uint32_t ub[4] = {wb[q].x, wb[q].y, wb[q].z, wb[q].w};
 #pragma unroll
             for (int h = 0; h < 8; h++) {
-              const uint16_t bw = (uint16_t)(u[h >> 1] >> (16 * (h & 1)));
-              p = __builtin_fmaf(bf16_to_f32(bw), xt[lane + 64 * (8 * q + h)], p);
+              const float xv = xt[lane + 64 * (8 * q + h)];
+              pa = __builtin_fmaf(bf16_to_f32((uint16_t)(ua[h >> 1] >> (16 * (h & 1)))), xv, pa);
+              pb = __builtin_fmaf(bf16_to_f32((uint16_t)(ub[h >> 1] >> (16 * (h & 1)))), xv, pb);
             }
           }
-          p = wave_sum_xor(p);
-          if (lane == 0) s_logit[tb][e] = canon_nan(p + a.bias[e]);
+          pa = wave_sum_xor(pa);
+          pb = wave_sum_xor(pb);
+          if (lane == 0) {
+            s_logit[tb][e] = canon_nan(pa + a.bias[e]);
+            if (e1 < E) s_logit[tb][e1] = canon_nan(pb + a.bias[e1]);
+          }
         }
       }
-    } else {
+    }
+  } else {
+    for (int e = wv; e < E; e += nw) {
+      const uint16_t *w_e = a.w + (size_t)e * nq * 512;
       for (int tb = 0; tb < nt; tb++) {
         const float p = router_dot<0>(w_e, s_x + tb * Hp, nq, lane);
         if (lane == 0) s_logit[tb][e] = canon_nan(p + a.bias[e]);
@@ -276,16 +314,129 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
     for (int s2 = 0; s2 < a.k; s2++) a.pos[s2] = s2 < sel ? s2 : -1;
   }
   if (a.bucket_ticket) {
-    wait_mem();  // this thread's idx stores (agent scope) have completed
+    // The grouping. When the per-block count table fits the block's LDS, in parallel: every
+    // block counts its entries per expert (blk_count[block][e]) and ranks each entry among the
+    // block's entries of its expert, in entry order t k + slot (rank[t k + slot]); the last
+    // block loads the whole table (and every entry's expert and rank) in one round of loads,
+    // turns it into per-block bases (an exclusive prefix over blocks, per expert) in LDS and
+    // scatters every entry to base + rank. Otherwise the last block runs bucket_block. Either
+    // way the entries of one expert end up ordered by t k + slot.
+    const int nblk = (int)gridDim.x, N = a.T * a.k;
+    const int ld_bc = nblk + 1;  // LDS row of one expert's counts (odd: rows on distinct banks)
+    const bool table = (size_t)ld_bc * E + 2 * (size_t)E <= (size_t)TB * Hp;
+    __syncthreads();  // s_order of every token of the block
+    if (table && wv == 0) {
+      int *s_cnt = reinterpret_cast<int *>(s_x);  // [E] (the x staging is free now)
+      const int ne = nt * a.k;
+      for (int e = lane; e < E; e += 64) s_cnt[e] = 0;
+      for (int p0 = 0; p0 < ne; p0 += 64) {
+        const int l = p0 + lane, tb = l / a.k, slot = l - tb * a.k;
+        const int e = l < ne ? s_order[tb][slot] : -1;
+        const uint32_t v = (uint32_t)(e + 1);  // 0 .. kMaxExperts: 9 bits
+        uint64_t same = ~0ull;
+#pragma unroll
+        for (int bit = 0; bit < 9; bit++) {
+          const uint64_t bb = __ballot((v >> bit) & 1u);
+          same &= ((v >> bit) & 1u) ? bb : ~bb;
+        }
+        const uint64_t below = same & ((1ull << lane) - 1ull);
+        const int base = e >= 0 ? s_cnt[e] : 0;
+        if (e >= 0) {
+          st_agent(reinterpret_cast<uint32_t *>(a.rank) + (size_t)t0 * a.k + l, (uint32_t)(base + __popcll(below)));
+          if (below == 0) s_cnt[e] = base + __popcll(same);  // the group's first lane
+        }
+      }
+      for (int e = lane; e < E; e += 64)
+        st_agent(reinterpret_cast<uint32_t *>(a.blk_count) + (size_t)blockIdx.x * E + e, (uint32_t)s_cnt[e]);
+    }
+    wait_mem();  // this thread's idx, rank and count stores (agent scope) have completed
     __syncthreads();
     if (threadIdx.x == 0)
       s_last = __hip_atomic_fetch_add(a.bucket_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     __syncthreads();
     if (!s_last) return;
     if (threadIdx.x == 0) st_agent(a.bucket_ticket, 0u);  // zero again for the next launch
-    int *ws = reinterpret_cast<int *>(s_x);  // (2 + 16) E ints; the host checked they fit
-    bucket_block<true>(a.idx, a.T, a.k, E, a.n_active, a.active_ids, a.active_off, a.entry_src,
-                       a.pos, ws, ws + E, ws + 2 * E);
+    if (!table) {
+      int *ws = reinterpret_cast<int *>(s_x);  // (2 + 16) E ints; the host checked they fit
+      bucket_block<true>(a.idx, a.T, a.k, E, a.n_active, a.active_ids, a.active_off, a.entry_src,
+                         a.pos, ws, ws + E, ws + 2 * E);
+      return;
+    }
+    // s_bc: the table expert-major in LDS, [e][block] with rows ld_bc apart
+    int *s_bc = reinterpret_cast<int *>(s_x), *s_tot = s_bc + (size_t)ld_bc * E, *s_base = s_tot + E;
+    const uint32_t *bc = reinterpret_cast<const uint32_t *>(a.blk_count);
+    const uint32_t *ix = reinterpret_cast<const uint32_t *>(a.idx), *rk = reinterpret_cast<const uint32_t *>(a.rank);
+    constexpr int kPerT = 16;  // entries per thread per round
+    // the count table into LDS, and the first round's entries, in one round of loads
+    int ev[kPerT], rv[kPerT];
+#pragma unroll
+    for (int i = 0; i < kPerT; i++) {
+      const int n = (int)threadIdx.x + i * kRouteThreads;
+      ev[i] = n < N ? (int)ld_agent(ix + n) : -1;
+      rv[i] = n < N ? (int)ld_agent(rk + n) : 0;
+    }
+    for (int i0 = threadIdx.x; i0 < nblk * E; i0 += 8 * kRouteThreads) {
+      uint32_t cv[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) cv[q] = i0 + q * kRouteThreads < nblk * E ? ld_agent(bc + i0 + q * kRouteThreads) : 0u;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const int i = i0 + q * kRouteThreads, bi = i / E;
+        if (i < nblk * E) s_bc[(i - bi * E) * ld_bc + bi] = (int)cv[q];
+      }
+    }
+    __syncthreads();
+    // per expert, bases = exclusive prefix of the counts over blocks: a wavefront per expert,
+    // lane l summing blocks [l S, l S + S) serially, then one wave scan of the 64 lane sums
+    const int S = (nblk + 63) / 64;
+    for (int e = wv; e < E; e += nw) {
+      int *row = s_bc + (size_t)e * ld_bc;
+      int sum = 0;
+      for (int q = 0; q < S; q++) {
+        const int bi = lane * S + q;
+        if (bi < nblk) sum += row[bi];
+      }
+      int incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o);
+        if (lane >= o) incl += u;
+      }
+      int run = incl - sum;
+      for (int q = 0; q < S; q++) {
+        const int bi = lane * S + q;
+        if (bi < nblk) {
+          const int c = row[bi];
+          row[bi] = run;
+          run += c;
+        }
+      }
+      if (lane == 63) s_tot[e] = incl;
+    }
+    __syncthreads();
+    if (wv == 0) expert_list_wave(s_tot, E, lane, s_base, a.active_ids, a.active_off, a.n_active);
+    __syncthreads();
+    for (int n0 = threadIdx.x;; n0 += kPerT * kRouteThreads) {
+#pragma unroll
+      for (int i = 0; i < kPerT; i++) {
+        const int n = n0 + i * kRouteThreads;
+        if (n >= N) break;
+        if (ev[i] < 0) {
+          a.pos[n] = -1;
+        } else {
+          const int ge = s_base[ev[i]] + s_bc[ev[i] * ld_bc + (n / a.k) / TB] + rv[i];
+          a.entry_src[ge] = n / a.k;
+          a.pos[n] = ge;
+        }
+      }
+      if (n0 + kPerT * kRouteThreads >= N) break;
+#pragma unroll
+      for (int i = 0; i < kPerT; i++) {  // the next round's entries
+        const int n = n0 + (kPerT + i) * kRouteThreads;
+        ev[i] = n < N ? (int)ld_agent(ix + n) : -1;
+        rv[i] = n < N ? (int)ld_agent(rk + n) : 0;
+      }
+    }
   }
 }
 
@@ -311,7 +462,7 @@ bool route_bucket_fits(int H, int E) { return 18 * E <= route_hp(H); }
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
   if (a.E < 1 || a.E > kMaxExperts || a.k < 1 || a.k > kMaxTopK || a.k > a.E || a.T < 1 ||
       a.H < 1 || (a.fuse_bucket && a.T != 1) || (a.xrec && a.H > 128 * kGemmNs) ||
-      (a.bucket_ticket && (a.fuse_bucket || !route_bucket_fits(a.H, a.E))))
+      (a.bucket_ticket && (a.fuse_bucket || !route_bucket_fits(a.H, a.E) || !a.blk_count || !a.rank)))
     return hipErrorInvalidValue;
   const int nq = ((a.H + 63) / 64 + 7) / 8;
   const size_t lds = (size_t)nq * 8 * 64 * sizeof(float);

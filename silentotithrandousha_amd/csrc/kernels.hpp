@@ -29,6 +29,8 @@ struct RouteArgs {
   int fuse_bucket;       // T == 1: also write the expert list
   int32_t *n_active, *active_ids, *active_off, *entry_src, *pos;
   uint32_t *bucket_ticket;  // T > 1: zeroed counter; the last block buckets (route_bucket_fits)
+  int32_t *blk_count;       // with bucket_ticket: [route blocks][E] per-block expert counts
+  int32_t *rank;            // with bucket_ticket: [T, k] rank of each entry in its block and expert
 };
 
 struct GemvArgs {

@@ -85,6 +85,7 @@ struct Work {
   uint16_t *xsplit, *hsplit;
   uint8_t *xrec, *hrec;  // grouped GEMM activation records: tokens, entries (padding zero)
   int32_t *idx, *n_active, *active_ids, *active_off, *entry_src, *pos;
+  int32_t *blk_count, *rank;  // the router's grouping: per-block expert counts, per-entry ranks
   size_t hrec_bytes;     // bytes of hrec, which must hold zeros where no kernel writes
 };
 
@@ -227,6 +228,8 @@ size_t carve_work(Work &w, char *b, size_t T, size_t k, size_t E, size_t H, size
   w.active_off = (int32_t *)take((E + 1) * 4);
   w.entry_src = (int32_t *)take(N * 4);
   w.pos = (int32_t *)take(N * 4);
+  w.blk_count = (int32_t *)take(T * E * 4);  // router blocks <= T
+  w.rank = (int32_t *)take(N * 4);
   w.xrec = (uint8_t *)take(T * GemmRec::kBytes);
   w.hrec_bytes = N * GemmRec::kBytes;
   w.hrec = (uint8_t *)take(w.hrec_bytes);
@@ -517,6 +520,8 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
   ra.pos = w.pos;
   const bool fuse_bucket = T > 1 && route_bucket_fits((int)c->H, (int)E);
   ra.bucket_ticket = fuse_bucket ? (uint32_t *)c->route_ticket.p : nullptr;
+  ra.blk_count = w.blk_count;
+  ra.rank = w.rank;
   RETURN_IF(timed(c, K_ROUTE, s, [&] { return launch_route(ra, s); }));
   if (T > 1 && !fuse_bucket)
     RETURN_IF(timed(c, K_BUCKET, s, [&] {
