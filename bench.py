@@ -10,9 +10,11 @@ distinct tokens, so every step streams its experts from HBM.
 The default run (`--workload all`) also times the other configurations in the same process and
 reports each under `configs` with its own dominant-kernel roofline: config 1 (one 2880x2880
 MXFP4 matvec), config 3 (64 tokens through one layer), config 4 (4096 tokens through all 24
-layers), config 5 (a 120B-shaped layer, 128 experts, at 1 and 2048 tokens), and the next row
-beside the path (the bf16 LM head). Those use their own step counts (in each entry); --steps /
---warmup apply to the headline.
+layers; once more with the grouped GEMM on MXFP6 activations, the opt-in MOE_OPT_ACT_QUANT
+contract, as `config4_prefill_4096x24_mxfp6`), config 5 (a 120B-shaped layer, 128 experts, at 1
+and 2048 tokens), and the next rows beside the path (the bf16 LM head, the Beaver-triple
+generator). Those use their own step counts (in each entry); --steps / --warmup apply to the
+headline.
 
 Prints ONE JSON line. `--workload <name>` runs one configuration alone (for profiling).
 """
@@ -42,8 +44,13 @@ ARITH_DECODE = ("MXFP4 weights as stored (E2M1 + E8M0) on the block-scaled MFMA;
 ARITH_GEMM = ("MXFP4 weights as stored (E2M1 + E8M0) on the block-scaled MFMA; activations as 3 "
               "fp6 E2M3 terms per 32-value block (exact to ~2^-13 of the block maximum); f32 "
               "accumulate")
+ARITH_GEMM_Q = ("MXFP4 weights as stored on the block-scaled MFMA; activations (x and the SwiGLU "
+                "output h) quantized to MXFP6 (one E2M3 value per element, OCP MX E8M0 scale per "
+                "32-value block): the opt-in MOE_OPT_ACT_QUANT contract (the fp32 path on the "
+                "quantized activations), not the default 1e-3 contract; f32 accumulate")
 DTYPE_DECODE = "mxfp4 x f32(4 fp8 terms), f32 acc"
 DTYPE_GEMM = "mxfp4 x f32(3 fp6 terms), f32 acc"
+DTYPE_GEMM_Q = "mxfp4 x mxfp6, f32 acc"
 
 # workload -> (config name, experts, tokens per layer, layers per step, default steps, warmup)
 WORKLOADS = {
@@ -184,7 +191,17 @@ KERNELS = ["route", "bucket", "gate_up", "down", "combine", "decode_gate_up", "d
 
 
 # ------------------------------------------------------------------ layer workloads (configs 2-5)
-def run_layer(model, workload, steps, warmup, graph=True, copy_mib=0, traffic_kib=0.0):
+def run_layer(model, workload, steps, warmup, graph=True, copy_mib=0, traffic_kib=0.0, act_quant=False):
+    """act_quant: the grouped GEMM on MXFP6 activations (MOE_OPT_ACT_QUANT) for this run only."""
+    disp = model.disp
+    disp.set_act_quant(act_quant)
+    try:
+        return _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act_quant)
+    finally:
+        disp.set_act_quant(False)
+
+
+def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act_quant):
     config_name, E, T, lps, _, _ = WORKLOADS[workload]
     assert E == model.E
     H, I, k, n_layers = model.H, model.I, 4, model.n_layers
@@ -275,12 +292,14 @@ def run_layer(model, workload, steps, warmup, graph=True, copy_mib=0, traffic_ki
     res = {
         "value": round(tokens_per_s, 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms_per_step, 6),
-        "dtype": DTYPE_DECODE if T == 1 and dom == "decode_layer" else DTYPE_GEMM,
+        "dtype": (DTYPE_DECODE if T == 1 and dom == "decode_layer" else DTYPE_GEMM_Q if act_quant and dom == "gate_up"
+                  else DTYPE_GEMM),
         "config": {"workload": config_name, "name": workload, "hidden": H, "intermediate": I,
                    "experts": E, "top_k": k, "tokens_per_layer": T, "layers_per_step": lps,
                    "resident_layers": n_layers,
                    "weights": "MXFP4 E2M1 + E8M0 (checkpoint layout repacked on preload)",
-                   "arithmetic": ARITH_DECODE if dom == "decode_layer" else ARITH_GEMM,
+                   "arithmetic": (ARITH_DECODE if dom == "decode_layer" else ARITH_GEMM_Q if act_quant and dom == "gate_up"
+                                  else ARITH_GEMM),
                    "graph_replay": ("all steps: %d x graph of %d steps%s" % (n_full, G, f" + graph of {rem}" if rem else "")
                                     if G else "none (eager launches)")},
         "roofline": {"bound": "hbm", "kernel": kname,
@@ -300,7 +319,8 @@ def run_layer(model, workload, steps, warmup, graph=True, copy_mib=0, traffic_ki
     }
     if mfma_bound and d_n:
         # dense regime: the MFMA roofline against the MXFP4 peak, algorithmic flops (one
-        # MXFP4 x MXFP4 product per multiply-add; the path issues 3 activation terms)
+        # MXFP4 x MXFP4 product per multiply-add; the exact path issues 3 activation terms, the
+        # quantized mode one, at the same fp4 x fp6 rate as fp4 x fp4)
         res["roofline"].update(bound="mfma", achieved=round(d_flops / d_avg_s / 1e12, 2),
                                peak=MXFP4_PEAK_TFLOPS, unit="TFLOP/s",
                                frac=round(d_flops / d_avg_s / 1e12 / MXFP4_PEAK_TFLOPS, 5),
@@ -632,6 +652,8 @@ def main():
     ap.add_argument("--gemm-band", type=int, default=0, help="grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)")
     ap.add_argument("--batch-gemm", type=int, default=1, choices=(0, 1, 2),
                     help="batches: 0 GEMV kernels, 1 grouped GEMM when experts average >= 4 entries, 2 always GEMM")
+    ap.add_argument("--act-quant", action="store_true",
+                    help="grouped GEMM on MXFP6 activations (MOE_OPT_ACT_QUANT; single --workload runs)")
     ap.add_argument("--traffic-kib", type=float, default=0.0,
                     help="HBM KiB per launch of the dominant kernel (overrides the calibrated "
                          "rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE figure in profiles/traffic.json)")
@@ -672,13 +694,14 @@ def main():
     else:
         E = WORKLOADS[head][1]
         m = Model(H20, I20, E, args.layers if E == 32 else args.layers_120b, args)
-        res = run_layer(m, head, steps, warmup, args.graph, args.copy_mib, args.traffic_kib)
+        res = run_layer(m, head, steps, warmup, args.graph, args.copy_mib, args.traffic_kib, args.act_quant)
         log(f"{head}: {res['value']} tokens/s ({res['ms_per_step']} ms/step)")
         extras = {}
         if args.workload == "all":
-            for w, key in (("decode64", "config3_decode64"), ("prefill", "config4_prefill_4096x24")):
-                extras[key] = run_layer(m, w, WORKLOADS[w][4], WORKLOADS[w][5], args.graph)
-                log(f"{w}: {extras[key]['value']} tokens/s")
+            for w, key, q in (("decode64", "config3_decode64", False), ("prefill", "config4_prefill_4096x24", False),
+                              ("prefill", "config4_prefill_4096x24_mxfp6", True)):
+                extras[key] = run_layer(m, w, WORKLOADS[w][4], WORKLOADS[w][5], args.graph, act_quant=q)
+                log(f"{key}: {extras[key]['value']} tokens/s")
             m.close()
             m = Model(H20, I20, 128, args.layers_120b, args)
             for w, key in (("decode1_120b", "config5_120b_decode1"), ("prefill_120b", "config5_120b_2048")):

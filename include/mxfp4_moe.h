@@ -93,7 +93,15 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * identical).
  * MOE_OPT_MATVEC: moe_mxfp4_matvec_device runs in one launch on the block-scaled MFMA (x as 4
  * fp8 terms, exact to 2^-16) when 1 (default) and cols <= 3072 with x 16-byte aligned; otherwise,
- * and when 0, as two launches on the bf16 MFMA (x as bf16 hi + lo). Results agree to 1e-5. */
+ * and when 0, as two launches on the bf16 MFMA (x as bf16 hi + lo). Results agree to 1e-5.
+ * MOE_OPT_ACT_QUANT: 0 (default) the grouped GEMM takes its activations (x, and the SwiGLU output
+ * h) exact to about 2^-13 of each 32-value block's maximum (3 E2M3 terms), within the 1e-3
+ * tolerance of the f32 path; 1 quantizes them to MXFP6 (one E2M3 value per element, one E8M0
+ * scale per 32-value block, the OCP MX rule: scale 2^(floor(log2 amax) - 2), round to nearest
+ * even, saturate at 7.5): a third of the MFMA work, and results that follow the f32 path applied
+ * to those quantized activations (not the f32 path itself). Routing is unchanged (the router
+ * reads x unquantized); single-token forwards and the GEMV batch path are unaffected. In this mode
+ * MOE_OPT_GEMM_SHAPE(_DOWN) codes 2, 3, 4, 6 and 8 select the default shape. */
 enum moe_option {
   MOE_OPT_FUSED_DECODE = 1,
   MOE_OPT_SPIN_LIMIT = 2,
@@ -101,7 +109,8 @@ enum moe_option {
   MOE_OPT_GEMM_SHAPE = 4,
   MOE_OPT_GEMM_BAND = 5,
   MOE_OPT_MATVEC = 6,
-  MOE_OPT_GEMM_SHAPE_DOWN = 7
+  MOE_OPT_GEMM_SHAPE_DOWN = 7,
+  MOE_OPT_ACT_QUANT = 8
 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 

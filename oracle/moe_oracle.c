@@ -231,18 +231,62 @@ void orc_mxfp4_matvec_f32(const uint8_t *blocks, const uint8_t *scales, size_t r
   free(W);
 }
 
-void orc_expert_ffn_f32(const float *x, size_t T, const uint8_t *gu_blocks,
-                        const uint8_t *gu_scales, const float *gu_bias, const uint8_t *d_blocks,
-                        const uint8_t *d_scales, const float *d_bias, size_t H, size_t I,
-                        float limit, float *y, float *h_out) {
+/* ------------------------------------------------------------------ MXFP6 activations */
+
+/* |v| (already divided by its block scale, so |v| < 8) on the E2M3 grid: steps of 1/8 below 2,
+ * 1/4 in [2, 4), 1/2 in [4, 8); round to nearest, ties to the even code (rintf in the default
+ * rounding mode: the step count is even exactly when the code's last mantissa bit is 0);
+ * everything from 7.5 up saturates to 7.5 (the largest E2M3 magnitude). */
+static float e2m3_rne(float v) {
+  const float a = fabsf(v);
+  float q;
+  if (a >= 7.5f) q = 7.5f;
+  else {
+    const float step = a < 2.0f ? 0.125f : (a < 4.0f ? 0.25f : 0.5f);
+    q = rintf(a / step) * step;
+  }
+  return v < 0.0f ? -q : q;
+}
+
+void orc_quant_mxfp6(const float *x, size_t rows, size_t cols, float *out) {
+  for (size_t r = 0; r < rows; r++) {
+    const float *xr = x + r * cols;
+    float *o = out + r * cols;
+    for (size_t b0 = 0; b0 < cols; b0 += 32) {
+      const size_t n = cols - b0 < 32 ? cols - b0 : 32;
+      float m = 0.0f;
+      int bad = 0;
+      for (size_t i = 0; i < n; i++) {
+        if (!isfinite(xr[b0 + i])) bad = 1;
+        else if (fabsf(xr[b0 + i]) > m) m = fabsf(xr[b0 + i]);
+      }
+      if (bad) {
+        for (size_t i = 0; i < n; i++) o[b0 + i] = u2f(ORC_CANON_NAN);
+        continue;
+      }
+      int E = 0;
+      if (m > 0.0f) frexpf(m, &E); /* m = f 2^E, f in [1/2, 1) */
+      int se = E - 3;              /* 2^(floor(log2 m) - 2): the block maximum in [4, 8) */
+      if (se < -126) se = -126;
+      for (size_t i = 0; i < n; i++) o[b0 + i] = ldexpf(e2m3_rne(ldexpf(xr[b0 + i], -se)), se);
+    }
+  }
+}
+
+static void expert_ffn(const float *x, size_t T, const uint8_t *gu_blocks, const uint8_t *gu_scales,
+                       const float *gu_bias, const uint8_t *d_blocks, const uint8_t *d_scales,
+                       const float *d_bias, size_t H, size_t I, float limit, int quant, float *y,
+                       float *h_out) {
   const float alpha = 1.702f; /* session.rs:99 */
   float *Wgu = (float *)malloc(2 * I * H * sizeof(float));
   float *Wd = (float *)malloc(H * I * sizeof(float));
   float *gu = (float *)malloc(T * 2 * I * sizeof(float));
   float *h = (float *)malloc(T * I * sizeof(float));
+  float *xq = quant ? (float *)malloc(T * H * sizeof(float)) : NULL;
   orc_dequant_mxfp4_matrix(gu_blocks, gu_scales, 2 * I, H, Wgu);
   orc_dequant_mxfp4_matrix(d_blocks, d_scales, H, I, Wd);
-  matmul_seq(Wgu, 2 * I, H, x, T, gu);
+  if (quant) orc_quant_mxfp6(x, T, H, xq);
+  matmul_seq(Wgu, 2 * I, H, quant ? xq : x, T, gu);
   for (size_t t = 0; t < T; t++) {
     float *g = gu + t * 2 * I;
     for (size_t r = 0; r < 2 * I; r++) g[r] = g[r] + gu_bias[r];
@@ -254,6 +298,7 @@ void orc_expert_ffn_f32(const float *x, size_t T, const uint8_t *gu_blocks,
       h[t * I + i] = (up + 1.0f) * glu;
     }
   }
+  if (quant) orc_quant_mxfp6(h, T, I, h);
   matmul_seq(Wd, H, I, h, T, y);
   for (size_t t = 0; t < T; t++)
     for (size_t r = 0; r < H; r++)
@@ -264,6 +309,21 @@ void orc_expert_ffn_f32(const float *x, size_t T, const uint8_t *gu_blocks,
   free(Wd);
   free(gu);
   free(h);
+  free(xq);
+}
+
+void orc_expert_ffn_f32(const float *x, size_t T, const uint8_t *gu_blocks,
+                        const uint8_t *gu_scales, const float *gu_bias, const uint8_t *d_blocks,
+                        const uint8_t *d_scales, const float *d_bias, size_t H, size_t I,
+                        float limit, float *y, float *h_out) {
+  expert_ffn(x, T, gu_blocks, gu_scales, gu_bias, d_blocks, d_scales, d_bias, H, I, limit, 0, y, h_out);
+}
+
+void orc_expert_ffn_mxfp6(const float *x, size_t T, const uint8_t *gu_blocks,
+                          const uint8_t *gu_scales, const float *gu_bias, const uint8_t *d_blocks,
+                          const uint8_t *d_scales, const float *d_bias, size_t H, size_t I,
+                          float limit, float *y, float *h_out) {
+  expert_ffn(x, T, gu_blocks, gu_scales, gu_bias, d_blocks, d_scales, d_bias, H, I, limit, 1, y, h_out);
 }
 
 /* ------------------------------------------------------------------ router */
@@ -433,12 +493,11 @@ void orc_moe_block_f32(const float *x, size_t T, size_t H, size_t I, size_t E, s
   free(y);
 }
 
-void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k,
-                       float limit, const uint16_t *router_w_bf16, const float *router_b,
-                       const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
-                       const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
-                       const orc_adaptive *ad, float *y, float *logits_out, int32_t *idx_out,
-                       float *w_out) {
+static void moe_layer(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k, float limit,
+                      const uint16_t *router_w_bf16, const float *router_b, const uint8_t *gu_blocks,
+                      const uint8_t *gu_scales, const float *gu_bias, const uint8_t *d_blocks,
+                      const uint8_t *d_scales, const float *d_bias, const orc_adaptive *ad, int quant,
+                      float *y, float *logits_out, int32_t *idx_out, float *w_out) {
   size_t nbh = H / 32, nbi = I / 32;
   float *logits = (float *)malloc(T * E * sizeof(float));
   int32_t *idx = (int32_t *)malloc(T * k * sizeof(int32_t));
@@ -459,9 +518,8 @@ void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, s
           slot_of[n++] = t * k + s;
         }
     if (!n) continue;
-    orc_expert_ffn_f32(xs, n, gu_blocks + e * 2 * I * nbh * 16, gu_scales + e * 2 * I * nbh,
-                       gu_bias + e * 2 * I, d_blocks + e * H * nbi * 16, d_scales + e * H * nbi,
-                       d_bias + e * H, H, I, limit, ys, NULL);
+    expert_ffn(xs, n, gu_blocks + e * 2 * I * nbh * 16, gu_scales + e * 2 * I * nbh, gu_bias + e * 2 * I,
+               d_blocks + e * H * nbi * 16, d_scales + e * H * nbi, d_bias + e * H, H, I, limit, quant, ys, NULL);
     for (size_t j = 0; j < n; j++) memcpy(outs + slot_of[j] * H, ys + j * H, H * sizeof(float));
   }
   for (size_t t = 0; t < T; t++) {
@@ -473,6 +531,24 @@ void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, s
   if (idx_out) memcpy(idx_out, idx, T * k * sizeof(int32_t));
   if (w_out) memcpy(w_out, w, T * k * sizeof(float));
   free(logits); free(idx); free(w); free(outs); free(xs); free(ys); free(slot_of);
+}
+
+void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k,
+                       float limit, const uint16_t *router_w_bf16, const float *router_b,
+                       const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                       const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                       const orc_adaptive *ad, float *y, float *logits, int32_t *idx, float *w) {
+  moe_layer(x, T, H, I, E, k, limit, router_w_bf16, router_b, gu_blocks, gu_scales, gu_bias, d_blocks, d_scales,
+            d_bias, ad, 0, y, logits, idx, w);
+}
+
+void orc_moe_layer_mxfp6(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k,
+                         float limit, const uint16_t *router_w_bf16, const float *router_b,
+                         const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                         const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                         const orc_adaptive *ad, float *y, float *logits, int32_t *idx, float *w) {
+  moe_layer(x, T, H, I, E, k, limit, router_w_bf16, router_b, gu_blocks, gu_scales, gu_bias, d_blocks, d_scales,
+            d_bias, ad, 1, y, logits, idx, w);
 }
 
 /* ------------------------------------------------------------------ live CPU path */

@@ -71,6 +71,22 @@ void orc_expert_ffn_f32(const float *x, size_t T, const uint8_t *gu_blocks,
                         const uint8_t *gu_scales, const float *gu_bias, const uint8_t *d_blocks,
                         const uint8_t *d_scales, const float *d_bias, size_t H, size_t I,
                         float limit, float *y, float *h_out);
+/* ---- quantized-activation mode (no counterpart in the reference: the GPU's opt-in
+ * MOE_OPT_ACT_QUANT contract) ----
+ * orc_quant_mxfp6: each row's values in blocks of 32 (a short last block as it is) replaced by
+ * their MXFP6 value: scale 2^(floor(log2 amax) - 2) = 2^(E - 3) where amax = f 2^E, f in
+ * [1/2, 1) (OCP MX v1.0 with E2M3's largest exponent 2; 2^-3 for an all-zero block, at least
+ * 2^-126), each value divided by it, rounded to nearest (ties to even) on the E2M3 grid and
+ * saturated at 7.5, then multiplied back. A block holding a non-finite value becomes NaN.
+ * out may equal x.
+ * orc_expert_ffn_mxfp6 (and orc_moe_layer_mxfp6 below): orc_expert_ffn_f32 with the
+ * expert's input x and its SwiGLU output h replaced by their MXFP6 values before each product
+ * (routing reads x unquantized). */
+void orc_quant_mxfp6(const float *x, size_t rows, size_t cols, float *out);
+void orc_expert_ffn_mxfp6(const float *x, size_t T, const uint8_t *gu_blocks,
+                          const uint8_t *gu_scales, const float *gu_bias, const uint8_t *d_blocks,
+                          const uint8_t *d_scales, const float *d_bias, size_t H, size_t I,
+                          float limit, float *y, float *h_out);
 /* y = W x with W decoded by weights.rs:350-371; sequential non-fused sum per row. */
 void orc_mxfp4_matvec_f32(const uint8_t *blocks, const uint8_t *scales, size_t rows, size_t cols,
                           const float *x, float *y);
@@ -110,6 +126,12 @@ void orc_moe_layer_f32(const float *x, size_t T, size_t H, size_t I, size_t E, s
                        const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
                        const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
                        const orc_adaptive *ad, float *y, float *logits, int32_t *idx, float *w);
+/* The same with the experts' activations as MXFP6 (orc_expert_ffn_mxfp6). */
+void orc_moe_layer_mxfp6(const float *x, size_t T, size_t H, size_t I, size_t E, size_t k,
+                         float limit, const uint16_t *router_w_bf16, const float *router_b,
+                         const uint8_t *gu_blocks, const uint8_t *gu_scales, const float *gu_bias,
+                         const uint8_t *d_blocks, const uint8_t *d_scales, const float *d_bias,
+                         const orc_adaptive *ad, float *y, float *logits, int32_t *idx, float *w);
 
 /* Post-attention RMSNorm of the reference's fp32 restatement (session.rs:483-493):
  * inv_rms = 1 / sqrt(mean(x^2) + eps) (mean = sum / H, sqrt and reciprocal correctly rounded),

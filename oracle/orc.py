@@ -64,6 +64,9 @@ def lib():
     L.orc_moe_layer_f32.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_float, _u16p, _f32p,
                                     _u8p, _u8p, _f32p, _u8p, _u8p, _f32p, ctypes.c_void_p, _f32p,
                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    L.orc_moe_layer_mxfp6.argtypes = L.orc_moe_layer_f32.argtypes
+    L.orc_quant_mxfp6.argtypes = [_f32p, _sz, _sz, _f32p]
+    L.orc_expert_ffn_mxfp6.argtypes = L.orc_expert_ffn_f32.argtypes
     L.orc_combine.argtypes = [_f32p, _f32p, _sz, _sz, ctypes.c_int, _f32p]
     L.orc_rms_inv.argtypes = [_f32p, _sz, ctypes.c_float]
     L.orc_rms_inv.restype = ctypes.c_float
@@ -135,12 +138,13 @@ def mxfp4_matvec(blocks, scales, rows, cols, x):
 
 
 def expert_ffn(x, gu_blocks, gu_scales, gu_bias, d_blocks, d_scales, d_bias, H, I, limit=7.0,
-               want_h=False):
+               want_h=False, mxfp6=False):
+    """session.rs:87-124 on f32 weights; mxfp6: x and h as their MXFP6 values (quant_mxfp6)."""
     x = _c(x, np.float32).reshape(-1, H)
     T = x.shape[0]
     y = np.empty((T, H), np.float32)
     h = np.empty((T, I), np.float32) if want_h else None
-    lib().orc_expert_ffn_f32(x.reshape(-1), T, _c(gu_blocks, np.uint8).reshape(-1),
+    (lib().orc_expert_ffn_mxfp6 if mxfp6 else lib().orc_expert_ffn_f32)(x.reshape(-1), T, _c(gu_blocks, np.uint8).reshape(-1),
                              _c(gu_scales, np.uint8).reshape(-1), _c(gu_bias, np.float32).reshape(-1),
                              _c(d_blocks, np.uint8).reshape(-1), _c(d_scales, np.uint8).reshape(-1),
                              _c(d_bias, np.float32).reshape(-1), H, I, limit, y.reshape(-1),
@@ -171,7 +175,23 @@ def topk(logits, k, adaptive=None):
     return idx, w, probs, kused
 
 
-def moe_layer(x, layer, k, limit=7.0, adaptive=None):
+def quant_mxfp6(x):
+    """MXFP6 values of x's rows in blocks of 32 (OCP MX scale 2^(floor(log2 amax) - 2), E2M3
+    round to nearest even, saturation at 7.5; a block with a non-finite value -> NaN)."""
+    x = _c(x, np.float32)
+    cols = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_quant_mxfp6(x.reshape(-1), x.size // cols, cols, out.reshape(-1))
+    return out
+
+
+def moe_layer_mxfp6(x, layer, k, limit=7.0, adaptive=None):
+    """moe_layer with each expert's x and SwiGLU output h as their MXFP6 values (the GPU's
+    quantized-activation mode); routing on the unquantized x."""
+    return moe_layer(x, layer, k, limit, adaptive, _fn="orc_moe_layer_mxfp6")
+
+
+def moe_layer(x, layer, k, limit=7.0, adaptive=None, _fn="orc_moe_layer_f32"):
     """session.rs:818-980 MoE block on the fp32 path. `layer` is a dict of checkpoint tensors."""
     H = layer["H"]
     I = layer["I"]
@@ -183,7 +203,7 @@ def moe_layer(x, layer, k, limit=7.0, adaptive=None):
     idx = np.empty((T, k), np.int32)
     w = np.empty((T, k), np.float32)
     ad = ctypes.byref(adaptive) if adaptive is not None else None
-    lib().orc_moe_layer_f32(x.reshape(-1), T, H, I, E, k, limit, _c(layer["router_w"], np.uint16).reshape(-1),
+    getattr(lib(), _fn)(x.reshape(-1), T, H, I, E, k, limit, _c(layer["router_w"], np.uint16).reshape(-1),
                             _c(layer["router_b"], np.float32).reshape(-1),
                             _c(layer["gu_blocks"], np.uint8).reshape(-1),
                             _c(layer["gu_scales"], np.uint8).reshape(-1),

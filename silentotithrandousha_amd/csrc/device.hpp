@@ -801,14 +801,23 @@ typedef float f32x16v __attribute__((ext_vector_type(16)));
 typedef float f32x32v __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x6v __attribute__((ext_vector_type(6)));
 
+// Scale exponent of term t of an NT-term split of a block whose maximum is m = f 2^E, f in
+// [1/2, 1). Several terms: 2^(E - 2 - 5t) (term 0 holds the block in [-4, 4), so its residual
+// never saturates; each later term removes 5 more bits). One term (the quantized mode): the OCP
+// MX rule, 2^(floor(log2 m) - 2) = 2^(E - 3), the block maximum in [4, 8) (values past 7.5
+// saturate). Stops at 2^-126 (a normal f32) for blocks below about 2^-120.
+template <int NT>
+__device__ __forceinline__ int split_scale_exp(int E, int t) {
+  return max(NT == 1 ? E - 3 : E - 2 - 5 * t, -126);
+}
+
 // Split of 16 values of a 32-value block (block max |x| = m, bad = some value of the block is
-// not finite) into kGemmTerms E2M3 terms: term t has scale 2^(E - 2 - 5t) where m = f 2^E,
-// f in [1/2, 1) (so term 0 holds the block in [-4, 4)), and takes the exact residual of the
-// terms before it (the activation is then exact to about 2^-13 of the block maximum). Codes of
-// value u at bits 6u of d[t][0..2]; sb byte t = the E8M0 scale of term t (0xFF, NaN, for a bad
-// block: the products come out NaN, as the f32 arithmetic would). Scales stop at 2^-126 (a
-// normal f32) for blocks below about 2^-120.
-__device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool bad, uint32_t (&d)[kGemmTerms][3],
+// not finite) into NT E2M3 terms at split_scale_exp's scales, each taking the exact residual of
+// the terms before it (3 terms: the activation is exact to about 2^-13 of the block maximum).
+// Codes of value u at bits 6u of d[t][0..2]; sb byte t = the E8M0 scale of term t (0xFF, NaN, for
+// a bad block: the products come out NaN, as the f32 arithmetic would).
+template <int NT>
+__device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool bad, uint32_t (&d)[NT][3],
                                             uint32_t &sb) {
   int E = 0;
   if (m > 0.0f && isfinite(m)) frexpf(m, &E);
@@ -817,8 +826,8 @@ __device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool 
   for (int i = 0; i < 16; i++) r[i] = bad ? 0.0f : x[i];
   sb = 0;
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-    const int se = max(E - 2 - 5 * t, -126);
+  for (int t = 0; t < NT; t++) {
+    const int se = split_scale_exp<NT>(E, t);
     sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
     const float sc = __builtin_amdgcn_ldexpf(1.0f, se);
     f32x16v a = {}, b = {};
@@ -830,9 +839,11 @@ __device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool 
     u32x6v c;
     f32x32v q;
     asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(c) : "v"(a), "v"(b), "v"(sc));
-    asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
+    if (t + 1 < NT) {  // the residual feeds the next term
+      asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
 #pragma unroll
-    for (int i = 0; i < 16; i++) r[i] = r[i] - q[i];
+      for (int i = 0; i < 16; i++) r[i] = r[i] - q[i];
+    }
     d[t][0] = c[0];
     d[t][1] = c[1];
     d[t][2] = c[2];
@@ -843,7 +854,8 @@ __device__ __forceinline__ void split16_fp6(const float (&x)[16], float m, bool 
 // split16_fp6 for a whole 32-value block in one lane (x[u] = value u, m = its maximum |x|): the
 // conversions take all 32 values at once, and term t's codes are the 6 dwords of the block's
 // B operand (value u at bits 6u). Same codes and scales as two split16_fp6 halves.
-__device__ __forceinline__ void split32_fp6(const float (&x)[32], float m, bool bad, uint32_t (&d)[kGemmTerms][6],
+template <int NT>
+__device__ __forceinline__ void split32_fp6(const float (&x)[32], float m, bool bad, uint32_t (&d)[NT][6],
                                             uint32_t &sb) {
   int E = 0;
   if (m > 0.0f && isfinite(m)) frexpf(m, &E);
@@ -852,8 +864,8 @@ __device__ __forceinline__ void split32_fp6(const float (&x)[32], float m, bool 
   for (int i = 0; i < 32; i++) r[i] = bad ? 0.0f : x[i];
   sb = 0;
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-    const int se = max(E - 2 - 5 * t, -126);
+  for (int t = 0; t < NT; t++) {
+    const int se = split_scale_exp<NT>(E, t);
     sb |= (bad ? 0xFFu : (uint32_t)(se + 127)) << (8 * t);
     const float sc = __builtin_amdgcn_ldexpf(1.0f, se);
     f32x16v a, b;
@@ -866,7 +878,7 @@ __device__ __forceinline__ void split32_fp6(const float (&x)[32], float m, bool 
     asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(c) : "v"(a), "v"(b), "v"(sc));
 #pragma unroll
     for (int k = 0; k < 6; k++) d[t][k] = c[k];
-    if (t + 1 < kGemmTerms) {  // the residual feeds the next term (the last term needs none)
+    if (t + 1 < NT) {  // the residual feeds the next term (the last term needs none)
       f32x32v q;
       asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(q) : "v"(c), "v"(sc));
 #pragma unroll
@@ -875,37 +887,11 @@ __device__ __forceinline__ void split32_fp6(const float (&x)[32], float m, bool 
   }
 }
 
-// Thread p (< 8 kGemmNs writes; every lane of the pair must run it) of a row's split: half
-// p & 1 (values 16 h .. 16 h + 15) of 32-value block p >> 1, given in v, into the row's GemmRec
-// record r: the kGemmTerms E2M3 terms of the half (block maximum and finiteness shared with the
-// neighbouring lane, which holds the other half) and, from the h = 0 lane, the terms' scales.
-__device__ __forceinline__ void rec_split_half(const float (&v)[16], int p, uint8_t *r) {
-  float m = 0.0f, bad = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    m = fmaxf(m, fabsf(v[i]));
-    if (!isfinite(v[i])) bad = 1.0f;
-  }
-  m = fmaxf(m, xor_lane<1>(m));
-  bad = fmaxf(bad, xor_lane<1>(bad));
-  uint32_t d[kGemmTerms][3], sb;
-  split16_fp6(v, m, bad != 0.0f, d, sb);
-  if (p >= 8 * kGemmNs) return;
-  const int b = p >> 1, h = p & 1, st = b >> 2, i = b & 3;
-#pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-#pragma unroll
-    for (int u = 0; u < 3; u++) *reinterpret_cast<uint32_t *>(r + GemmRec::dword(st, t, i, 3 * h + u)) = d[t][u];
-  }
-  if (h == 0) {
-#pragma unroll
-    for (int t = 0; t < kGemmTerms; t++) r[GemmRec::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
-  }
-}
-
 // Block blk (values 32 blk .. 32 blk + 31, in v; 0 <= blk < 4 kGemmNs) of a row into the row's
-// GemmRec record r: one lane per block (split32_fp6), the same bytes as rec_split_half's pair.
+// GemmRecT<NT> record r: one lane per block (split32_fp6): the NT terms' codes and scale bytes.
+template <int NT>
 __device__ __forceinline__ void rec_split_block(const float (&v)[32], int blk, uint8_t *r) {
+  using R = GemmRecT<NT>;
   float m = 0.0f;
   bool bad = false;
 #pragma unroll
@@ -913,14 +899,14 @@ __device__ __forceinline__ void rec_split_block(const float (&v)[32], int blk, u
     m = fmaxf(m, fabsf(v[i]));
     bad = bad || !isfinite(v[i]);
   }
-  uint32_t d[kGemmTerms][6], sb;
-  split32_fp6(v, m, bad, d, sb);
+  uint32_t d[NT][6], sb;
+  split32_fp6<NT>(v, m, bad, d, sb);
   const int st = blk >> 2, i = blk & 3;
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
-    *reinterpret_cast<uint4 *>(r + GemmRec::dword(st, t, i, 0)) = make_uint4(d[t][0], d[t][1], d[t][2], d[t][3]);
-    *reinterpret_cast<uint2 *>(r + GemmRec::dword(st, t, i, 4)) = make_uint2(d[t][4], d[t][5]);
-    r[GemmRec::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+  for (int t = 0; t < NT; t++) {
+    *reinterpret_cast<uint4 *>(r + R::dword(st, t, i, 0)) = make_uint4(d[t][0], d[t][1], d[t][2], d[t][3]);
+    *reinterpret_cast<uint2 *>(r + R::dword(st, t, i, 4)) = make_uint2(d[t][4], d[t][5]);
+    r[R::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
   }
 }
 

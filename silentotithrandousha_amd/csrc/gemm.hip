@@ -2,11 +2,12 @@
 // applied to every (token, slot) entry routed to an expert, session.rs:943-972) on the
 // block-scaled MFMA v_mfma_scale_f32_16x16x128_f8f6f4: A = the expert's MXFP4 weights as
 // stored (E2M1 nibbles + E8M0 scales, resident tile16 layout), B = the activations of the
-// expert's entries as kGemmTerms E2M3 terms (split16_fp6; the batch router writes the tokens'
-// records, rec_split_half), f32 accumulation.
+// expert's entries as NT E2M3 terms per value (kGemmTerms: the exact split, the default; 1: the
+// quantized-activation mode, one MXFP6 term), written as GemmRecT<NT> records (the batch router
+// writes the tokens', rec_split_block; the gate_up epilogue the entries' h), f32 accumulation.
 //
 //   k_gemm_fp8     one block = WR x WC wavefronts; wavefront (wr, wc) owns RT tiles of 16 weight
-//                  rows x CGW column groups of 16 entries of one expert, x kGemmTerms terms.
+//                  rows x CGW column groups of 16 entries of one expert, x NT terms.
 //                  K-steps of 128 run through a ring of D = 2 or 3 LDS slots: the entries' B
 //                  records, the A chunks and their scale words all go into LDS by LDS-DMA
 //                  (global_load_lds), D - 1 steps ahead of the MFMAs.
@@ -20,17 +21,14 @@
 
 namespace moe {
 
-using G = GemmRec;  // step-major activation record (kernels.hpp)
-
 // ------------------------------------------------------------------ grouped GEMM
 
 // The batch path's activations are kGemmTerms E2M3 terms (exact to about 2^-13 of each block's
 // maximum, well inside the 1e-3 tolerance): the fp4 x fp6 MFMA issues in 16 cycles where fp4 x
-// fp8 takes 32, and a K-step of a record is 304 bytes instead of 400 for three fp8 terms.
-// B in LDS, per K-step: the entries' record steps one after the other (kEntryStep bytes each, as
-// the LDS-DMA copies them: each DMA reads whole record steps, a few rows per instruction).
-constexpr int kEntryStep = G::kStep;             // LDS bytes of one entry's K-step (a record step)
-constexpr int kChunks = G::kChunks;              // 16-byte chunks per entry K-step (19)
+// fp8 takes 32, and a K-step of a record is 304 bytes instead of 400 for three fp8 terms (112
+// bytes and a third of the MFMAs with one term, in the quantized mode).
+// B in LDS, per K-step: the entries' record steps one after the other (GemmRecT<NT>::kStep bytes
+// each, as the LDS-DMA copies them: each DMA reads whole record steps, a few rows per instruction).
 
 // s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
 // outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima).
@@ -68,8 +66,9 @@ __device__ __forceinline__ void lds_dma4_s(uint32_t voff, const void *sbase, con
 // LDS-DMA (global_load_lds) into a ring of D K-steps: per step, the B records of the block's
 // entries (kDma 1 KB pieces per wavefront), the block's WR * RT A chunks (1 KB each) and A-scale
 // words (256 B each), kDmaA of each per wavefront.
-template <int RT, int CGW, int WR, int WC, int D>
+template <int RT, int CGW, int WR, int WC, int D, int NT>
 struct GemmShape {
+  static constexpr int kChunks = GemmRecT<NT>::kChunks;     // 16-byte chunks per entry K-step
   static constexpr int W = WR * WC;
   static constexpr int kThreads = 64 * W;
   static constexpr int kRows = 16 * RT * WR;                 // weight rows per block
@@ -102,9 +101,10 @@ struct GemmShape {
 
 // B operands of one column group for the wavefront's lanes (entry j, lane group g): per term the
 // 32 bytes of the MFMA B layout and the E8M0 scale of the lane's block.
+template <int NT>
 struct GemmB {
-  i32x8 v[kGemmTerms];
-  uint32_t sc[kGemmTerms];
+  i32x8 v[NT];
+  uint32_t sc[NT];
 };
 
 // Term t of lane (j, g) from entry j's record step at eb: the first 16 bytes of block g (chunk
@@ -112,37 +112,44 @@ struct GemmB {
 // bytes per cycle of 8-byte reads): the pair chunk is read whole by both lanes of a pair, so 16
 // lanes share one address pair-wise and the reads of a 32-lane half have no bank conflicts; the
 // first-16-byte reads (records 304 bytes apart) take two passes where 8-byte reads took two each.
-__device__ __forceinline__ void gemm_read_b_t(GemmB &b, const uint8_t *eb, int g, int t) {
+template <int NT>
+__device__ __forceinline__ void gemm_read_b_t(GemmB<NT> &b, const uint8_t *eb, int g, int t) {
   const uint4 x = *reinterpret_cast<const uint4 *>(eb + (6 * t + g) * 16);
   const uint4 y = *reinterpret_cast<const uint4 *>(eb + (6 * t + 4 + (g >> 1)) * 16);
   const bool odd = (g & 1) != 0;
   b.v[t] = i32x8{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)(odd ? y.z : y.x), (int)(odd ? y.w : y.y), 0, 0};
 }
 
-// The scale words of the terms (chunk kChunks - 1 of the record step; byte g is the lane's block).
-__device__ __forceinline__ void gemm_read_sc(GemmB &b, const uint8_t *eb, int g) {
-  static_assert(kGemmTerms == 3, "three scale words per chunk");
-  const uint4 sc = *reinterpret_cast<const uint4 *>(eb + (kChunks - 1) * 16);
-  b.sc[0] = sc.x >> (8 * g);
-  b.sc[1] = sc.y >> (8 * g);
-  b.sc[2] = sc.z >> (8 * g);
+// The scale words of the terms (the last chunk of the record step; byte g is the lane's block).
+template <int NT>
+__device__ __forceinline__ void gemm_read_sc(GemmB<NT> &b, const uint8_t *eb, int g) {
+  const uint8_t *p = eb + (GemmRecT<NT>::kChunks - 1) * 16;
+  if constexpr (NT == 1) {
+    b.sc[0] = *reinterpret_cast<const uint32_t *>(p) >> (8 * g);
+  } else {
+    const uint4 sc = *reinterpret_cast<const uint4 *>(p);
+    const uint32_t w[3] = {sc.x, sc.y, sc.z};
+#pragma unroll
+    for (int t = 0; t < NT; t++) b.sc[t] = w[t] >> (8 * g);
+  }
 }
 
-__device__ __forceinline__ void gemm_read_b(GemmB &b, const uint8_t *eb, int g) {
+template <int NT>
+__device__ __forceinline__ void gemm_read_b(GemmB<NT> &b, const uint8_t *eb, int g) {
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) gemm_read_b_t(b, eb, g, t);
+  for (int t = 0; t < NT; t++) gemm_read_b_t(b, eb, g, t);
   gemm_read_sc(b, eb, g);
 }
 
-// MFMAs of one K-step for a wavefront: RT row tiles x CG column groups x kGemmTerms terms, all
+// MFMAs of one K-step for a wavefront: RT row tiles x CG column groups x NT terms, all
 // operands from the step's ring slot (sb: the step's A-scale words); sh = 8 * (s % 4) selects the
 // step's byte of them. The B operands of column group c + 1 are read while the MFMAs of group c
 // run. Column groups past the block's entries compute on repeated entries (not stored).
-template <int RT, int CGW, int WR, int WC, int D>
+template <int RT, int CGW, int WR, int WC, int D, int NT>
 __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *slot, const uint8_t *sb, int wr,
                                           int wc, int lane, int sh) {
-  using S = GemmShape<RT, CGW, WR, WC, D>;
-  constexpr int CG = CGW;
+  using S = GemmShape<RT, CGW, WR, WC, D, NT>;
+  constexpr int CG = CGW, kEntryStep = GemmRecT<NT>::kStep;
   const int j = lane & 15, g = lane >> 4;
   const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024;
   sb += wr * RT * 256;
@@ -153,14 +160,14 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *
     ar[r] = *reinterpret_cast<const uint4 *>(ab + r * 1024 + 16 * lane);
     sw[r] = *reinterpret_cast<const uint32_t *>(sb + r * 256 + 4 * lane) >> sh;
   }
-  GemmB bc, bn;
+  GemmB<NT> bc, bn;
   gemm_read_b(bc, bb, g);
 #pragma unroll
   for (int c = 0; c < CG; c++) {
     if (c + 1 < CG) gemm_read_b(bn, bb + 16 * (c + 1) * kEntryStep, g);
     __builtin_amdgcn_sched_barrier(0);  // the next group's reads issue before this group's MFMAs
 #pragma unroll
-    for (int t = 0; t < kGemmTerms; t++) {
+    for (int t = 0; t < NT; t++) {
 #pragma unroll
       for (int r = 0; r < RT; r++) {
         const i32x8 A = {(int)ar[r].x, (int)ar[r].y, (int)ar[r].z, (int)ar[r].w, 0, 0, 0, 0};
@@ -176,45 +183,55 @@ __device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *
 
 // All operands of one K-step for a wavefront (gemm_step's, read up front): the A chunks and scale
 // words of its RT row tiles and the B operands of its CG column groups.
-template <int RT, int CG>
+template <int RT, int CG, int NT>
 struct GemmOps {
   uint4 ar[RT];
   uint32_t sw[RT];
-  GemmB b[CG];
+  GemmB<NT> b[CG];
 };
 
 // One column group's B as read (both 16-byte chunks of each term, the scale chunk), before
 // gemm_read_b_t's half selection: reads issued early, selected once they are needed.
+template <int NT>
 struct GemmBRaw {
-  uint4 x[kGemmTerms], y[kGemmTerms], sc;
+  uint4 x[NT], y[NT];
+  uint32_t sc[NT];
 };
-__device__ __forceinline__ void gemm_read_b_raw(GemmBRaw &b, const uint8_t *eb, int g) {
+template <int NT>
+__device__ __forceinline__ void gemm_read_b_raw(GemmBRaw<NT> &b, const uint8_t *eb, int g) {
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
+  for (int t = 0; t < NT; t++) {
     b.x[t] = *reinterpret_cast<const uint4 *>(eb + (6 * t + g) * 16);
     b.y[t] = *reinterpret_cast<const uint4 *>(eb + (6 * t + 4 + (g >> 1)) * 16);
   }
-  b.sc = *reinterpret_cast<const uint4 *>(eb + (kChunks - 1) * 16);
+  const uint8_t *p = eb + (GemmRecT<NT>::kChunks - 1) * 16;
+  if constexpr (NT == 1) {
+    b.sc[0] = *reinterpret_cast<const uint32_t *>(p);
+  } else {
+    const uint4 sc = *reinterpret_cast<const uint4 *>(p);
+    const uint32_t w[3] = {sc.x, sc.y, sc.z};
+#pragma unroll
+    for (int t = 0; t < NT; t++) b.sc[t] = w[t];
+  }
 }
-__device__ __forceinline__ void gemm_select_b(GemmB &b, const GemmBRaw &r, int g) {
-  static_assert(kGemmTerms == 3, "three scale words per chunk");
+template <int NT>
+__device__ __forceinline__ void gemm_select_b(GemmB<NT> &b, const GemmBRaw<NT> &r, int g) {
   const bool odd = (g & 1) != 0;
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
+  for (int t = 0; t < NT; t++) {
     const uint4 &x = r.x[t], &y = r.y[t];
     b.v[t] = i32x8{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)(odd ? y.z : y.x), (int)(odd ? y.w : y.y), 0, 0};
+    b.sc[t] = r.sc[t] >> (8 * g);
   }
-  b.sc[0] = r.sc.x >> (8 * g);
-  b.sc[1] = r.sc.y >> (8 * g);
-  b.sc[2] = r.sc.z >> (8 * g);
 }
 
 // The A operands and the B operands of column groups [0, C1) (selected); C1 < CGW: the later
 // groups are read with gemm_read_b_raw and selected by the caller.
-template <int RT, int CGW, int WR, int WC, int D, int C1 = CGW>
-__device__ __forceinline__ void gemm_read_ops(GemmOps<RT, CGW> &o, const uint8_t *slot, const uint8_t *sb, int wr,
+template <int RT, int CGW, int WR, int WC, int D, int NT, int C1 = CGW>
+__device__ __forceinline__ void gemm_read_ops(GemmOps<RT, CGW, NT> &o, const uint8_t *slot, const uint8_t *sb, int wr,
                                               int wc, int lane, int sh) {
-  using S = GemmShape<RT, CGW, WR, WC, D>;
+  using S = GemmShape<RT, CGW, WR, WC, D, NT>;
+  constexpr int kEntryStep = GemmRecT<NT>::kStep;
   const int j = lane & 15, g = lane >> 4;
   const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024;
   sb += wr * RT * 256;
@@ -235,25 +252,27 @@ __device__ __forceinline__ void gemm_read_ops(GemmOps<RT, CGW> &o, const uint8_t
 // at the end takes the groups' accumulators as operands, so their MFMAs stay before the barrier
 // that follows (the compiler otherwise moved them past it, where they ran after every other part
 // of the step).
-template <int RT, int CGW, int C0, int C1, int NI, typename F>
-__device__ __forceinline__ void gemm_mfma_ops(f32x4 (&acc)[RT][CGW], const GemmOps<RT, CGW> &o, F &&dma) {
-  constexpr int NM = (C1 - C0) * kGemmTerms * RT;
+template <int RT, int CGW, int NT, int C0, int C1, int NI, typename F>
+__device__ __forceinline__ void gemm_mfma_ops(f32x4 (&acc)[RT][CGW], const GemmOps<RT, CGW, NT> &o, F &&dma) {
+  constexpr int NM = (C1 - C0) * NT * RT;
   if constexpr (NI > 0) dma(0);
   __builtin_amdgcn_sched_barrier(0);  // (a branch in dma(0) ends the block here)
 #pragma unroll
   for (int c = C0; c < C1; c++) {
 #pragma unroll
-    for (int t = 0; t < kGemmTerms; t++) {
+    for (int t = 0; t < NT; t++) {
 #pragma unroll
       for (int r = 0; r < RT; r++) {
         const i32x8 A = {(int)o.ar[r].x, (int)o.ar[r].y, (int)o.ar[r].z, (int)o.ar[r].w, 0, 0, 0, 0};
         // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
         acc[r][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, o.b[c].v[t], acc[r][c], 4, 2, 0, (int)o.sw[r], 0,
                                                                      (int)o.b[c].sc[t]);
-        const int m = ((c - C0) * kGemmTerms + t) * RT + r;
+        const int m = ((c - C0) * NT + t) * RT + r;
 #pragma unroll
         for (int i = 1; i < NI; i++) {
-          if (m == (i * NM) / NI - 1) {
+          // DMA i after MFMA (i NM) / NI - 1; with more DMAs than MFMAs (one term) several
+          // share an MFMA, the first ones MFMA 0
+          if (m == max((i * NM) / (NI > 0 ? NI : 1) - 1, 0)) {
             __builtin_amdgcn_sched_barrier(0);
             dma(i);
             __builtin_amdgcn_sched_barrier(0);
@@ -277,12 +296,12 @@ __device__ __forceinline__ void gemm_mfma_ops(f32x4 (&acc)[RT][CGW], const GemmO
 // row tile of the wavefront is inside the matrix (no test in the loop); otherwise row pairs from
 // nrt_valid on issue no MFMAs (a pair straddling the end computes its second tile on a clamped
 // tile, not stored).
-template <int RT, int CGW, int WR, int WC, int D, bool FULL>
+template <int RT, int CGW, int WR, int WC, int D, int NT, bool FULL>
 __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uint8_t *slot, int wr, int wc,
                                                 int lane, int sh, int nrt_valid) {
-  using S = GemmShape<RT, CGW, WR, WC, D>;
+  using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(RT % 2 == 0, "row tiles in pairs");
-  constexpr int CG = CGW;
+  constexpr int CG = CGW, kEntryStep = GemmRecT<NT>::kStep;
   const int j = lane & 15, g = lane >> 4;
   const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024,
                 *sb = slot + S::kBufB + S::kBufA + wr * RT * 256;
@@ -292,9 +311,9 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
   uint4 a1 = *reinterpret_cast<const uint4 *>(ab + 1024 + 16 * lane);
   uint32_t s0 = *reinterpret_cast<const uint32_t *>(sb + 4 * lane) >> sh;
   uint32_t s1 = *reinterpret_cast<const uint32_t *>(sb + 256 + 4 * lane) >> sh;
-  GemmB b[CG];
+  GemmB<NT> b[CG];
 #pragma unroll
-  for (int t = 0; t < kGemmTerms; t++) {
+  for (int t = 0; t < NT; t++) {
 #pragma unroll
     for (int c = 0; c < CG; c++) gemm_read_b_t(b[c], bb + 16 * c * kEntryStep, g, t);
   }
@@ -315,7 +334,7 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
       const i32x8 A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, 0, 0, 0, 0};
       const i32x8 A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w, 0, 0, 0, 0};
 #pragma unroll
-      for (int t = 0; t < kGemmTerms; t++) {
+      for (int t = 0; t < NT; t++) {
 #pragma unroll
         for (int c = 0; c < CG; c++) {
           // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
@@ -338,10 +357,11 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
 template <int MODE, typename S>
 constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP; }
 
-template <int MODE, int RT, int CGW, int WR, int WC, int D>
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
-  using S = GemmShape<RT, CGW, WR, WC, D>;
-  constexpr int W = S::W, CG = CGW;
+  using S = GemmShape<RT, CGW, WR, WC, D, NT>;
+  using G = GemmRecT<NT>;  // the activation records (x or h) of the launch
+  constexpr int W = S::W, CG = CGW, kChunks = G::kChunks, kEntryStep = G::kStep;
   // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
   // alias the reads of another, so those reads do not wait for it
   __shared__ __attribute__((aligned(1024))) uint8_t s_r0[S::kSlot];
@@ -558,9 +578,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     __builtin_amdgcn_sched_barrier(0);                                                              \
     GEMM_LOAD(min((st) + D - 1, ns - 1), nxt, (st) + D - 1 < ns);                                   \
     if constexpr (S::kBStat)                                                                        \
-      gemm_step_bstat<RT, CGW, WR, WC, D, false>(acc, cur, wr, wc, lane, 8 * ((st) & 3), nrt_valid); \
+      gemm_step_bstat<RT, CGW, WR, WC, D, NT, false>(acc, cur, wr, wc, lane, 8 * ((st) & 3), nrt_valid); \
     else                                                                                            \
-      gemm_step<RT, CGW, WR, WC, D>(acc, cur, S::kScale4 ? s_sc[((st) >> 2) & 1] : (cur) + S::kBufB + S::kBufA, \
+      gemm_step<RT, CGW, WR, WC, D, NT>(acc, cur, S::kScale4 ? s_sc[((st) >> 2) & 1] : (cur) + S::kBufB + S::kBufA, \
                                     wr, wc, lane, 8 * ((st) & 3));                                  \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));                                  \
@@ -608,15 +628,15 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   } while (0)
 #define GEMM_STEP2(st, cur, jj)                                                                     \
   do {                                                                                              \
-    GemmOps<RT, CGW> ops_;                                                                          \
-    gemm_read_ops<RT, CGW, WR, WC, D, kCSplit>(ops_, cur, s_sc[((st) >> 2) & 1], wr, wc, lane, 8 * (jj)); \
+    GemmOps<RT, CGW, NT> ops_;                                                                      \
+    gemm_read_ops<RT, CGW, WR, WC, D, NT, kCSplit>(ops_, cur, s_sc[((st) >> 2) & 1], wr, wc, lane, 8 * (jj)); \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     /* the first column groups' MFMAs run while the other groups' operands arrive */               \
-    GemmBRaw raw_[CGW - kCSplit];                                                                   \
+    GemmBRaw<NT> raw_[CGW - kCSplit];                                                               \
     _Pragma("unroll") for (int c_ = kCSplit; c_ < CGW; c_++)                                        \
       gemm_read_b_raw(raw_[c_ - kCSplit], cur + (16 * CGW * wc + (lane & 15) + 16 * c_) * kEntryStep, lane >> 4); \
     __builtin_amdgcn_sched_barrier(0);                                                              \
-    gemm_mfma_ops<RT, CGW, 0, kCSplit, 0>(acc, ops_, [](int) {});                                   \
+    gemm_mfma_ops<RT, CGW, NT, 0, kCSplit, 0>(acc, ops_, [](int) {});                               \
     _Pragma("unroll") for (int c_ = kCSplit; c_ < CGW; c_++)                                        \
       gemm_select_b(ops_.b[c_], raw_[c_ - kCSplit], lane >> 4);                                     \
     __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));                                                   \
@@ -624,9 +644,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     const int ld_ = (st) + 2;                                                                       \
     auto dma_ = [&](int k_) { dma2(k_, ld_, cur); };                                                \
     if ((st) + 2 < ns)                                                                              \
-      gemm_mfma_ops<RT, CGW, kCSplit, CGW, S::kDma + S::kDmaA + ((jj) == 2 ? S::kDmaA : 0)>(acc, ops_, dma_); \
+      gemm_mfma_ops<RT, CGW, NT, kCSplit, CGW, S::kDma + S::kDmaA + ((jj) == 2 ? S::kDmaA : 0)>(acc, ops_, dma_); \
     else                                                                                            \
-      gemm_mfma_ops<RT, CGW, kCSplit, CGW, 0>(acc, ops_, dma_);                                     \
+      gemm_mfma_ops<RT, CGW, NT, kCSplit, CGW, 0>(acc, ops_, dma_);                                 \
     const bool more_ = (st) + 2 < ns;                                                               \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     if (more_) GEMM_VM_WAIT(S::kDmaA + ((jj) == 2 ? S::kDmaA : 0));                                 \
@@ -689,12 +709,12 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   if constexpr (MODE == GEMV_GATE_UP) {
     // every 4 row tiles (64 rows) of the wavefront = h block hb (h values 32 hb .. 32 hb + 31)
     // of its entries. The SwiGLU values are staged in the (now free) ring as f32 [entry][32];
-    // then lane 2 e + h takes half h of entry e's block: the kGemmTerms E2M3 terms of its 16
+    // then lane 2 e + h takes half h of entry e's block: the NT E2M3 terms of its 16
     // values (block maximum shared with the neighbouring lane) go to the h record.
     static_assert(RT % 4 == 0, "whole h blocks per wavefront");
     constexpr int kWaveCols = 16 * CGW;  // entries of the wavefront
     static_assert(kWaveCols <= 32 || kWaveCols == 64, "one or two passes of 64 lanes");
-    static_assert(W <= 8 && 4 * kWaveCols * 128 <= S::kSlot, "staging fits in two ring slots");
+    static_assert(W <= 8 && (W < 4 ? W : 4) * kWaveCols * 128 <= S::kSlot, "staging fits in two ring slots");
     // with D = 3 the loop ends with one step's loads (the repeat of the last step) still in
     // flight into a ring slot, which may be a staging slot: every wavefront's loads complete
     // before any wavefront stages
@@ -755,13 +775,13 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
           m = fmaxf(m, fabsf(v[k]));
           bad = bad || !isfinite(v[k]);
         }
-        uint32_t dq[kGemmTerms][6], sb;
-        split32_fp6(v, m, bad, dq, sb);
+        uint32_t dq[NT][6], sb;
+        split32_fp6<NT>(v, m, bad, dq, sb);
         if (valid) {
           const int hb = t0 / 4 + hbk, st = hb >> 2, i = hb & 3;
           uint8_t *hr = hout + (size_t)(beg + e0 + e) * G::kBytes;
 #pragma unroll
-          for (int t = 0; t < kGemmTerms; t++) {
+          for (int t = 0; t < NT; t++) {
             *reinterpret_cast<uint4 *>(hr + G::dword(st, t, i, 0)) = make_uint4(dq[t][0], dq[t][1], dq[t][2], dq[t][3]);
             *reinterpret_cast<uint2 *>(hr + G::dword(st, t, i, 4)) = make_uint2(dq[t][4], dq[t][5]);
             hr[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
@@ -807,18 +827,18 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         }
         m = fmaxf(m, xor_lane<1>(m));
         bad = fmaxf(bad, xor_lane<1>(bad));
-        uint32_t dq[kGemmTerms][3], sb;
-        split16_fp6(v, m, bad != 0.0f, dq, sb);
+        uint32_t dq[NT][3], sb;
+        split16_fp6<NT>(v, m, bad != 0.0f, dq, sb);
         if (e < nloc) {
           uint8_t *hr = hout + (size_t)(beg + e0 + e) * G::kBytes;
 #pragma unroll
-          for (int t = 0; t < kGemmTerms; t++) {
+          for (int t = 0; t < NT; t++) {
 #pragma unroll
             for (int u = 0; u < 3; u++) *reinterpret_cast<uint32_t *>(hr + G::dword(st, t, i, 3 * h + u)) = dq[t][u];
           }
           if (h == 0) {
 #pragma unroll
-            for (int t = 0; t < kGemmTerms; t++) hr[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+            for (int t = 0; t < NT; t++) hr[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
           }
         }
       }
@@ -863,9 +883,9 @@ static int device_cus() {
   return cus[dev];
 }
 
-template <int MODE, int RT, int CGW, int WR, int WC, int D>
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT>
 static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
-  using S = GemmShape<RT, CGW, WR, WC, D>;
+  using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
   a.n_row_blocks = (int)((a.d.rows + S::kRows - 1) / S::kRows);
   const size_t col_tiles = (size_t)a.max_active + (a.n_entries + S::kCols - 1) / S::kCols;
@@ -877,7 +897,7 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   a.n_blocks = (int)blocks;
   // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
   const size_t grid = gemm_persistent<MODE, S>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -887,29 +907,36 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
 // with 32 or 16 entries, small enough (50-60 KB of LDS) for 2-3 blocks per CU, which keeps
 // every CU streaming weights when the grid is only a few blocks per CU (measured at 64, 128 and
 // 256 tokens against the 256-row blocks of 4 wavefronts: 4-10 % faster layers).
-template <int MODE>
+template <int MODE, int NT>
 static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   const size_t active = std::max<size_t>(1, std::min<size_t>((size_t)a.max_active, a.n_entries));
   const size_t mean = a.n_entries / active;
-  if (a.shape == 2) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3>(a, s);
-  if (a.shape == 3) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
-  if (a.shape == 4) {  // 128 rows in 4 wavefronts of 2 row tiles: down only (gate_up needs whole h blocks)
-    if constexpr (MODE == GEMV_GATE_UP) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3>(a, s);
-    else return launch_gemm_shape<MODE, 2, 1, 4, 1, 3>(a, s);
+  if constexpr (NT == kGemmTerms) {  // tuning shapes of the exact split only (the quantized mode
+                                      // takes its default shape for these codes)
+    if (a.shape == 2) return launch_gemm_shape<MODE, 4, 2, 4, 1, 3, NT>(a, s);
+    if (a.shape == 3) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3, NT>(a, s);
+    if (a.shape == 4) {  // 128 rows in 4 wavefronts of 2 row tiles: down only (gate_up needs whole h blocks)
+      if constexpr (MODE == GEMV_GATE_UP) return launch_gemm_shape<MODE, 4, 1, 4, 1, 3, NT>(a, s);
+      else return launch_gemm_shape<MODE, 2, 1, 4, 1, 3, NT>(a, s);
+    }
+    if (a.shape == 6) return launch_gemm_shape<MODE, 4, 1, 1, 1, 3, NT>(a, s);
+    if (a.shape == 8) return launch_gemm_shape<MODE, 16, 4, 2, 2, 2, NT>(a, s);
   }
-  if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3>(a, s);
-  if (a.shape == 6) return launch_gemm_shape<MODE, 4, 1, 1, 1, 3>(a, s);
-  if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3>(a, s);
-  if (a.shape == 8) return launch_gemm_shape<MODE, 16, 4, 2, 2, 2>(a, s);
+  if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
+  if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
   if (mean >= 48)
-    return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2>(a, s);
-  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3>(a, s);
-  return launch_gemm_shape<MODE, 4, 1, 2, 1, 3>(a, s);
+    return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
+  if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
+  return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
 }
 
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s) {
   if (a.d.ns > (uint32_t)kGemmNs || (mode == GEMV_GATE_UP && a.d.rows % 64)) return hipErrorInvalidValue;
-  return mode == GEMV_GATE_UP ? launch_gemm_mode<GEMV_GATE_UP>(a, s) : launch_gemm_mode<GEMV_DOWN>(a, s);
+  if (a.terms == 1)
+    return mode == GEMV_GATE_UP ? launch_gemm_mode<GEMV_GATE_UP, 1>(a, s) : launch_gemm_mode<GEMV_DOWN, 1>(a, s);
+  if (a.terms != kGemmTerms) return hipErrorInvalidValue;
+  return mode == GEMV_GATE_UP ? launch_gemm_mode<GEMV_GATE_UP, kGemmTerms>(a, s)
+                              : launch_gemm_mode<GEMV_DOWN, kGemmTerms>(a, s);
 }
 
 }  // namespace moe

@@ -212,7 +212,10 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
         xv[4 * q + 2] = k0 + 4 * q + 2 < H ? x4.z : 0.0f;
         xv[4 * q + 3] = k0 + 4 * q + 3 < H ? x4.w : 0.0f;
       }
-      rec_split_block(xv, blk, a.xrec + (size_t)(t0 + tb) * GemmRec::kBytes);
+      if (a.rec_terms == 1)
+        rec_split_block<1>(xv, blk, a.xrec + (size_t)(t0 + tb) * GemmRecT<1>::kBytes);
+      else
+        rec_split_block<kGemmTerms>(xv, blk, a.xrec + (size_t)(t0 + tb) * GemmRec::kBytes);
     }
   }
   if constexpr (KI > 0) {

@@ -25,7 +25,8 @@ struct RouteArgs {
   int32_t *idx;          // [T, k]
   float *wts;            // [T, k]
   uint16_t *xsplit;      // [T, 2, H] bf16 hi / lo
-  uint8_t *xrec;         // [T] GemmRec records of x (grouped GEMM operands; H <= 128 kGemmNs)
+  uint8_t *xrec;         // [T] GemmRecT<rec_terms> records of x (grouped GEMM operands; H <= 128 kGemmNs)
+  int rec_terms;         // kGemmTerms (exact split) or 1 (one MXFP6 term per value)
   int fuse_bucket;       // T == 1: also write the expert list
   int32_t *n_active, *active_ids, *active_off, *entry_src, *pos;
   uint32_t *bucket_ticket;  // T > 1: zeroed counter; the last block buckets (route_bucket_fits)
@@ -53,28 +54,32 @@ struct GemvArgs {
 constexpr int kTerms = 4;
 
 // Step-major activation record of one row (token or entry) for the grouped GEMM (gemm.hip):
-// kGemmTerms fp6 (E2M3) terms per value, rows of up to 4 * kGemmNs 32-value blocks. The B operand
-// of block 4s + b (b = 0..3, the MFMA lane group b: K = 32 b + u, value u at bits 6u) is 6 dwords;
+// NT fp6 (E2M3) terms per value, rows of up to 4 * kGemmNs 32-value blocks. The B operand of
+// block 4s + b (b = 0..3, the MFMA lane group b: K = 32 b + u, value u at bits 6u) is 6 dwords;
 // K-step s holds, per term t, 96 bytes: dwords 0-3 of blocks 0..3 (16 bytes each, block b at 16 b),
 // then dwords 4-5 of blocks 0..3 (8 bytes each, at 64 + 8 b); then [term t][4 scale bytes, byte
-// i = E8M0 of block 4s+i] (12 bytes) and 4 pad bytes. A step is kChunks 16-byte chunks: chunk
-// 6t + b = the first 16 bytes of block b, chunk 6t + 4 + (b >> 1) = the last 8 bytes of blocks b
-// and b ^ 1, chunk 18 = the scales (the grouped GEMM stages them chunk by chunk). Blocks past the
-// row are zero.
+// i = E8M0 of block 4s+i] (4 NT bytes) and pad bytes to 16. A step is kChunks 16-byte chunks:
+// chunk 6t + b = the first 16 bytes of block b, chunk 6t + 4 + (b >> 1) = the last 8 bytes of
+// blocks b and b ^ 1, chunk 6 NT = the scales (the grouped GEMM stages them chunk by chunk).
+// Blocks past the row are zero. NT = kGemmTerms: the exact split (the default); NT = 1: the
+// quantized-activation mode (one MXFP6 term per value).
 constexpr int kGemmNs = 24;
 constexpr int kGemmTerms = 3;
-struct GemmRec {
+template <int NT>
+struct GemmRecT {
+  static constexpr int kNT = NT;
   static constexpr int kTermBytes = 96;
-  static constexpr int kStep = kGemmTerms * kTermBytes + 16;
+  static constexpr int kStep = NT * kTermBytes + 16;
   static constexpr int kChunks = kStep / 16;
   static constexpr int kBytes = kGemmNs * kStep;
   // byte offset of dword d (0..5) of the B operand of block b (0..3) of step s, term t
   MOE_HD static constexpr int dword(int s, int t, int b, int d) {
     return s * kStep + t * kTermBytes + (d < 4 ? 16 * b + 4 * d : 64 + 8 * b + 4 * (d - 4));
   }
-  MOE_HD static constexpr int scale(int s, int t) { return s * kStep + kGemmTerms * kTermBytes + 4 * t; }
+  MOE_HD static constexpr int scale(int s, int t) { return s * kStep + NT * kTermBytes + 4 * t; }
+  static_assert(NT >= 1 && NT <= 3 && kStep % 16 == 0 && kChunks == 6 * NT + 1, "record chunks");
 };
-static_assert(GemmRec::kStep % 16 == 0 && GemmRec::kChunks == 6 * kGemmTerms + 1, "record chunks");
+using GemmRec = GemmRecT<kGemmTerms>;
 
 struct GemmArgs {
   const uint8_t *base;       // expert records of the layer
@@ -92,6 +97,7 @@ struct GemmArgs {
   int n_row_blocks;          // set by launch_gemm_fp8: row blocks of the launch
   int n_tiles;               //                         row blocks x column tiles
   int n_blocks;              //                         workgroups of the tile order (>= n_tiles)
+  int terms;                 // E2M3 terms per activation value: kGemmTerms, or 1 (quantized mode)
 };
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
 

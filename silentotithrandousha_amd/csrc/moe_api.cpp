@@ -130,7 +130,8 @@ struct moe_ctx {
   int gemm_shape = 0;  // grouped GEMM block shape override (tuning)
   int matvec_one_launch = 1;  // moe_mxfp4_matvec_device: one launch (1) or split + GEMV (0)
   int gemm_band = 0;
-  int gemm_shape_down = 0;  // block shape of the down GEMM (0: as gemm_shape)   // grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)
+  int gemm_shape_down = 0;  // block shape of the down GEMM (0: as gemm_shape)
+  int act_quant = 0;  // grouped GEMM activations: 0 the exact kGemmTerms split, 1 one MXFP6 term
   DevBuf route_ticket;  // k_route's block counter for the fused bucketing, zero between launches
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
@@ -512,6 +513,7 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
                         (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   ra.xsplit = use_gemm ? nullptr : w.xsplit;
   ra.xrec = use_gemm ? w.xrec : nullptr;  // the router writes the GEMM's activation records
+  ra.rec_terms = c->act_quant ? 1 : kGemmTerms;
   ra.fuse_bucket = T == 1;
   ra.n_active = w.n_active;
   ra.active_ids = w.active_ids;
@@ -542,6 +544,7 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
     ga.n_entries = N;
     ga.shape = c->gemm_shape;
     ga.band = c->gemm_band;  // default: gate_up in workgroup order, down in XCD bands of 1 row block
+    ga.terms = c->act_quant ? 1 : kGemmTerms;
     GemmArgs gu = ga;
     gu.mat_off = c->L.gu_off;
     gu.bias_off = c->L.gub_off;
@@ -1178,6 +1181,18 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
     case MOE_OPT_MATVEC:
       if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_MATVEC is 0 or 1");
       c->matvec_one_launch = (int)value;
+      return MOE_OK;
+    case MOE_OPT_ACT_QUANT:
+      if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_ACT_QUANT is 0 or 1");
+      if ((int)value != c->act_quant && c->w.hrec) {
+        // the two record layouts place h blocks differently, and the padding blocks past I, which
+        // no kernel writes, must read as zeros in the new one
+        if (c->capturing) return fail(MOE_ERR_STATE, "MOE_OPT_ACT_QUANT cannot change during graph capture");
+        RETURN_IF(use_dev(c));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        HIP_TRY(hipMemset(c->w.hrec, 0, c->w.hrec_bytes));
+      }
+      c->act_quant = (int)value;
       return MOE_OK;
     case MOE_OPT_SPIN_LIMIT:
       if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");

@@ -176,6 +176,13 @@ class GpuMoeDispatcher:
         from ._ffi import MOE_OPT_MATVEC
         check(lib().moe_set_option(self._ctx, MOE_OPT_MATVEC, int(one_launch)))
 
+    def set_act_quant(self, on):
+        """Grouped GEMM activations: 0 / False exact to ~2^-13 of each block maximum (default);
+        1 / True quantized to MXFP6 (one E2M3 value per element, OCP MX block scale), whose results
+        follow the f32 path applied to the quantized activations. Other values are refused."""
+        from ._ffi import MOE_OPT_ACT_QUANT
+        check(lib().moe_set_option(self._ctx, MOE_OPT_ACT_QUANT, int(on)))
+
     def set_spin_limit(self, polls):
         from ._ffi import MOE_OPT_SPIN_LIMIT
         check(lib().moe_set_option(self._ctx, MOE_OPT_SPIN_LIMIT, int(polls)))

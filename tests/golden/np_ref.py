@@ -95,3 +95,37 @@ def moe_layer(x, layer, k, limit=7.0):
                              layer["d_blocks"][e], layer["d_scales"][e], layer["d_bias"][e], limit)
             y[t] += w[t, s] * out[0]
     return y, logits, idx, w
+
+
+def e2m3_grid():
+    """The 32 E2M3 magnitudes in code order (code = exponent bits << 3 | mantissa bits, bias 1):
+    exponent 0 gives mantissa / 8, exponent e > 0 gives (1 + mantissa / 8) 2^(e - 1)."""
+    c = np.arange(32)
+    e, m = c >> 3, c & 7
+    return np.where(e == 0, m / 8.0, (1.0 + m / 8.0) * 2.0 ** (e - 1))
+
+
+def quant_mxfp6(x):
+    """MXFP6 values of x (last axis in blocks of 32, a multiple of 32): per block the OCP MX scale
+    2^(floor(log2 amax) - emax) with E2M3's emax = 2 (2^-3 for an all-zero block), then each
+    scaled value replaced by the nearest grid magnitude, a tie going to the even code, values past
+    the largest magnitude clamped to it; a block holding a non-finite value becomes NaN."""
+    x = np.asarray(x, np.float64)
+    xb = x.reshape(-1, 32)
+    grid = e2m3_grid()
+    out = np.empty_like(xb)
+    for i, blk in enumerate(xb):
+        if not np.all(np.isfinite(blk)):
+            out[i] = np.nan
+            continue
+        amax = np.abs(blk).max()
+        s = 2.0 ** (np.floor(np.log2(amax)) - 2) if amax > 0 else 2.0 ** -3
+        s = max(s, 2.0 ** -126)
+        a = np.minimum(np.abs(blk) / s, grid[-1])
+        d = np.abs(a[:, None] - grid[None, :])
+        best = d.min(axis=1, keepdims=True)
+        cand = d == best                       # one code, or two at a tie
+        code = np.where(cand[:, ::2].any(axis=1) & (cand.sum(axis=1) > 1),
+                        np.argmax(cand & (np.arange(32) % 2 == 0), axis=1), np.argmax(cand, axis=1))
+        out[i] = np.sign(blk) * grid[code] * s
+    return out.reshape(x.shape)

@@ -698,6 +698,70 @@ def test_prefill_2048_tokens_120b(orc):
         d.close()
 
 
+# ---------------------------------------------------------------- quantized activations (opt-in)
+
+def _act_quant_check(orc, d, layer, x, k, what, n_sample=None, seed=0, shapes=()):
+    """MOE_OPT_ACT_QUANT 1: top-k exact; the output (or n_sample sampled tokens) within the
+    tolerance of the fp32 path on MXFP6 activations (orc.moe_layer_mxfp6: the GPU and the oracle
+    quantize the same x to the same codes; h differs by summation order, so an h value at a
+    rounding midpoint may take the neighbouring code); the forced shapes bit-identical; the
+    exact mode afterwards bit-identical to before (the h records are re-laid out)."""
+    d.set_batch_gemm(1)
+    d.set_gemm_shape(0)
+    exact = d.layer_forward(0, x, k)
+    d.set_act_quant(1)
+    try:
+        got = d.layer_forward(0, x, k)
+        for shape, down in shapes:
+            d.set_gemm_shape(shape, down)
+            assert np.array_equal(d.layer_forward(0, x, k), got), f"{what}: shape {shape} down {down}"
+        d.set_gemm_shape(0)
+    finally:
+        d.set_act_quant(0)
+    assert np.array_equal(d.layer_forward(0, x, k), exact), f"{what}: exact mode after the quantized one"
+    rows = np.arange(x.shape[0])
+    if n_sample:
+        rows = np.sort(np.random.default_rng(seed).choice(x.shape[0], n_sample, replace=False))
+    want, _, idx, _ = orc.moe_layer_mxfp6(x[rows], layer, k)
+    gidx, _ = d.router_topk(0, x[rows], k)
+    assert np.array_equal(gidx, idx)
+    # measured ~1e-7 (no code differs); one h value on its neighbouring code moves its token's
+    # output by ~1e-3 / sqrt(entries), so 2e-4 leaves room for a few
+    e = assert_rel_l2(got[rows], want, f"{what} vs mxfp6 oracle", tol=2e-4)
+    strict = rel_l2(got[rows], orc.moe_layer(x[rows], layer, k)[0])
+    print(f"{what}: rel-L2 {e:.2e} vs the MXFP6 oracle, {strict:.2e} vs the fp32 path")
+    return e
+
+
+@pytest.mark.parametrize("shape", [(512, 512, 16, 4, 300), (256, 256, 8, 4, 64)])
+def test_act_quant_small(orc, shape):
+    H, I, E, k, T = shape
+    L = syn.make_layer(H, I, E, seed=480 + T, scale_lo=120, scale_hi=126, router_sigma=0.1)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    try:
+        d.preload_layer(0, L)
+        x = syn.hidden(T, H, seed=481 + T)
+        _act_quant_check(orc, d, L, x, k, f"act_quant {shape}",
+                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5)])
+    finally:
+        d.close()
+
+
+def test_act_quant_20b_decode64_and_prefill(orc, disp20, layer20):
+    """The 20B layer at 64 tokens (128- and 256-row shapes) and at 4096 tokens (the 512-row x
+    64-entry shape at K = 2880), quantized activations."""
+    _act_quant_check(orc, disp20, layer20, syn.hidden(64, H20, seed=490), 4, "act_quant 20B T=64",
+                     shapes=[(5, 5), (7, 7), (7, 5)])
+    _act_quant_check(orc, disp20, layer20, syn.hidden(4096, H20, seed=491), 4, "act_quant 20B T=4096",
+                     n_sample=48, seed=492, shapes=[(1, 0), (1, 7)])
+
+
+def test_act_quant_option_checks(disp20):
+    from silentotithrandousha_amd._ffi import MoeError
+    with pytest.raises(MoeError, match="ACT_QUANT"):
+        disp20.set_act_quant(2)
+
+
 def test_invalid_calls_leave_context_usable(orc, disp20, layer20):
     """Calls refused for their arguments (top-k 0 or above the expert count, a layer never
     loaded) change nothing: the next valid call of each size still matches the oracle."""

@@ -459,3 +459,79 @@ def test_rms_norm_rows_and_block_residual(orc):
     out, lg, idx, w = orc.moe_block(x, L, 2, g, 1e-5)
     y, lg2, idx2, w2 = orc.moe_layer(n, L, 2)
     assert np.array_equal(out, x + y) and np.array_equal(lg, lg2) and np.array_equal(idx, idx2)
+
+
+# ---------------------------------------------------------------- MXFP6 activations (quantized mode)
+
+def test_quant_mxfp6_grid_ties_saturation(orc):
+    """Closed forms of the MXFP6 rule: a block whose maximum is 7.5 2^s holds every E2M3 value
+    times 2^s exactly (a scale one step too coarse would lose the 1/8 steps); midpoints between
+    neighbouring values go to the even code; magnitudes in (7.5, 8) 2^s saturate to 7.5 2^s; an
+    all-zero block stays zero; a non-finite value makes its own block NaN and no other."""
+    grid = np_ref.e2m3_grid()
+    for s in (-20, -3, 0, 5, 40):
+        blk = (np.where(np.arange(32) % 2, -1, 1) * grid * 2.0 ** s).astype(np.float32)
+        blk[31] = np.float32(7.5 * 2.0 ** s)
+        assert np.array_equal(orc.quant_mxfp6(blk[None])[0], blk)
+    mids = (grid[:-1] + grid[1:]) / 2
+    blk = np.concatenate([[7.5], mids[:31]]).astype(np.float32)
+    got = orc.quant_mxfp6(blk[None])[0]
+    lo, hi = grid[:31], grid[1:32]
+    even = np.where(np.arange(31) % 2 == 0, lo, hi)  # code i even -> lo
+    assert np.array_equal(got[1:], even.astype(np.float32))
+    sat = np.array([[7.9, 7.6, 7.5001, -7.99] + [1.0] * 28], np.float32)
+    assert np.array_equal(orc.quant_mxfp6(sat)[0, :4], np.array([7.5, 7.5, 7.5, -7.5], np.float32))
+    z = np.zeros((1, 64), np.float32)
+    z[0, 40] = np.inf
+    q = orc.quant_mxfp6(z)
+    assert np.all(q[0, :32] == 0) and np.all(np.isnan(q[0, 32:]))
+    # a value needing the small steps beside a large maximum: 1.1 -> 1.125 at scale 1
+    assert orc.quant_mxfp6(np.array([[7.0, 1.1] + [0.0] * 30], np.float32))[0, 1] == np.float32(1.125)
+
+
+def test_quant_mxfp6_matches_float64_table_rule(orc):
+    """Random rows over 60 binades against np_ref.quant_mxfp6 (nearest of the 32-entry grid table
+    with ties to even codes, an independent formulation): bit-exact, as every MXFP6 value is a
+    float32; a partial last block in the oracle equals the zero-padded block."""
+    rng = np.random.default_rng(60)
+    x = (rng.standard_normal((64, 320)) * 2.0 ** rng.integers(-30, 30, (64, 1))).astype(np.float32)
+    x[::7, ::5] *= 40.0
+    want = np_ref.quant_mxfp6(x.astype(np.float64)).astype(np.float32)
+    assert_bit_exact(orc.quant_mxfp6(x), want, "mxfp6 vs table rule")
+    part = orc.quant_mxfp6(x[:, :300])
+    pad = orc.quant_mxfp6(np.concatenate([x[:, :300], np.zeros((64, 20), np.float32)], axis=1))[:, :300]
+    assert_bit_exact(part, pad, "partial last block")
+
+
+def test_oracle_mxfp6_expert_and_layer(orc):
+    """The quantized-activation expert and layer: the expert equals the fp32 expert on
+    quant_mxfp6(x) up to the h quantization (checked against a float64 expert whose x and h are
+    quantized by the table rule); the layer routes on the unquantized x (same indices and weights
+    as the fp32 layer) and combines the quantized experts."""
+    H, I, E, k, T = 256, 128, 8, 4, 6
+    L = syn.make_layer(H, I, E, seed=61, scale_lo=120, scale_hi=126, router_sigma=0.2)
+    x = syn.hidden(T, H, seed=62)
+    e = 3
+    y6, h6 = orc.expert_ffn(x, L["gu_blocks"][e], L["gu_scales"][e], L["gu_bias"][e], L["d_blocks"][e],
+                            L["d_scales"][e], L["d_bias"][e], H, I, want_h=True, mxfp6=True)
+    xq = np_ref.quant_mxfp6(x.astype(np.float64))
+    gu = xq @ np_ref.decode(L["gu_blocks"][e], L["gu_scales"][e]).T + L["gu_bias"][e]
+    gate, up = np.minimum(gu[:, 0::2], 7.0), np.clip(gu[:, 1::2], -7.0, 7.0)
+    h = (up + 1.0) * gate / (1.0 + np.exp(-1.702 * gate))
+    hq = np_ref.quant_mxfp6(h)
+    assert np.mean(h6 == hq.astype(np.float32)) > 0.99     # f32 vs float64 h: rare rounding flips
+    yq = np.clip(hq @ np_ref.decode(L["d_blocks"][e], L["d_scales"][e]).T + L["d_bias"][e], -65504, 65504)
+    assert rel_l2(y6, yq) < 1e-3
+    assert rel_l2(y6, np_ref.expert_ffn(x, L["gu_blocks"][e], L["gu_scales"][e], L["gu_bias"][e],
+                                        L["d_blocks"][e], L["d_scales"][e], L["d_bias"][e])) > 1e-3
+    yl, lg, idx, w = orc.moe_layer_mxfp6(x, L, k)
+    yf, lgf, idxf, wf = orc.moe_layer(x, L, k)
+    assert np.array_equal(idx, idxf) and np.array_equal(w, wf) and np.array_equal(lg, lgf)
+    want = np.zeros((T, H))
+    for t in range(T):
+        for s in range(k):
+            ee = idx[t, s]
+            want[t] += w[t, s] * orc.expert_ffn(x[t], L["gu_blocks"][ee], L["gu_scales"][ee], L["gu_bias"][ee],
+                                                L["d_blocks"][ee], L["d_scales"][ee], L["d_bias"][ee], H, I,
+                                                mxfp6=True)[0]
+    assert rel_l2(yl, want) < 1e-6
