@@ -714,7 +714,10 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     static_assert(RT % 4 == 0, "whole h blocks per wavefront");
     constexpr int kWaveCols = 16 * CGW;  // entries of the wavefront
     static_assert(kWaveCols <= 32 || kWaveCols == 64, "one or two passes of 64 lanes");
-    static_assert(W <= 8 && (W < 4 ? W : 4) * kWaveCols * 128 <= S::kSlot, "staging fits in two ring slots");
+    // staging rows of kRow floats (36, not 32: 16 consecutive rows' 16-byte reads then hit
+    // distinct banks, and their 8-byte writes two ways at most)
+    constexpr int kRow = 36;
+    static_assert(W <= 8 && (W < 4 ? W : 4) * kWaveCols * kRow * 4 <= S::kSlot, "staging fits in two ring slots");
     // with D = 3 the loop ends with one step's loads (the repeat of the last step) still in
     // flight into a ring slot, which may be a staging slot: every wavefront's loads complete
     // before any wavefront stages
@@ -732,7 +735,6 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     // entry) splits the whole 32-value block (split32_fp6: a third fewer instructions than two
     // 16-value halves) and stores each term's 24 bytes as one 16- and one 8-byte store.
     constexpr int NHB = RT / 4;                        // h blocks of the wavefront
-    constexpr int kRow = 36;                           // staging row stride (floats)
     constexpr int kStageW = NHB * kWaveCols * kRow * 4;  // staging bytes per wavefront
     constexpr int kHalf = W > 1 ? W / 2 : 1;           // wavefronts per ring slot
     if constexpr (kHalf * kStageW <= S::kSlot && NHB * kWaveCols <= 64) {  // one lane pass
@@ -789,7 +791,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         }
       }
     } else {
-    float *stage = reinterpret_cast<float *>((wv < 4 ? s_r0 : s_r1) + (wv & 3) * kWaveCols * 128);
+    float *stage = reinterpret_cast<float *>((wv < 4 ? s_r0 : s_r1) + (wv & 3) * kWaveCols * kRow * 4);
 #pragma unroll
     for (int hbk = 0; hbk < RT / 4; hbk++) {
       if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
@@ -797,7 +799,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 #pragma unroll
       for (int c = 0; c < CG; c++) {
         if (16 * c >= nloc) break;
-        float *se = stage + (16 * c + j) * 32;
+        float *se = stage + (16 * c + j) * kRow;
 #pragma unroll
         for (int r = 0; r < 4; r++) {  // h values 8r + 2g, 8r + 2g + 1 of the block
           const f32x4 &av = acc[4 * hbk + r][c];
@@ -813,7 +815,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const float4 x = *reinterpret_cast<const float4 *>(stage + min(e, kWaveCols - 1) * 32 + 16 * h + 4 * q);
+          const float4 x = *reinterpret_cast<const float4 *>(stage + min(e, kWaveCols - 1) * kRow + 16 * h + 4 * q);
           v[4 * q] = x.x;
           v[4 * q + 1] = x.y;
           v[4 * q + 2] = x.z;
@@ -921,6 +923,12 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
     }
     if (a.shape == 6) return launch_gemm_shape<MODE, 4, 1, 1, 1, 3, NT>(a, s);
     if (a.shape == 8) return launch_gemm_shape<MODE, 16, 4, 2, 2, 2, NT>(a, s);
+  }
+  // one activation term: 512 rows x 128 entries, a wavefront holding 128 x 64 (twice the entries
+  // per A read of the 512 x 64 block; with three terms its operands do not fit the registers of
+  // two wavefronts per SIMD). Measured at prefill: gate_up 322 -> 297 us, down 203 -> 181 us.
+  if constexpr (NT == 1) {
+    if (a.shape == 9 || (a.shape == 0 && mean >= 96)) return launch_gemm_shape<MODE, 8, 4, 4, 2, 2, NT>(a, s);
   }
   if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
   if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);

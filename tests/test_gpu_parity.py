@@ -742,7 +742,7 @@ def test_act_quant_small(orc, shape):
         d.preload_layer(0, L)
         x = syn.hidden(T, H, seed=481 + T)
         _act_quant_check(orc, d, L, x, k, f"act_quant {shape}",
-                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5)])
+                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9)])
     finally:
         d.close()
 
@@ -753,7 +753,7 @@ def test_act_quant_20b_decode64_and_prefill(orc, disp20, layer20):
     _act_quant_check(orc, disp20, layer20, syn.hidden(64, H20, seed=490), 4, "act_quant 20B T=64",
                      shapes=[(5, 5), (7, 7), (7, 5)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(4096, H20, seed=491), 4, "act_quant 20B T=4096",
-                     n_sample=48, seed=492, shapes=[(1, 0), (1, 7)])
+                     n_sample=48, seed=492, shapes=[(1, 0), (1, 7), (9, 9), (9, 0)])
 
 
 def test_act_quant_option_checks(disp20):
