@@ -1,9 +1,10 @@
 // Beaver-triple generation over p = 2^31 - 1 for gfx950 (include/beaver32.h): the GPU backend
 // GpuTripleGen32 of the reference (src/gpu/mod.rs:511-1012; kernels shader32.metal:75-167).
 //
-// One thread per output triple k (round r = k / spr, j = k % spr), so a wavefront's stores are
-// 64 consecutive words of each output array; a block takes 64 whole rounds. The field products are exact 32 x 32 -> 64-bit
-// multiplies folded by 2^31 = 1 (mod p); every value is kept in [0, p).
+// A thread produces triple j of 16 rounds 64 apart, so each pass of a wavefront stores 64
+// consecutive words of each output array; a block takes 1024 whole rounds. The field products
+// are exact 32 x 32 -> 64-bit multiplies folded by 2^31 = 1 (mod p), those by the parties'
+// evaluation points 1..8 sums of 31-bit rotations; every value is kept in [0, p).
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -67,53 +68,80 @@ __device__ __forceinline__ uint32_t chash32_m(uint32_t seed, uint32_t idx_mul) {
   return x >= kP ? x - kP : x;
 }
 
-// A block takes kRounds consecutive rounds (SPR triples each, one thread per triple). bt_r is
-// the SIMD-group reduction of the reference kernel: lanes i < n of a threadgroup of `group`
-// rounds hold H(seed of round r0 + i, 3i), and the reduction over 8 lanes (xor 1, 2, 4) gives
-// the first 8 rounds of the threadgroup sum_i him[j][i] H(...) and every other round 0 (its
-// lanes are inactive, weight 0); rounds past num_rounds add nothing. The block's threadgroups
-// (at most kRounds / group + 1 of them) get their hashes and sums once, in LDS.
-constexpr uint32_t kRounds = 64;
+// c * 2^k mod p for c in [0, p), k in [0, 30]: 2^31 = 1 (mod p), so the product is c rotated
+// left by k within 31 bits (a 31-bit pattern other than all ones stays below p).
+__device__ __forceinline__ uint32_t frot(uint32_t c, uint32_t k) {
+  return k ? ((c << k) | (c >> (31u - k))) & kP : c;
+}
+
+// c * x mod p for a small wavefront-uniform x (the parties' evaluation points 1..8): a sum of
+// rotations by the set bits of x, each a field value, instead of a 32 x 32 -> 64-bit product
+// (two quarter-rate multiplies). Equal to fmul(c, x) for every c in [0, p).
+__device__ __forceinline__ uint32_t fmul_small(uint32_t c, uint32_t x) {
+  uint32_t r = (x & 1u) ? c : 0u;
+  if (x & 2u) r = fadd(r, frot(c, 1));
+  if (x & 4u) r = fadd(r, frot(c, 2));
+  if (x & 8u) r = fadd(r, frot(c, 3));
+  return r;
+}
+
+// A block takes kRounds = 64 kIter consecutive rounds: thread (kl, j) of its 64 SPR threads
+// produces triple j of rounds R0 + kl + 64 m, m = 0 .. kIter - 1, so each pass of a wavefront
+// stores 64 consecutive words of each output array. bt_r is the SIMD-group reduction of the
+// reference kernel: lanes i < n of a threadgroup of `group` rounds hold H(seed of round
+// r0 + i, 3i), and the reduction over 8 lanes (xor 1, 2, 4) gives the first 8 rounds of the
+// threadgroup sum_i him[j][i] H(...) and every other round 0 (its lanes are inactive, weight
+// 0); rounds past num_rounds add nothing. The block's threadgroups (at most kRounds / group + 1
+// of them) get their hashes and sums once, in LDS, before the passes.
+constexpr uint32_t kIter = 16;
+constexpr uint32_t kRounds = 64 * kIter;
+constexpr uint32_t kMaxGroups = kRounds / 32 + 1;  // threadgroups of 32 rounds a block overlaps
 
 template <int SPR>
 __global__ __launch_bounds__(64 * SPR) void k_beaver32(TripleArgs a) {
-  __shared__ uint32_t s_rt[3][8];
-  __shared__ uint32_t s_bt[3][3];
+  __shared__ uint32_t s_rt[kMaxGroups][8];
+  __shared__ uint32_t s_bt[kMaxGroups][SPR];
   const uint32_t R0 = blockIdx.x * kRounds, tid = threadIdx.x;
-  const uint32_t g0 = R0 / a.group;  // first threadgroup of the reference overlapping the block
-  if (tid < 3 * 8) {  // hashes of the first n rounds of threadgroups g0, g0 + 1, g0 + 2
-    const uint32_t gi = tid / 8, i = tid % 8, r = (g0 + gi) * a.group + i;
+  // group < 32 only when num_rounds < 32: a single block, whose rounds lie in group 0
+  const uint32_t g0 = a.group == 32u ? R0 / 32u : 0u;  // first threadgroup overlapping the block
+  const uint32_t ng = a.group == 32u ? kMaxGroups : 1u;
+  for (uint32_t u = tid; u < ng * 8u; u += 64u * SPR) {  // hashes of each group's first n rounds
+    const uint32_t gi = u / 8u, i = u % 8u, r = (g0 + gi) * a.group + i;
     s_rt[gi][i] = i < a.n && r < a.num_rounds && i < a.group ? chash32(a.seeds[r], 3u * i) : 0u;
   }
   __syncthreads();
-  if (tid < 3 * SPR) {
-    const uint32_t gi = tid / SPR, j = tid % SPR;
+  for (uint32_t u = tid; u < ng * SPR; u += 64u * SPR) {
+    const uint32_t gi = u / SPR, j = u % SPR;
     uint32_t acc = 0u;
     for (uint32_t i = 0; i < a.n; i++) acc = fadd(acc, fmul(a.him[j][i], s_rt[gi][i]));
     s_bt[gi][j] = acc;
   }
   __syncthreads();
-  const uint32_t kl = tid / SPR, j = tid - kl * SPR;  // round within the block, triple within it
-  const uint32_t r = R0 + kl, k = r * SPR + j;
-  if (k >= a.count) return;
-  const uint32_t seed = a.seeds[r];
-  const uint32_t a0 = chash32_m(seed, a.hmul[j][0]), b0 = chash32_m(seed, a.hmul[j][1]);
-  const uint32_t ca = chash32_m(seed, a.hmul[j][2]), cb = chash32_m(seed, a.hmul[j][3]);
-  const uint32_t lane = r % a.group;
-  const uint32_t bt = lane < 8 ? s_bt[r / a.group - g0][j] : 0u;
-  const uint32_t ab = fmul(a0, b0);
-  if (a.party >= 0) {
-    const uint32_t x = a.eval[a.party];
-    a.a[k] = fadd(a0, fmul(ca, x));
-    a.b[k] = fadd(b0, fmul(cb, x));
-    a.c[k] = fadd(ab, fmul(x, bt));
-  } else {
-    for (uint32_t p = 0; p < a.n; p++) {
-      const uint32_t x = a.eval[p];
-      const size_t o = (size_t)p * a.count + k;
-      a.a[o] = fadd(a0, fmul(ca, x));
-      a.b[o] = fadd(b0, fmul(cb, x));
-      a.c[o] = fadd(ab, fmul(x, bt));
+  const uint32_t kl = tid / SPR, j = tid - kl * SPR;  // round within a pass, triple within it
+  const uint32_t h0 = a.hmul[j][0], h1 = a.hmul[j][1], h2 = a.hmul[j][2], h3 = a.hmul[j][3];
+  for (uint32_t m = 0; m < kIter; m++) {
+    const uint32_t r = R0 + 64u * m + kl, k = r * SPR + j;
+    if (k >= a.count) return;  // rounds increase with m
+    const uint32_t seed = a.seeds[r];
+    const uint32_t a0 = chash32_m(seed, h0), b0 = chash32_m(seed, h1);
+    const uint32_t ca = chash32_m(seed, h2), cb = chash32_m(seed, h3);
+    // lane r % group of threadgroup r / group (group = 32, or the one group of a short call)
+    const uint32_t lane = a.group == 32u ? (r & 31u) : r;
+    const uint32_t bt = lane < 8u ? s_bt[a.group == 32u ? (r >> 5) - g0 : 0u][j] : 0u;
+    const uint32_t ab = fmul(a0, b0);
+    if (a.party >= 0) {
+      const uint32_t x = a.eval[a.party];
+      a.a[k] = fadd(a0, fmul_small(ca, x));
+      a.b[k] = fadd(b0, fmul_small(cb, x));
+      a.c[k] = fadd(ab, fmul_small(bt, x));
+    } else {
+      for (uint32_t p = 0; p < a.n; p++) {
+        const uint32_t x = a.eval[p];
+        const size_t o = (size_t)p * a.count + k;
+        a.a[o] = fadd(a0, fmul_small(ca, x));
+        a.b[o] = fadd(b0, fmul_small(cb, x));
+        a.c[o] = fadd(ab, fmul_small(bt, x));
+      }
     }
   }
 }
