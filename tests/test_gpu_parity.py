@@ -748,10 +748,13 @@ def test_act_quant_small(orc, shape):
 
 
 def test_act_quant_20b_decode64_and_prefill(orc, disp20, layer20):
-    """The 20B layer at 64 tokens (128- and 256-row shapes) and at 4096 tokens (the 512-row x
-    64-entry shape at K = 2880), quantized activations."""
+    """The 20B layer at 64 tokens (128- and 256-row shapes), at 512 tokens (experts averaging 64
+    entries: the 512-row x 64-entry shape at K = 2880) and at 4096 tokens (512 entries: the
+    512 x 128 block), quantized activations."""
     _act_quant_check(orc, disp20, layer20, syn.hidden(64, H20, seed=490), 4, "act_quant 20B T=64",
                      shapes=[(5, 5), (7, 7), (7, 5)])
+    _act_quant_check(orc, disp20, layer20, syn.hidden(512, H20, seed=493), 4, "act_quant 20B T=512",
+                     n_sample=32, seed=494, shapes=[(1, 0), (9, 9), (0, 9)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(4096, H20, seed=491), 4, "act_quant 20B T=4096",
                      n_sample=48, seed=492, shapes=[(1, 0), (1, 7), (9, 9), (9, 0)])
 
