@@ -765,6 +765,29 @@ def test_act_quant_option_checks(disp20):
         disp20.set_act_quant(2)
 
 
+def test_empty_batches(orc, disp20, layer20):
+    """Zero tokens: every forward entry point succeeds and writes nothing (the reference's loops
+    over tokens and slots simply do not run); the batched dispatch over an empty expert list
+    returns zeros (moe_dispatch.rs:473-607 sums an empty list); the next real call still matches
+    the oracle."""
+    x0 = np.zeros((0, H20), np.float32)
+    assert disp20.layer_forward(0, x0, 4).shape == (0, H20)
+    idx, w = disp20.router_topk(0, x0, 4)
+    assert idx.shape == (0, 4) and w.shape == (0, 4)
+    sentinel = np.full(64, 7.0, np.float32)
+    yd = DeviceBuffer.from_array(sentinel)
+    xd = DeviceBuffer.from_array(np.zeros(64, np.float32))
+    disp20.layer_forward_device(0, xd, 0, 4, yd)
+    disp20.synchronize()
+    assert np.array_equal(yd.download(np.float32, 64), sentinel)
+    x1 = syn.hidden(1, H20, seed=475)[0]
+    assert np.array_equal(disp20.dispatch_experts_batched(x1, []), np.zeros(H20, np.float32))
+    want, _, widx, _ = orc.moe_layer(x1[None], layer20, 4)
+    gidx, _ = disp20.router_topk(0, x1[None], 4)
+    assert np.array_equal(gidx, widx)
+    assert_rel_l2(disp20.layer_forward(0, x1[None], 4), want, "after the empty calls")
+
+
 def test_invalid_calls_leave_context_usable(orc, disp20, layer20):
     """Calls refused for their arguments (top-k 0 or above the expert count, a layer never
     loaded) change nothing: the next valid call of each size still matches the oracle."""
