@@ -82,17 +82,19 @@ struct GemmShape {
   // one wavefront per SIMD with 16+ row tiles (B-stationary steps): B holds exactly kGroups pieces
   // and the pieces past them land in a dummy area; otherwise the slot also holds those pieces
   static constexpr bool kBStat = RT >= 16;
-  static constexpr int kBufB = (kBStat ? kGroups : kDma * W) * 1024;
+  // D = 2, and D = 3 with 512 rows (whose 8 KB of scale words per step would leave no room for a
+  // third slot): the A-scale words (one byte per step) go once per 4 steps into a pair of buffers
+  // outside the ring, and B pieces past kGroups are not loaded (11 of the 64 KB a 512 x 64 step
+  // moved were such repeats), so the number of a step's DMAs varies and the waits count it
+  static constexpr bool kScale4 = !kBStat && (D == 2 || kRows >= 512);
+  // (the 3-slot ring keeps only the kGroups pieces in a slot, so that three fit)
+  static constexpr int kBufB = (kBStat || (kScale4 && D == 3) ? kGroups : kDma * W) * 1024;
   static constexpr int kBufA = kTilesA * 1024;               // A chunks of one step
-  // D = 2 (each step waits for all of its DMAs, so their number may vary): the A-scale words
-  // (one byte per step) go once per 4 steps into a pair of buffers outside the ring, and B
-  // pieces past kGroups are not loaded: 11 of the 64 KB a 512 x 64 step moved were such repeats
-  static constexpr bool kScale4 = !kBStat && D == 2;
   // two steps in flight (operands read into registers, then the slot refilled), for column
   // groups narrow enough to hold a step's operands
-  static constexpr bool kTwoAhead = kScale4 && CGW <= 2;
+  static constexpr bool kTwoAhead = kScale4 && D == 2 && CGW <= 2;
   // DMA addresses as wavefront-uniform bases plus 32-bit lane offsets (fewer VGPRs)
-  static constexpr bool kSAddr = kBStat || kTwoAhead;
+  static constexpr bool kSAddr = kBStat || kTwoAhead || (kScale4 && D == 3);
   static constexpr int kBufS = kScale4 ? 0 : kTilesA * 256;  // A-scale words of one step
   static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
   static constexpr int kLds = D * kSlot;
@@ -529,6 +531,19 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   do {                                                                                              \
     if constexpr (S::kBStat) {                                                                      \
       GEMM_LOAD_S(step, sl);                                                                        \
+    } else if constexpr (S::kSAddr && !S::kTwoAhead) { /* the 3-slot ring, scale words per 4 steps */ \
+      const uint8_t *bb_ = a.brec + (size_t)(step) * G::kStep;                                      \
+      _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                         \
+        if (W * i + wvu < S::kGroups) lds_dma16_s(boff[i], bb_, (sl) + 1024 * (W * i + wvu));        \
+      }                                                                                             \
+      const uint32_t ao_ = min((uint32_t)(step) * 1024u + 16u * lane, a_last);                      \
+      _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                          \
+        lds_dma16_s(ao_, asrc[i], (sl) + S::kBufB + (W * i + wvu) * 1024);                         \
+      if ((fresh) && ((step) & 3) == 0) {                                                           \
+        const uint32_t so_ = (uint32_t)((step) >> 2) * 256u + 4u * lane;                             \
+        _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                        \
+          lds_dma4_s(so_, ssrc[i], s_sc[((step) >> 2) & 1] + (W * i + wvu) * 256);                  \
+      }                                                                                             \
     } else if constexpr (!S::kTwoAhead) {                                                           \
       _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                         \
         if (!S::kScale4 || W * i + wvu < S::kGroups)                                                \
@@ -573,6 +588,28 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   //      its LDS reads done, then a barrier: slot (s + 1) % D is whole, slot s % D is free.
   static_assert(D == 2 || D == 3, "ring depth");
   const int ns = (int)d.ns;
+  // The wait that ends a step (ld: the step whose loads it issued, fresh: not a repeat): this
+  // wavefront's loads of the next step complete, those of step ld (D - 2 steps' loads) in flight.
+  // With kScale4 and D = 3 their number is this wavefront's B pieces (the last one only inside
+  // kGroups), its A tiles and, for a fresh step that is a multiple of 4, its scale words.
+  const bool fullb3 = W * (S::kDma - 1) + wvu < S::kGroups;
+#define GEMM_WAIT_AHEAD(ld, fresh)                                                                  \
+  do {                                                                                              \
+    if constexpr (D == 2) {                                                                         \
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));                                                  \
+    } else if constexpr (!S::kScale4) {                                                             \
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kIssue));                                          \
+    } else {                                                                                        \
+      const bool sc_ = (fresh) && ((ld) & 3) == 0;                                                  \
+      if (fullb3) {                                                                                 \
+        if (sc_) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + 2 * S::kDmaA));                 \
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + S::kDmaA));                         \
+      } else {                                                                                      \
+        if (sc_) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + 2 * S::kDmaA));             \
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + S::kDmaA));                     \
+      }                                                                                             \
+    }                                                                                               \
+  } while (0)
 #define GEMM_STEP(st, cur, nxt)                                                                     \
   do {                                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                              \
@@ -583,7 +620,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       gemm_step<RT, CGW, WR, WC, D, NT>(acc, cur, S::kScale4 ? s_sc[((st) >> 2) & 1] : (cur) + S::kBufB + S::kBufA, \
                                     wr, wc, lane, 8 * ((st) & 3));                                  \
     __builtin_amdgcn_sched_barrier(0);                                                              \
-    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));                                  \
+    GEMM_WAIT_AHEAD(min((st) + D - 1, ns - 1), (st) + D - 1 < ns);                                  \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
     __builtin_amdgcn_s_barrier();                                                                   \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
@@ -676,7 +713,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   } else {
   GEMM_LOAD(0, s_r0, true);
   if (D == 3) GEMM_LOAD(min(1, ns - 1), s_r1, true);
-  __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((D - 2) * S::kIssue));
+  GEMM_WAIT_AHEAD(min(1, ns - 1), true);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -694,6 +731,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   }
   }
 #undef GEMM_STEP
+#undef GEMM_WAIT_AHEAD
 #undef GEMM_LOAD
 #undef GEMM_LOAD_S
 
@@ -928,7 +966,7 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   // per A read of the 512 x 64 block; with three terms its operands do not fit the registers of
   // two wavefronts per SIMD). Measured at prefill: gate_up 322 -> 297 us, down 203 -> 181 us.
   if constexpr (NT == 1) {
-    if (a.shape == 9 || (a.shape == 0 && mean >= 96)) return launch_gemm_shape<MODE, 8, 4, 4, 2, 2, NT>(a, s);
+    if (a.shape == 9 || (a.shape == 0 && mean >= 96)) return launch_gemm_shape<MODE, 8, 4, 4, 2, 3, NT>(a, s);
   }
   if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
   if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
