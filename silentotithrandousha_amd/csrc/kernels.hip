@@ -147,6 +147,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
   __shared__ float s_w[TB][kMaxTopK];
   __shared__ int s_sel[TB];
   __shared__ int s_last;
+  __shared__ int s_cnt[kMaxExperts];  // the grouping's per-expert counts of the block's entries
   const int t0 = blockIdx.x * TB;
   const int nt = min(TB, a.T - t0);
   const int lane = threadIdx.x & 63;
@@ -198,9 +199,12 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
       for (int k = threadIdx.x; k < Hp; k += kRouteThreads) stage(tb, k, k < H ? a.x[(size_t)(t0 + tb) * H + k] : 0.0f);
   }
   __syncthreads();
-  if (a.xrec) {  // the grouped GEMM's activation records of the block's tokens: a lane per block
+  // the grouped GEMM's activation records of the block's tokens, a lane per 32-value block, by
+  // threads u0, u0 + stride, ... (after the router, beside the top-k: off the critical path)
+  auto write_records = [&](int u0, int stride) {
+    if (!a.xrec) return;
     constexpr int kRecBlocks = 4 * kGemmNs;
-    for (int u = threadIdx.x; u < nt * kRecBlocks; u += kRouteThreads) {
+    for (int u = u0; u < nt * kRecBlocks; u += stride) {
       const int tb = u / kRecBlocks, blk = u - tb * kRecBlocks, k0 = 32 * blk;
       const float *xt = s_x + tb * Hp;
       float xv[32];
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
       else
         rec_split_block<kGemmTerms>(xv, blk, a.xrec + (size_t)(t0 + tb) * GemmRec::kBytes);
     }
-  }
+  };
   if constexpr (KI > 0) {
     // experts in pairs (e, e + nw): each x value is read from LDS once for both chains (the
     // reads, not the FMAs, bound this loop); each chain keeps router_dot's order
@@ -269,8 +273,11 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
 
   const TopkCfg c{E, a.k, a.adaptive, a.min_k, a.top1_min, a.margin_min, a.top2_mass};
   const bool per_wave = a.k <= 4 && E <= 128;
+  // per-wavefront top-k: wavefronts TB .. 15 write the records meanwhile; else all threads first
+  static_assert(TB < kRouteThreads / 64, "a wavefront per token, and wavefronts for the records");
+  if (!per_wave || wv >= TB)
+    write_records(per_wave ? (int)threadIdx.x - 64 * TB : (int)threadIdx.x, per_wave ? kRouteThreads - 64 * TB : kRouteThreads);
   if (per_wave) {
-    static_assert(TB <= kRouteThreads / 64, "a wavefront per token");
     if (wv < nt) {
       const int tb = wv, t = t0 + tb;
       float l[2];
@@ -329,7 +336,6 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
     const bool table = (size_t)ld_bc * E + 2 * (size_t)E <= (size_t)TB * Hp;
     __syncthreads();  // s_order of every token of the block
     if (table && wv == 0) {
-      int *s_cnt = reinterpret_cast<int *>(s_x);  // [E] (the x staging is free now)
       const int ne = nt * a.k;
       for (int e = lane; e < E; e += 64) s_cnt[e] = 0;
       for (int p0 = 0; p0 < ne; p0 += 64) {
