@@ -420,15 +420,31 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     }
   }
   if (wv == 0) {
-    const int na = min(*a.n_active, a.max_active);
-    int ex = -1, beg = 0, cnt = 0, base = 0;
-    for (int q0 = 0; q0 < na; q0 += 64) {
-      const int ai = q0 + lane;
-      int o0 = 0, o1 = 0;
-      if (ai < na) {
-        o0 = a.active_off[ai];
-        o1 = a.active_off[ai + 1];
+    // the expert count and every lane's entry range and expert id in one round of loads: lanes
+    // below max_active (the lists' length) load before the count is known, lanes past the count
+    // are ignored
+    constexpr int kQ = (kMaxExperts + 63) / 64;
+    const int ma = min(a.max_active, kMaxExperts);
+    int lo[kQ], lh[kQ], lid[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; q++) {
+      const int ai = 64 * q + lane;
+      lo[q] = lh[q] = 0;
+      lid[q] = -1;
+      if (ai < ma) {
+        lo[q] = a.active_off[ai];
+        lh[q] = a.active_off[ai + 1];
+        lid[q] = a.active_ids[ai];
       }
+    }
+    const int na = min(*a.n_active, ma);
+    int ex = -1, beg = 0, cnt = 0, base = 0;
+#pragma unroll
+    for (int q = 0; q < kQ; q++) {
+      const int q0 = 64 * q;
+      if (q0 >= na) break;
+      const int ai = q0 + lane;
+      const int o0 = ai < na ? lo[q] : 0, o1 = ai < na ? lh[q] : 0;
       const int nct = (o1 - o0 + S::kCols - 1) / S::kCols;
       int incl = nct;  // inclusive prefix sum over the lanes
 #pragma unroll
@@ -441,7 +457,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       if (hit) {
         const int hl = __builtin_ctzll(hit);
         if (lane == hl) {
-          ex = a.active_ids[ai];
+          ex = lid[q];
           beg = o0 + (cl - start) * S::kCols;
           cnt = min(S::kCols, o1 - beg);
         }
