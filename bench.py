@@ -328,7 +328,8 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
     if not traffic_kib:  # calibrated PMC measurement of the same kernel and workload
         tf = os.path.join(ROOT, "profiles", "traffic.json")
         if os.path.exists(tf):
-            rec = json.load(open(tf)).get(kname)
+            recs = json.load(open(tf))
+            rec = recs.get(f"{kname}@{workload}") or recs.get(kname)
             if rec and rec.get("workload") == workload:
                 res["roofline"]["traffic"] = rec["bytes_per_launch"]
                 res["roofline"]["traffic_source"] = rec["source"]
