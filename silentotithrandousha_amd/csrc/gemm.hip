@@ -235,19 +235,19 @@ __device__ __forceinline__ void gemm_select_b(GemmB<NT> &b, const GemmBRaw<NT> &
 }
 
 // The A operands and the B operands of column groups [0, C1) (selected); C1 < CGW: the later
-// groups are read with gemm_read_b_raw and selected by the caller.
+// groups are read with gemm_read_b_raw and selected by the caller. sw4: the wavefront's A-scale
+// words of the current 4 steps (read from LDS once per 4 steps; sh selects the step's byte).
 template <int RT, int CGW, int WR, int WC, int D, int NT, int C1 = CGW>
-__device__ __forceinline__ void gemm_read_ops(GemmOps<RT, CGW, NT> &o, const uint8_t *slot, const uint8_t *sb, int wr,
+__device__ __forceinline__ void gemm_read_ops(GemmOps<RT, CGW, NT> &o, const uint8_t *slot, const uint32_t *sw4, int wr,
                                               int wc, int lane, int sh) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   constexpr int kEntryStep = GemmRecT<NT>::kStep;
   const int j = lane & 15, g = lane >> 4;
   const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024;
-  sb += wr * RT * 256;
 #pragma unroll
   for (int r = 0; r < RT; r++) {
     o.ar[r] = *reinterpret_cast<const uint4 *>(ab + r * 1024 + 16 * lane);
-    o.sw[r] = *reinterpret_cast<const uint32_t *>(sb + r * 256 + 4 * lane) >> sh;
+    o.sw[r] = sw4[r] >> sh;
   }
 #pragma unroll
   for (int c = 0; c < C1; c++) gemm_read_b(o.b[c], bb + 16 * c * kEntryStep, g);
@@ -689,7 +689,11 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 #define GEMM_STEP2(st, cur, jj)                                                                     \
   do {                                                                                              \
     GemmOps<RT, CGW, NT> ops_;                                                                      \
-    gemm_read_ops<RT, CGW, WR, WC, D, NT, kCSplit>(ops_, cur, s_sc[((st) >> 2) & 1], wr, wc, lane, 8 * (jj)); \
+    if ((jj) == 0) {                                                                                \
+      _Pragma("unroll") for (int r_ = 0; r_ < RT; r_++)                                             \
+        sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[((st) >> 2) & 1] + (wr * RT + r_) * 256 + 4 * lane); \
+    }                                                                                               \
+    gemm_read_ops<RT, CGW, WR, WC, D, NT, kCSplit>(ops_, cur, sw4_, wr, wc, lane, 8 * (jj));        \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     /* the first column groups' MFMAs run while the other groups' operands arrive */               \
     GemmBRaw<NT> raw_[CGW - kCSplit];                                                               \
@@ -713,6 +717,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));                                               \
     GEMM_BARRIER();                                                                                 \
   } while (0)
+    // the A-scale words of the current 4 steps, read from LDS once per 4 steps (their DMA is
+    // complete from the step before the first of them until the DMA of the quad after next)
+    uint32_t sw4_[RT];
     constexpr int kAll = S::kDma + 2 * S::kDmaA;  // the DMAs of a step whose scale words load
 #pragma unroll
     for (int k = 0; k < kAll; k++) dma2(k, 0, s_r0);
