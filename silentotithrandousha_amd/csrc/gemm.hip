@@ -151,23 +151,22 @@ __device__ __forceinline__ void gemm_read_b(GemmB<NT> &b, const uint8_t *eb, int
 }
 
 // MFMAs of one K-step for a wavefront: RT row tiles x CG column groups x NT terms, all
-// operands from the step's ring slot (sb: the step's A-scale words); sh = 8 * (s % 4) selects the
-// step's byte of them. The B operands of column group c + 1 are read while the MFMAs of group c
+// operands from the step's ring slot (sw4: the wavefront's A-scale words of the current 4 steps,
+// read from LDS once per 4 steps); sh = 8 * (s % 4) selects the step's byte of them. The B operands of column group c + 1 are read while the MFMAs of group c
 // run. Column groups past the block's entries compute on repeated entries (not stored).
 template <int RT, int CGW, int WR, int WC, int D, int NT>
-__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *slot, const uint8_t *sb, int wr,
+__device__ __forceinline__ void gemm_step(f32x4 (&acc)[RT][CGW], const uint8_t *slot, const uint32_t (&sw4)[RT], int wr,
                                           int wc, int lane, int sh) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   constexpr int CG = CGW, kEntryStep = GemmRecT<NT>::kStep;
   const int j = lane & 15, g = lane >> 4;
   const uint8_t *bb = slot + (16 * CGW * wc + j) * kEntryStep, *ab = slot + S::kBufB + wr * RT * 1024;
-  sb += wr * RT * 256;
   uint4 ar[RT];
   uint32_t sw[RT];
 #pragma unroll
   for (int r = 0; r < RT; r++) {
     ar[r] = *reinterpret_cast<const uint4 *>(ab + r * 1024 + 16 * lane);
-    sw[r] = *reinterpret_cast<const uint32_t *>(sb + r * 256 + 4 * lane) >> sh;
+    sw[r] = sw4[r] >> sh;
   }
   GemmB<NT> bc, bn;
   gemm_read_b(bc, bb, g);
@@ -637,11 +636,16 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   do {                                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     GEMM_LOAD(min((st) + D - 1, ns - 1), nxt, (st) + D - 1 < ns);                                   \
-    if constexpr (S::kBStat)                                                                        \
+    if constexpr (S::kBStat) {                                                                      \
       gemm_step_bstat<RT, CGW, WR, WC, D, NT, false>(acc, cur, wr, wc, lane, 8 * ((st) & 3), nrt_valid); \
-    else                                                                                            \
-      gemm_step<RT, CGW, WR, WC, D, NT>(acc, cur, S::kScale4 ? s_sc[((st) >> 2) & 1] : (cur) + S::kBufB + S::kBufA, \
-                                    wr, wc, lane, 8 * ((st) & 3));                                  \
+    } else {                                                                                        \
+      if (((st) & 3) == 0) { /* the scale words of steps st .. st + 3 (whole since step st - 1) */  \
+        const uint8_t *sb_ = (S::kScale4 ? s_sc[((st) >> 2) & 1] : (cur) + S::kBufB + S::kBufA) + wr * RT * 256; \
+        _Pragma("unroll") for (int r_ = 0; r_ < RT; r_++)                                           \
+          sw4_[r_] = *reinterpret_cast<const uint32_t *>(sb_ + r_ * 256 + 4 * lane);                \
+      }                                                                                             \
+      gemm_step<RT, CGW, WR, WC, D, NT>(acc, cur, sw4_, wr, wc, lane, 8 * ((st) & 3));              \
+    }                                                                                               \
     __builtin_amdgcn_sched_barrier(0);                                                              \
     GEMM_WAIT_AHEAD(min((st) + D - 1, ns - 1), (st) + D - 1 < ns);                                  \
     __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                        \
@@ -741,6 +745,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 #undef GEMM_BARRIER
 #undef GEMM_VM_WAIT
   } else {
+  uint32_t sw4_[RT];  // the A-scale words of the current 4 steps (gemm_step)
   GEMM_LOAD(0, s_r0, true);
   if (D == 3) GEMM_LOAD(min(1, ns - 1), s_r1, true);
   GEMM_WAIT_AHEAD(min(1, ns - 1), true);
