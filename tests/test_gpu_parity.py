@@ -700,6 +700,34 @@ def test_prefill_2048_tokens_120b(orc):
 
 # ---------------------------------------------------------------- quantized activations (opt-in)
 
+def test_prefill_partial_router_block_20b(orc, disp20, layer20):
+    """2053 tokens, a multiple of 8 plus 5: the last 8-token router block holds 5 tokens (its
+    idle top-k wavefronts and the wavefronts that write the GEMM records see a partial block).
+    Top-k indices of every token exact against the oracle's router; tokens of the first, the
+    last full and the partial block within the tolerance of the oracle, on the exact path and on
+    the quantized one (against the MXFP6 oracle)."""
+    T, k = 2053, 4
+    x = syn.hidden(T, H20, seed=470)
+    logits = orc.router_logits(layer20["router_w"], layer20["router_b"], x, E20, H20)
+    widx, _, _, _ = orc.topk(logits, k)
+    gidx, _ = disp20.router_topk(0, x, k)
+    assert np.array_equal(gidx, widx)
+    rows = np.array([0, 1, 7, 2040, 2047, 2048, 2049, 2050, 2051, 2052])
+    disp20.set_batch_gemm(1)
+    disp20.set_gemm_shape(0)
+    got = disp20.layer_forward(0, x, k)
+    want, _, idx, _ = orc.moe_layer(x[rows], layer20, k)
+    assert np.array_equal(idx, widx[rows])
+    assert_rel_l2(got[rows], want, "T=2053 exact split")
+    disp20.set_act_quant(1)
+    try:
+        gq = disp20.layer_forward(0, x, k)
+    finally:
+        disp20.set_act_quant(0)
+    wq, _, _, _ = orc.moe_layer_mxfp6(x[rows], layer20, k)
+    assert_rel_l2(gq[rows], wq, "T=2053 quantized", tol=2e-4)
+
+
 def _act_quant_check(orc, d, layer, x, k, what, n_sample=None, seed=0, shapes=()):
     """MOE_OPT_ACT_QUANT 1: top-k exact; the output (or n_sample sampled tokens) within the
     tolerance of the fp32 path on MXFP6 activations (orc.moe_layer_mxfp6: the GPU and the oracle
