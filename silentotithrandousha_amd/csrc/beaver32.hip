@@ -119,10 +119,18 @@ __global__ __launch_bounds__(64 * SPR) void k_beaver32(TripleArgs a) {
   __syncthreads();
   const uint32_t kl = tid / SPR, j = tid - kl * SPR;  // round within a pass, triple within it
   const uint32_t h0 = a.hmul[j][0], h1 = a.hmul[j][1], h2 = a.hmul[j][2], h3 = a.hmul[j][3];
+  // every round's seed in flight at once (loaded pass by pass, each pass waited for its load)
+  uint32_t seedv[kIter];
+#pragma unroll
+  for (uint32_t m = 0; m < kIter; m++) {
+    const uint32_t r = R0 + 64u * m + kl;
+    seedv[m] = r < a.num_rounds ? a.seeds[r] : 0u;
+  }
+#pragma unroll
   for (uint32_t m = 0; m < kIter; m++) {
     const uint32_t r = R0 + 64u * m + kl, k = r * SPR + j;
     if (k >= a.count) return;  // rounds increase with m
-    const uint32_t seed = a.seeds[r];
+    const uint32_t seed = seedv[m];
     const uint32_t a0 = chash32_m(seed, h0), b0 = chash32_m(seed, h1);
     const uint32_t ca = chash32_m(seed, h2), cb = chash32_m(seed, h3);
     // lane r % group of threadgroup r / group (group = 32, or the one group of a short call)
