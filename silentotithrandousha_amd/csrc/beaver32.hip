@@ -139,16 +139,17 @@ __global__ __launch_bounds__(64 * SPR) void k_beaver32(TripleArgs a) {
     const uint32_t ab = fmul(a0, b0);
     if (a.party >= 0) {
       const uint32_t x = a.eval[a.party];
-      a.a[k] = fadd(a0, fmul_small(ca, x));
-      a.b[k] = fadd(b0, fmul_small(cb, x));
-      a.c[k] = fadd(ab, fmul_small(bt, x));
+      // streaming stores: the outputs are written once and not read back by this kernel
+      __builtin_nontemporal_store(fadd(a0, fmul_small(ca, x)), a.a + k);
+      __builtin_nontemporal_store(fadd(b0, fmul_small(cb, x)), a.b + k);
+      __builtin_nontemporal_store(fadd(ab, fmul_small(bt, x)), a.c + k);
     } else {
       for (uint32_t p = 0; p < a.n; p++) {
         const uint32_t x = a.eval[p];
         const size_t o = (size_t)p * a.count + k;
-        a.a[o] = fadd(a0, fmul_small(ca, x));
-        a.b[o] = fadd(b0, fmul_small(cb, x));
-        a.c[o] = fadd(ab, fmul_small(bt, x));
+        __builtin_nontemporal_store(fadd(a0, fmul_small(ca, x)), a.a + o);
+        __builtin_nontemporal_store(fadd(b0, fmul_small(cb, x)), a.b + o);
+        __builtin_nontemporal_store(fadd(ab, fmul_small(bt, x)), a.c + o);
       }
     }
   }
