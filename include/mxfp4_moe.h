@@ -104,7 +104,10 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * even, saturate at 7.5): a third of the MFMA work, and results that follow the f32 path applied
  * to those quantized activations (not the f32 path itself). Routing is unchanged (the router
  * reads x unquantized); single-token forwards and the GEMV batch path are unaffected. In this mode
- * MOE_OPT_GEMM_SHAPE(_DOWN) codes 2, 3, 4, 6 and 8 select the default shape. */
+ * MOE_OPT_GEMM_SHAPE(_DOWN) codes 2, 3, 4, 6 and 8 select the default shape. Changing it
+ * re-lays out the context's h records: the call waits until the whole device is idle
+ * (hipDeviceSynchronize), so forwards enqueued on any stream finish first, and it is refused
+ * during graph capture. */
 enum moe_option {
   MOE_OPT_FUSED_DECODE = 1,
   MOE_OPT_SPIN_LIMIT = 2,
@@ -238,7 +241,9 @@ int moe_init_lm_head_bf16_device(moe_ctx *ctx, const uint16_t *weights_bf16, siz
  * Returns MOE_ERR_STATE where the reference panics ("call init_lm_head first"). */
 int moe_dispatch_lm_head(moe_ctx *ctx, const float *input, size_t vocab_size, float *logits);
 /* The same with device pointers, enqueued on `stream` (NULL = the context's stream); no
- * synchronisation (no reference counterpart: the device-resident form of dispatch_lm_head). */
+ * synchronisation (no reference counterpart: the device-resident form of dispatch_lm_head).
+ * After moe_init_lm_head_bf16(_device) `input` must be 16-byte aligned (MOE_ERR_INVALID
+ * otherwise); the f32 head takes any 4-byte aligned input. */
 int moe_dispatch_lm_head_device(moe_ctx *ctx, const float *input, size_t vocab_size, float *logits,
                                 void *stream);
 

@@ -115,13 +115,6 @@ void orc_dequant_gate_up_reordered(const uint8_t *blocks, const uint8_t *scales,
   }
 }
 
-void orc_reorder_gate_up_bias(const float *bias, size_t inter, float *out) {
-  for (size_t i = 0; i < inter; i++) {
-    out[i] = bias[2 * i];
-    out[inter + i] = bias[2 * i + 1];
-  }
-}
-
 /* ------------------------------------------------------------------ MXFP4 -> fp16 */
 
 /* weights.rs:465-485: the LUT as fp16 bits (exact). */

@@ -47,8 +47,6 @@ void orc_dequant_mxfp4_matrix(const uint8_t *blocks, const uint8_t *scales, size
 /* weights.rs:425-452 de-interleave: source row 2i -> gate row i, 2i+1 -> up row inter+i */
 void orc_dequant_gate_up_reordered(const uint8_t *blocks, const uint8_t *scales, size_t inter,
                                    size_t cols, float *out);
-/* weights.rs:454-460 */
-void orc_reorder_gate_up_bias(const float *bias, size_t inter, float *out);
 
 /* ---- MXFP4 -> fp16 decode of the live path (scalar fallback, weights.rs:593-639) ---- */
 uint16_t orc_f16_mul_scalar(uint16_t val_bits, uint16_t scale_bits);   /* weights.rs:619-639 */

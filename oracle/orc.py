@@ -42,7 +42,6 @@ def lib():
     L.orc_dequant_mxfp4_row.argtypes = [_u8p, _u8p, _sz, _f32p]
     L.orc_dequant_mxfp4_matrix.argtypes = [_u8p, _u8p, _sz, _sz, _f32p]
     L.orc_dequant_gate_up_reordered.argtypes = [_u8p, _u8p, _sz, _sz, _f32p]
-    L.orc_reorder_gate_up_bias.argtypes = [_f32p, _sz, _f32p]
     L.orc_f16_mul_scalar.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
     L.orc_f16_mul_scalar.restype = ctypes.c_uint16
     L.orc_dequant_mxfp4_row_f16.argtypes = [_u8p, _u8p, _sz, _u16p]

@@ -15,6 +15,7 @@
 //                  of the wavefront's 32 h values per entry into the h records; DOWN epilogue:
 //                  bias and +-65504 clamp into f32 [entry][H].
 #include <algorithm>
+#include <atomic>
 
 #include "device.hpp"
 #include "kernels.hpp"
@@ -31,8 +32,13 @@ namespace moe {
 // each, as the LDS-DMA copies them: each DMA reads whole record steps, a few rows per instruction).
 
 // s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
-// outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima).
-constexpr int vm_wait(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+// outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima). n must fit
+// the 6-bit vmcnt field: a count outside [0, 63] reaches the non-constexpr function below, and
+// since __builtin_amdgcn_s_waitcnt takes only a constant expression, such a wait does not compile.
+__host__ __device__ inline int vmcnt_outside_6_bits() { return 0; }
+constexpr int vm_wait(int n) {
+  return n >= 0 && n <= 63 ? (0x0F70 | (n & 0xF) | ((n >> 4) << 14)) : vmcnt_outside_6_bits();
+}
 // The same with lgkmcnt 0: also this wavefront's LDS operations complete.
 constexpr int vm_lgkm_wait(int n) { return vm_wait(n) & ~0x0F00; }
 
@@ -106,6 +112,9 @@ struct GemmShape {
   static constexpr int kSlot = kBufB + kBufA + kBufS;        // one ring slot
   static constexpr int kLds = D * kSlot;
   static constexpr int kIssue = kDma + 2 * kDmaA;            // VMEM operations per wavefront per step
+  // the counted waits hold at most two steps' loads of a wavefront outstanding (its B pieces, A
+  // tiles and scale words), which must fit the 6-bit vmcnt field
+  static_assert(2 * kIssue <= 63, "a step's loads fit the vmcnt field");
 };
 
 // B operands of one column group for the wavefront's lanes (entry j, lane group g): per term the
@@ -947,15 +956,17 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 
 // Compute units of the current device (cached per device).
 static int device_cus() {
-  static int cus[64] = {};
+  static std::atomic<int> cus[64] = {};  // (threads racing here store the same value)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
+  int c = cus[dev].load(std::memory_order_relaxed);
+  if (!c) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
-    cus[dev] = n / 8 * 8;
+    c = n / 8 * 8;
+    cus[dev].store(c, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return c;
 }
 
 template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT>

@@ -450,20 +450,20 @@ __global__ __launch_bounds__(kRouteThreads) void k_route(RouteArgs a) {
 }
 
 template <int KI>
-static void launch_route_ki(const RouteArgs &a, int nq, hipStream_t s) {
+static hipError_t launch_route_ki(const RouteArgs &a, int nq, hipStream_t s) {
   const size_t hp = (size_t)nq * 8 * 64 * sizeof(float);
   if (a.T >= 2048 && kRouteTokens * hp <= 144 * 1024) {
-    static bool attr = false;  // TB tokens of x may exceed the default 64 KB of dynamic LDS
-    if (!attr) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_route<KI, kRouteTokens>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kRouteTokens * hp));
-      attr = true;
-    }
+    // TB tokens of x may exceed the default 64 KB of dynamic LDS
+    static DynLdsOnce once;
+    const hipError_t e = ensure_dyn_lds(once, reinterpret_cast<const void *>(&k_route<KI, kRouteTokens>),
+                                        kRouteTokens * hp);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_route<KI, kRouteTokens>), dim3((unsigned)((a.T + kRouteTokens - 1) / kRouteTokens)),
                        dim3(kRouteThreads), kRouteTokens * hp, s, a);
   } else {
     hipLaunchKernelGGL((k_route<KI, 1>), dim3((unsigned)a.T), dim3(kRouteThreads), hp, s, a);
   }
+  return hipGetLastError();
 }
 
 bool route_bucket_fits(int H, int E) { return 18 * E <= route_hp(H); }
@@ -477,12 +477,11 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
   const size_t lds = (size_t)nq * 8 * 64 * sizeof(float);
   if (lds > 65536) return hipErrorInvalidValue;
   switch (nq) {  // 2880 -> 45 chain terms -> 6 loads per lane
-    case 1: launch_route_ki<1>(a, nq, s); break;
-    case 2: launch_route_ki<2>(a, nq, s); break;
-    case 6: launch_route_ki<6>(a, nq, s); break;
-    default: launch_route_ki<0>(a, nq, s); break;
+    case 1: return launch_route_ki<1>(a, nq, s);
+    case 2: return launch_route_ki<2>(a, nq, s);
+    case 6: return launch_route_ki<6>(a, nq, s);
+    default: return launch_route_ki<0>(a, nq, s);
   }
-  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ bucketing
@@ -575,13 +574,11 @@ constexpr int kSmallNsMax = 24;  // tiles of up to 96 blocks (K <= 3072)
 template <int MODE, int NE>
 static hipError_t launch_small(const GemvArgs &a, hipStream_t s) {
   const size_t lds = (size_t)NE * 2 * a.d.nb * 32 * 2;
-  static bool attr_set = false;
-  if (!attr_set && lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&k_expert_gemv_small<MODE, NE, kSmallNsMax>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (lds > 65536) {
+    static DynLdsOnce once;
+    const hipError_t e = ensure_dyn_lds(
+        once, reinterpret_cast<const void *>(&k_expert_gemv_small<MODE, NE, kSmallNsMax>), 160 * 1024);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   const size_t wgs = (size_t)a.max_active * ((a.d.tiles + 3) / 4);
   hipLaunchKernelGGL((k_expert_gemv_small<MODE, NE, kSmallNsMax>), dim3((unsigned)wgs), dim3(256),

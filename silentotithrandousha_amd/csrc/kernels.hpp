@@ -5,9 +5,31 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "layout.hpp"
 
 namespace moe {
+
+// Raises a kernel's dynamic-LDS limit on the current device once per device. One DynLdsOnce per
+// kernel (a function-local static at the launch site); thread-safe; a failed call is returned
+// and retried by the next launch.
+struct DynLdsOnce {
+  static constexpr int kDevices = 64;
+  std::mutex mu;
+  bool done[kDevices] = {};
+};
+inline hipError_t ensure_dyn_lds(DynLdsOnce &once, const void *kernel, size_t bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= DynLdsOnce::kDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(once.mu);
+  if (once.done[dev]) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) once.done[dev] = true;
+  return e;
+}
 
 constexpr int kMaxExperts = 256;  // router / bucketing LDS tables
 constexpr int kMaxTopK = 16;

@@ -245,6 +245,10 @@ int ensure_work(moe_ctx *c, size_t T, size_t k, size_t E) {
   k = std::max(k, c->work_k);
   E = std::max({E, c->work_E, (size_t)kMaxExperts});
   Work w{};
+  // ensure() may release the old buffer: forget it first, so that a failure below leaves an empty
+  // workspace (the next call sizes it again) and never pointers into freed memory
+  c->w = Work{};
+  c->work_T = c->work_k = c->work_E = 0;
   RETURN_IF(c->work.ensure(carve_work(w, nullptr, T, k, E, c->H, c->I, true)));
   carve_work(w, (char *)c->work.p, T, k, E, c->H, c->I, true);
   // h records are written block by block; their padding past I must read as zeros
@@ -320,8 +324,8 @@ int check_layer(moe_ctx *c, size_t layer, bool need_router, long expert = -1) {
 
 // Token count and top-k of a path-level call on a loaded layer (checked before any workspace
 // is sized for them).
-int check_tokens(moe_ctx *c, size_t layer, size_t T, size_t k) {
-  const size_t E = c->layers[layer].n_experts;
+// E: the experts top_k selects from (the layer's, or its router's for a router-only call).
+int check_tokens(size_t E, size_t T, size_t k) {
   if (k < 1 || k > (size_t)kMaxTopK || k > E)
     return fail(MOE_ERR_INVALID, "top_k %zu outside [1, min(%d, %zu)]", k, kMaxTopK, E);
   if (T > kMaxTokens) return fail(MOE_ERR_INVALID, "n_tokens %zu above %zu", T, kMaxTokens);
@@ -417,7 +421,7 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
                 Ly.router_experts, E);
   if (T == 0) return MOE_OK;
   if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
-  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(check_tokens(c->layers[layer].n_experts, T, k));
   if (norm && !Ly.has_norm) return fail(MOE_ERR_STATE, "layer %zu has no RMSNorm weight", layer);
   const float *resid = nullptr;  // x for the residual add of the unfused paths
   if (norm) {
@@ -914,6 +918,8 @@ int moe_dispatch_lm_head_device(moe_ctx *c, const float *input, size_t vocab, fl
   RETURN_IF(use_dev(c));
   if (!c->lm_vocab) return fail(MOE_ERR_STATE, "call init_lm_head first");
   if (!input || !logits) return fail(MOE_ERR_INVALID, "null input or logits");
+  if (c->lm_bf16 && (reinterpret_cast<uintptr_t>(input) & 15))
+    return fail(MOE_ERR_INVALID, "the bf16 LM head reads input with 16-byte loads: input must be 16-byte aligned");
   if (vocab > c->lm_vocab)
     return fail(MOE_ERR_INVALID, "vocab_size %zu exceeds the initialised %zu", vocab, c->lm_vocab);
   HIP_TRY(lm_head_launch(c, input, vocab, logits, pick(c, stream)));
@@ -927,8 +933,7 @@ int moe_router_topk(moe_ctx *c, size_t layer, const float *x, size_t T, size_t k
   RETURN_IF(check_layer(c, layer, true));
   const size_t E = c->layers[layer].router_experts;
   if (T == 0) return MOE_OK;
-  RETURN_IF(check_tokens(c, layer, T, k));
-  if (k > E) return fail(MOE_ERR_INVALID, "top_k %zu above the router's %zu experts", k, E);
+  RETURN_IF(check_tokens(E, T, k));
   RETURN_IF(ensure_work(c, T, k, E));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
   RouteArgs ra{};
@@ -964,7 +969,7 @@ int moe_layer_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
   if (T == 0) return MOE_OK;
   RETURN_IF(check_layer(c, layer, true));
-  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(check_tokens(c->layers[layer].n_experts, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
   RETURN_IF(forward_device(c, c->w, layer, c->w.x, T, k, c->w.y, c->stream));
@@ -978,7 +983,7 @@ int moe_layer_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T,
   RETURN_IF(use_dev(c));
   RETURN_IF(check_layer(c, layer, true));
   if (T == 0) return MOE_OK;
-  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(check_tokens(c->layers[layer].n_experts, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   return forward_device(c, c->w, layer, x, T, k, y, pick(c, stream));
 }
@@ -991,7 +996,7 @@ int moe_layer_forward_device_noalloc(moe_ctx *c, size_t layer, const float *x, s
   RETURN_IF(check_layer(c, layer, true));
   if (T == 0) return MOE_OK;
   if (!x || !y) return fail(MOE_ERR_INVALID, "null x or y");
-  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(check_tokens(c->layers[layer].n_experts, T, k));
   if (!c->scratch) return fail(MOE_ERR_STATE, "no scratch array address for device %d", c->dev);
   const size_t E = c->layers[layer].n_experts;
   Work w{};
@@ -1013,7 +1018,7 @@ int moe_block_forward(moe_ctx *c, size_t layer, const float *x, size_t T, size_t
   if (!x || !out) return fail(MOE_ERR_INVALID, "null x or out");
   if (T == 0) return MOE_OK;
   RETURN_IF(check_layer(c, layer, true));
-  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(check_tokens(c->layers[layer].n_experts, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   HIP_TRY(hipMemcpyAsync(c->w.x, x, T * c->H * 4, hipMemcpyHostToDevice, c->stream));
   RETURN_IF(forward_device(c, c->w, layer, c->w.x, T, k, c->w.y, c->stream, true));
@@ -1028,7 +1033,7 @@ int moe_block_forward_device(moe_ctx *c, size_t layer, const float *x, size_t T,
   if (x == out) return fail(MOE_ERR_INVALID, "out must not alias x");
   RETURN_IF(check_layer(c, layer, true));
   if (T == 0) return MOE_OK;
-  RETURN_IF(check_tokens(c, layer, T, k));
+  RETURN_IF(check_tokens(c->layers[layer].n_experts, T, k));
   RETURN_IF(ensure_work(c, T, k, c->layers[layer].n_experts));
   return forward_device(c, c->w, layer, x, T, k, out, pick(c, stream), true);
 }
@@ -1189,8 +1194,11 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
         // no kernel writes, must read as zeros in the new one
         if (c->capturing) return fail(MOE_ERR_STATE, "MOE_OPT_ACT_QUANT cannot change during graph capture");
         RETURN_IF(use_dev(c));
-        HIP_TRY(hipStreamSynchronize(c->stream));
+        // forwards may be in flight on caller streams (the _device calls): the whole device
+        // drains before the records are cleared, so no old-layout write lands after the clear
+        HIP_TRY(hipDeviceSynchronize());
         HIP_TRY(hipMemset(c->w.hrec, 0, c->w.hrec_bytes));
+        HIP_TRY(hipDeviceSynchronize());
       }
       c->act_quant = (int)value;
       return MOE_OK;

@@ -224,6 +224,11 @@ def test_lm_head_bf16(orc, H, V):
     d.dispatch_lm_head_device(xd, V, yd)
     d.synchronize()
     assert np.array_equal(yd.download(np.float32, (V,)), got.astype(np.float32))
+    # the bf16 head reads x with 16-byte loads: an input 4 bytes past an aligned address is refused
+    from silentotithrandousha_amd._ffi import MoeError
+    xo = DeviceBuffer((H + 4) * 4)
+    with pytest.raises(MoeError, match="aligned"):
+        d.dispatch_lm_head_device(xo.ptr + 4, V, yd)
     wf = syn.bf16_to_f32(w[:8])
     d.init_lm_head(wf, 8)
     assert rel_l2(d.dispatch_lm_head(x, 8), wf.astype(np.float64) @ x.astype(np.float64)) < 1e-5

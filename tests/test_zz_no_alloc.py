@@ -67,3 +67,44 @@ def test_noalloc_two_contexts_one_device():
             assert_bit_exact(outs[0], outs[1], f"context {ds.index(d)} rep {rep}")
     for d in ds:
         d.close()
+
+
+def test_noalloc_under_graph_capture():
+    """The property the entry point exists for: on a fresh context, whose workspace no call has
+    sized, the allocation-free forward is captured into a HIP graph (the allocating forward
+    refuses to size its workspace while capturing); every replay, with eager calls between them,
+    gives the allocating forward's bits. Covers a batch (the grouped-GEMM path) and a single token
+    (the one-launch path)."""
+    L = syn.make_layer(H, I, 32, seed=500)
+    for T, seed in ((48, 501), (1, 502)):
+        d = GpuMoeDispatcher(H, I, 7.0)
+        d.preload_layer(0, L)
+        x = syn.hidden(T, H, seed=seed)
+        xd, yd = DeviceBuffer.from_array(x), DeviceBuffer(T * H * 4)
+        check(lib().moe_memset_device(ctypes.c_void_p(yd.ptr), 0, T * H * 4))
+        ref_fn, na = lib().moe_layer_forward_device, lib().moe_layer_forward_device_noalloc
+        with pytest.raises(MoeError):  # the allocating forward cannot size a workspace in a capture
+            check(lib().moe_graph_begin(d.ctx))
+            try:
+                check(ref_fn(d.ctx, 0, ctypes.c_void_p(xd.ptr), T, 4, ctypes.c_void_p(yd.ptr), None))
+            finally:
+                g = ctypes.c_void_p()
+                if lib().moe_graph_end(d.ctx, ctypes.byref(g)) == 0 and g.value:
+                    lib().moe_graph_destroy(g)
+        check(lib().moe_graph_begin(d.ctx))
+        try:
+            check(na(d.ctx, 0, ctypes.c_void_p(xd.ptr), T, 4, ctypes.c_void_p(yd.ptr), None))
+        finally:
+            g = ctypes.c_void_p()
+            check(lib().moe_graph_end(d.ctx, ctypes.byref(g)))
+        want = _run(d, ref_fn, x, 4)  # eager, after the capture (sizes the context's workspace)
+        try:
+            for rep in range(3):
+                check(lib().moe_memset_device(ctypes.c_void_p(yd.ptr), 0xFF, T * H * 4))
+                check(lib().moe_graph_launch(d.ctx, g))
+                d.synchronize()
+                assert_bit_exact(yd.download(np.float32, (T, H)), want, f"graph replay {rep} T={T}")
+                _run(d, na, syn.hidden(T, H, seed=seed + 10 + rep), 4)  # eager work between replays
+        finally:
+            check(lib().moe_graph_destroy(g))
+        d.close()
