@@ -117,18 +117,41 @@ constexpr int kLayerMaxHexp = 5;
 constexpr int kHRecBytes = kLayerMaxK / 8 * 32;
 static_assert(kTerms == 4, "h record piece = 4 terms x 8 bytes");
 
-// MFMA sweep of a loaded down tile against an h record in LDS: the B operand of tile_mfma_f8 from
-// the tile-major layout. Lane (column j = term j % 4, group gb) takes, for step s, values
-// 16(gb&1) .. +15 of block 4s + (gb>>1) (two 8-value pieces, 32 bytes apart) and the same values
-// of block 4s + 2 + (gb>>1) (256 bytes further); sb = the lane's B scale byte in every byte
-// (term j's fixed scale, 0 for columns >= kTerms).
+// LDS-DMA of 16 bytes per lane (lane l's bytes land at lds + 16 l) with the agent-coherent cache
+// policy (sc1: the h records are written by other blocks with agent-scope stores), written as
+// inline assembly so that the compiler's wait tracking does not see it (with the builtin it makes
+// every later LDS read wait for all DMAs in flight); the caller waits with counted vmcnt. Every
+// LDS-DMA of this kernel goes through here, so the compiler keeps no value of its own in m0.
+__device__ __forceinline__ void lds_dma16_sc1(const void *g, const void *lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
+// The down sweep of a loaded down tile against its slot's h record: the record (tile-major, 512
+// bytes per MFMA step) comes into LDS at hdst by 12 LDS-DMAs of 1 KB, two steps each, and the MFMAs
+// start as soon as the first KB has landed: step q's bytes lie in DMA q / 2, complete once at most
+// 11 - q / 2 of the wavefront's DMAs are outstanding (they complete in order). B operand of
+// tile_mfma_f8 from the tile-major layout: lane (column j = term j % 4, group gb) takes, for step s,
+// values 16(gb&1) .. +15 of block 4s + (gb>>1) (two 8-value pieces, 32 bytes apart) and the same
+// values of block 4s + 2 + (gb>>1) (256 bytes further); sb = the lane's B scale byte in every byte
+// (term j's fixed scale, 0 for columns >= kTerms). Step s accumulates into chain s % 4 (four short
+// dependent chains), summed (c0 + c1) + (c2 + c3) at the end.
 template <int NSMAX>
-__device__ __forceinline__ f32x4 tile_mfma_h(const TileRegs<NSMAX> &r, const uint8_t *rec, uint32_t sb, int lane) {
+__device__ __forceinline__ f32x4 tile_mfma_h_stream(const TileRegs<NSMAX> &r, const uint8_t *hsrc, uint8_t *hdst,
+                                                    uint32_t sb, int lane) {
+  constexpr int kD = kHRecBytes / 1024;  // DMAs of the record
+  static_assert(NSMAX == 2 * kD, "two MFMA steps per DMA");
+#pragma unroll
+  for (int c = 0; c < kD; c++) lds_dma16_sc1(hsrc + 1024 * c + 16 * lane, hdst + 1024 * c);
   const int j = lane & 15, gb = lane >> 4;
-  const uint8_t *bt = rec + 128 * (gb >> 1) + 64 * (gb & 1) + 8 * (j & (kTerms - 1));
-  f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+  const uint8_t *bt = hdst + 128 * (gb >> 1) + 64 * (gb & 1) + 8 * (j & (kTerms - 1));
+  f32x4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   constexpr int PD = 2;  // B of step s is read two steps ahead
   uint2 pb[PD][4];
+  __builtin_amdgcn_s_waitcnt(vm_wait(kD - 1));  // steps 0 and 1
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
   for (int s = 0; s < PD; s++) {
     pb[s][0] = *reinterpret_cast<const uint2 *>(bt + 512 * s);
@@ -140,6 +163,10 @@ __device__ __forceinline__ f32x4 tile_mfma_h(const TileRegs<NSMAX> &r, const uin
   for (int s = 0; s < NSMAX; s++) {
     const uint2 b0 = pb[s % PD][0], b1 = pb[s % PD][1], b2 = pb[s % PD][2], b3 = pb[s % PD][3];
     if (s + PD < NSMAX) {
+      if ((s + PD) % 2 == 0) {  // the first step of a DMA: wait for it
+        wait_vmcnt_upto15(kD - 1 - (s + PD) / 2);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      }
       pb[s % PD][0] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD));
       pb[s % PD][1] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD) + 32);
       pb[s % PD][2] = *reinterpret_cast<const uint2 *>(bt + 512 * (s + PD) + 256);
@@ -149,12 +176,40 @@ __device__ __forceinline__ f32x4 tile_mfma_h(const TileRegs<NSMAX> &r, const uin
     const uint4 a = r.raw[s];
     const i32x8 A = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
     const i32x8 B = {(int)b0.x, (int)b0.y, (int)b1.x, (int)b1.y, (int)b2.x, (int)b2.y, (int)b3.x, (int)b3.y};
-    if (s & 1)
-      acc1 = mfma_fp4_fp8(s & 3, A, B, acc1, r.sw[s / 4], sb);
-    else
-      acc0 = mfma_fp4_fp8(s & 3, A, B, acc0, r.sw[s / 4], sb);
+    acc[s % 4] = mfma_fp4_fp8(s & 3, A, B, acc[s % 4], r.sw[s / 4], sb);
   }
-  return acc0 + acc1;
+  return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+// The extra gate_up tile of gate_up block b (index e in [0, X) of the X = k TPS - 4 n_gu tiles past
+// the first 4 n_gu), or -1. Workgroups are dispatched in index order, breadth first over the CUs,
+// so with a grid of G in (n_cu, 2 n_cu] blocks i and i + n_cu share a CU (measured: 97 % of the
+// pairs), and a CU's share of the weight stream sets when it is done (measured: a CU streaming 10
+// tiles finishes its gate_up tiles ~2.3 us after one streaming 8). The extra tiles therefore go
+// first to the gate_up blocks whose partner is a router block or missing (class 0), then to those
+// whose partner is a down block (class 1), then to the lower (class 2) and last to the upper
+// (class 3) block of each gate_up pair: every CU streams at most one tile more than the lightest
+// CU of two full blocks. The classes partition the gate_up blocks [R, R + n_gu) into the
+// intervals below; a block's rank is the count of blocks before it in class order. Other grids
+// spread the extra tiles evenly.
+__host__ __device__ inline int layer_extra_tile(int b, int n_rt, int n_gu, int n_dn, int n_cu, int X) {
+  const int G = n_rt + n_gu + n_dn, N = n_cu, R = n_rt, i = R + b;
+  if (G <= N || G > 2 * N || R >= N) {
+    const int lo = (int)((long long)b * X / n_gu), hi = (int)((long long)(b + 1) * X / n_gu);
+    return hi > lo ? lo : -1;
+  }
+  const int iv[4][2] = {{G - N, N + R},                                   // partner router / none
+                        {R + n_gu - N, G - N},                            // partner down
+                        {R - N, R + n_gu - N < G - N ? R + n_gu - N : G - N},  // lower of a gate_up pair
+                        {N + R, N + R + n_gu}};                           // upper of a gate_up pair
+  int rank = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int lo = iv[c][0] > R ? iv[c][0] : R, hi = iv[c][1] < R + n_gu ? iv[c][1] : R + n_gu;
+    if (i >= lo && i < hi) return rank + (i - lo) < X ? rank + (i - lo) : -1;
+    rank += hi > lo ? hi - lo : 0;
+  }
+  return -1;  // (unreachable: the classes cover every gate_up block)
 }
 
 __device__ __forceinline__ LogitCopy *logit_copy(void *sync, int r) {
@@ -403,13 +458,14 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
     }
     ep = s_ep;
     // 3. this wavefront's gate_up tile: tile 4b + wv; and for X of the blocks (spread evenly)
-    //    one of the X = k * TPS - 4 * n_gu tiles past the first 4 * n_gu (X <= n_gu), split by K
-    //    over the 4 wavefronts (steps [6 wv, 6 wv + 6)), so its bytes stream with the others.
+    //    one of the X = k * TPS - 4 * n_gu tiles past the first 4 * n_gu (X <= n_gu; which blocks:
+    //    layer_extra_tile), split by K over the 4 wavefronts (steps [6 wv, 6 wv + 6)), so its
+    //    bytes stream with the others.
     //    Tile u is row tile u % TPS (rows 16 t .. 16 t + 15 -> h[8t, 8t+8)) of slot u / TPS;
     //    tiles of dropped slots are skipped (uniformly over the block: 4b .. 4b+3 share a slot).
     const int n_tiles = K * TPS, W = 4 * n_gu, X = n_tiles > W ? n_tiles - W : 0;
-    const int e_lo = (int)((long long)b * X / n_gu), e_hi = (int)((long long)(b + 1) * X / n_gu);
-    const int u0 = 4 * b + wv, ux = e_hi > e_lo ? W + e_lo : n_tiles;
+    const int ex = X > 0 ? layer_extra_tile(b, la.n_rt, n_gu, la.n_dn, la.n_cu, X) : -1;
+    const int u0 = 4 * b + wv, ux = ex >= 0 ? W + ex : n_tiles;
     const int slot0 = u0 / TPS, tt0 = u0 - slot0 * TPS, slotx = ux / TPS, ttx = ux - slotx * TPS;
     const bool act0 = u0 < n_tiles && slot0 < sel, actx = ux < n_tiles && slotx < sel;
     const uint8_t *rec0 = a.base + (size_t)(act0 ? s_order[slot0] : s_order[0]) * a.stride;
@@ -546,8 +602,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
   }
   // 3. wavefront 0 waits until every gate_up block has published (its replica of the block flags
   //    reads epoch + 1); then wavefront `slot` brings its slot's h record (the kTerms term rows)
-  //    into LDS, 1 KB per instruction, straight into LDS (the last one only on the lanes inside
-  //    the rows, so no byte of a neighbour's record is written)
+  //    into LDS, 1 KB per instruction, straight into LDS, and sweeps it as it lands
   bool wfail = false;
   if (wv == 0 && sel > 0) {
     const uint32_t want = s_ep + 1;
@@ -573,21 +628,12 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
   __syncthreads();
   MOE_TRACE(2);
   wfail = s_wfail[0];
-  if (ok && !wfail) {
-    const uint8_t *src = la.hterm + (size_t)slot * kHRecBytes;
-    uint8_t *dst = s_h + (size_t)slot * kHRecBytes;
-#pragma unroll
-    for (int cix = 0; cix < kHRecBytes / 1024; cix++)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src + (size_t)cix * 1024) + lane,
-                                       (__attribute__((address_space(3))) void *)(dst + (size_t)cix * 1024),
-                                       16, 0, 16);
-    wait_mem();
-  }
   MOE_TRACE(3);
   if (ok && !wfail) {
-    const uint8_t *hrec = s_h + (size_t)slot * kHRecBytes;
+    // the slot's h record into LDS, the MFMAs following the DMAs as they land
     const uint32_t sb = j < kTerms ? (uint32_t)(127 + la.hexp - 4 * j) * 0x01010101u : 0u;
-    const f32x4 acc = tile_mfma_h<kLayerNs>(r, hrec, sb, lane);
+    const f32x4 acc = tile_mfma_h_stream<kLayerNs>(r, la.hterm + (size_t)slot * kHRecBytes,
+                                                   s_h + (size_t)slot * kHRecBytes, sb, lane);
     float v[4];
     sum_terms(acc, v);
     if (j == 0) {
@@ -628,6 +674,7 @@ void layer_geometry(LayerArgs &la, int n_cu) {
   la.n_tps = (int)a.gu.tiles;
   la.n_dn = (int)a.dn.tiles;
   la.n_rt = (a.E + kLayerWaves - 1) / kLayerWaves;
+  la.n_cu = n_cu;
   const int tiles = a.k * la.n_tps;
   const int lo = (tiles + 4) / 5, hi = (tiles + 3) / 4;
   la.n_gu = std::min(hi, std::max(lo, 2 * n_cu - la.n_rt - la.n_dn));

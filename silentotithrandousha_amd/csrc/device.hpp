@@ -778,6 +778,31 @@ __device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ void st_agent64(uint64_t *p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
+// outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima). n must fit
+// the 6-bit vmcnt field: a count outside [0, 63] reaches the non-constexpr function below, and
+// since __builtin_amdgcn_s_waitcnt takes only a constant expression, such a wait does not compile.
+__host__ __device__ inline int vmcnt_outside_6_bits() { return 0; }
+constexpr int vm_wait(int n) {
+  return n >= 0 && n <= 63 ? (0x0F70 | (n & 0xF) | ((n >> 4) << 14)) : vmcnt_outside_6_bits();
+}
+// The same with lgkmcnt 0: also this wavefront's LDS operations complete.
+constexpr int vm_lgkm_wait(int n) { return vm_wait(n) & ~0x0F00; }
+
+// s_waitcnt vmcnt(n) for n in [0, 15] held in a variable that loop unrolling makes a constant (the
+// switch then folds to one instruction; the builtin itself takes only a constant expression).
+__device__ __forceinline__ void wait_vmcnt_upto15(int n) {
+#define MOE_VM_CASE(k) \
+  case k: __builtin_amdgcn_s_waitcnt(vm_wait(k)); break;
+  switch (n) {
+    MOE_VM_CASE(0) MOE_VM_CASE(1) MOE_VM_CASE(2) MOE_VM_CASE(3) MOE_VM_CASE(4) MOE_VM_CASE(5)
+    MOE_VM_CASE(6) MOE_VM_CASE(7) MOE_VM_CASE(8) MOE_VM_CASE(9) MOE_VM_CASE(10) MOE_VM_CASE(11)
+    MOE_VM_CASE(12) MOE_VM_CASE(13) MOE_VM_CASE(14)
+    default: __builtin_amdgcn_s_waitcnt(vm_wait(15)); break;
+  }
+#undef MOE_VM_CASE
+}
+
 // Wait until every memory operation this wavefront issued has completed.
 __device__ __forceinline__ void wait_mem() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);

@@ -31,16 +31,6 @@ namespace moe {
 // B in LDS, per K-step: the entries' record steps one after the other (GemmRecT<NT>::kStep bytes
 // each, as the LDS-DMA copies them: each DMA reads whole record steps, a few rows per instruction).
 
-// s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
-// outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima). n must fit
-// the 6-bit vmcnt field: a count outside [0, 63] reaches the non-constexpr function below, and
-// since __builtin_amdgcn_s_waitcnt takes only a constant expression, such a wait does not compile.
-__host__ __device__ inline int vmcnt_outside_6_bits() { return 0; }
-constexpr int vm_wait(int n) {
-  return n >= 0 && n <= 63 ? (0x0F70 | (n & 0xF) | ((n >> 4) << 14)) : vmcnt_outside_6_bits();
-}
-// The same with lgkmcnt 0: also this wavefront's LDS operations complete.
-constexpr int vm_lgkm_wait(int n) { return vm_wait(n) & ~0x0F00; }
 
 // LDS-DMA of 16 (dwordx4) or 4 (dword) bytes per lane: lane l's bytes land at LDS address
 // lds + l * size (lds uniform over the wavefront). Written as inline assembly so that the compiler does not see these LDS writes:

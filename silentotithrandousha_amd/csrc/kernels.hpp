@@ -161,6 +161,7 @@ struct LayerArgs {
   int n_gu;              //                           gate_up blocks
   int n_dn;              //                           down blocks = down tiles
   int n_rt;              //                           router blocks, ceil(E / 4)
+  int n_cu;              //                           compute units of the device
 };
 size_t layer_sync_bytes();
 size_t layer_hterm_bytes();
