@@ -120,6 +120,7 @@ struct GemmB {
 // bytes per cycle of 8-byte reads): the pair chunk is read whole by both lanes of a pair, so 16
 // lanes share one address pair-wise and the reads of a 32-lane half have no bank conflicts; the
 // first-16-byte reads (records 304 bytes apart) take two passes where 8-byte reads took two each.
+// (Tails in the block order 0, 2, 1, 3, read by lane groups g and g ^ 2, cost 4 % at prefill.)
 template <int NT>
 __device__ __forceinline__ void gemm_read_b_t(GemmB<NT> &b, const uint8_t *eb, int g, int t) {
   const uint4 x = *reinterpret_cast<const uint4 *>(eb + (6 * t + g) * 16);
@@ -295,6 +296,121 @@ __device__ __forceinline__ void gemm_mfma_ops(f32x4 (&acc)[RT][CGW], const GemmO
     for (int c = C0; c < C1; c++) asm volatile("" : "+v"(acc[r][c]));
 }
 
+// ---- the 32x32x64 form (v_mfma_scale_f32_32x32x64_f8f6f4) of the 512 x 64 two-ahead shape: a
+//      wavefront holds 4 row tiles of 32 rows (its 8 tile16 chunks taken in pairs) x 32 entries,
+//      and a K-step of 128 is two 64-value halves h. Lane layouts (measured on gfx950): A lane l =
+//      row l % 32, K-block 2h + l / 32 of the step (16 bytes of E2M1, its E8M0 scale); B lane l =
+//      entry l % 32, the same K-block (24 bytes of E2M3, its scale); accumulator v of lane l = row
+//      8 (v / 4) + 4 (l / 32) + v % 4, entry l % 32. The A operand comes from the tile16 chunks as
+//      stored: lane m = (l % 16) + 16 (2h + l / 32) of chunk (l % 32) / 16 of the pair, so the same
+//      DMA layout serves both forms; a lane reads each term's 48 bytes of a step as two 16-byte and
+//      two 8-byte reads (none discarded); a step is 24 MFMAs of 32 x 32 x 64 where the 16 x 16 x 128
+//      form issues 48 (measured: 1.66x the issue cycles for 2x the work). Measured slower than the
+//      16 x 16 x 128 form at prefill all the same (gate_up 581 against 548 us, down 315 against
+//      306): the loop is bound by its LDS reads and waits, not the MFMA issue, and the 16-register
+//      accumulators at the 256-register limit make the compiler move them between steps.
+template <int NT>
+struct Gemm32Ops {
+  uint4 a[4][2];       // [row tile][half]
+  uint32_t sa[4][2];   // A scale of the step (byte 0)
+  i32x8 b[NT][2];      // [term][half]: the lane's 24 bytes of E2M3 (the MFMA operand; built as read,
+                       // so no wider load spans two fields and the operands stay in registers)
+  uint32_t sb[NT][2];  // B scale of the step (byte 0)
+};
+
+// The wavefront's A-scale words of the current 4 steps for (row tile R, half h), from the 4-step
+// scale buffer: words of the tile16 chunk and lane the A operand of (R, h) comes from.
+template <int RT>
+__device__ __forceinline__ void gemm32_read_sw4(uint32_t (&sw4)[4][2], const uint8_t *sbuf, int wr, int lane) {
+  const int m0 = lane & 15, u = lane >> 5, cpair = (lane & 31) >> 4;
+#pragma unroll
+  for (int R = 0; R < 4; R++)
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      sw4[R][h] = *reinterpret_cast<const uint32_t *>(sbuf + (wr * RT + 2 * R + cpair) * 256 + 4 * (m0 + 16 * (2 * h + u)));
+}
+
+// Every operand of one K-step for the wavefront, half 0 first (its MFMAs can start while half 1's
+// reads are in flight).
+template <int RT, int NT, int kBufB>
+__device__ __forceinline__ void gemm32_read_ops(Gemm32Ops<NT> &o, const uint8_t *slot, const uint32_t (&sw4)[4][2],
+                                                int wr, int wc, int lane, int sh) {
+  constexpr int kEntryStep = GemmRecT<NT>::kStep;
+  const int j = lane & 31, u = lane >> 5, m0 = lane & 15, cpair = (lane & 31) >> 4;
+  const uint8_t *ab = slot + kBufB + wr * RT * 1024, *eb = slot + (32 * wc + j) * kEntryStep;
+  const uint8_t *scp = eb + (GemmRecT<NT>::kChunks - 1) * 16;
+  uint32_t w[NT];
+  if constexpr (NT == 1) {
+    w[0] = *reinterpret_cast<const uint32_t *>(scp);
+  } else {
+    const uint4 sc = *reinterpret_cast<const uint4 *>(scp);
+    const uint32_t ww[3] = {sc.x, sc.y, sc.z};
+#pragma unroll
+    for (int t = 0; t < NT; t++) w[t] = ww[t];
+  }
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+#pragma unroll
+    for (int R = 0; R < 4; R++) {
+      o.a[R][h] = *reinterpret_cast<const uint4 *>(ab + (2 * R + cpair) * 1024 + 16 * (m0 + 16 * (2 * h + u)));
+      o.sa[R][h] = sw4[R][h] >> sh;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      // the operand's 6 registers must be contiguous: the 16 head bytes and the 8 tail bytes of
+      // block 2h + u are two reads straight into them
+      const uint4 pv = *reinterpret_cast<const uint4 *>(eb + (6 * t + 2 * h + u) * 16);
+      const uint2 qv = *reinterpret_cast<const uint2 *>(eb + (6 * t + 4) * 16 + 8 * (2 * h + u));
+      o.b[t][h] = i32x8{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w, (int)qv.x, (int)qv.y, 0, 0};
+      o.sb[t][h] = w[t] >> (8 * (2 * h + u));
+      // (the compiler would merge neighbouring 8-byte tail reads into one wider read and copy)
+      asm volatile("" ::: "memory");
+    }
+  }
+}
+
+// The MFMAs of half H of a step (per row tile R: terms t = 0, 1, .. in turn, so every output
+// accumulates half 0's terms then half 1's), with dma(0) before them and dma(1 .. NI - 1) spread
+// over them, as gemm_mfma_ops. Every MFMA issues, as in the 16 x 16 x 128 shapes: rows past the
+// matrix compute on clamped rows that are not stored, and the second half of the last step on
+// zero-scale weights and zero activations (adds exact zeros); a branch around them made the
+// compiler copy the accumulators and operands between the paths. The empty asm keeps the MFMAs
+// before the barrier that follows.
+template <int NT, int H, int NI, typename F>
+__device__ __forceinline__ void gemm32_mfma_half(f32x16 (&acc)[4], const Gemm32Ops<NT> &o, F &&dma) {
+  constexpr int NM = NT * 4;
+  if constexpr (NI > 0) dma(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+#pragma unroll
+    for (int R = 0; R < 4; R++) {
+      {
+        const uint4 &av = o.a[R][H];
+        const i32x8 A = {(int)av.x, (int)av.y, (int)av.z, (int)av.w, 0, 0, 0, 0};
+        const i32x8 &B = o.b[t][H];
+        // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
+        acc[R] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, acc[R], 4, 2, 0, (int)o.sa[R][H], 0,
+                                                                 (int)o.sb[t][H]);
+      }
+      const int m = t * 4 + R;
+#pragma unroll
+      for (int i = 1; i < NI; i++) {
+        if (m == max((i * NM) / (NI > 0 ? NI : 1) - 1, 0)) {
+          __builtin_amdgcn_sched_barrier(0);
+          dma(i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // (the accumulators as inputs only: an in-out operand redefines them, and the compiler then moves
+  // all 64 registers between the steps' register assignments)
+#pragma unroll
+  for (int R = 0; R < 4; R++) asm volatile("" ::"v"(acc[R]));
+}
+
 // MFMAs of one K-step for a wavefront with many row tiles (one wavefront per SIMD): the B
 // operands of all CG column groups are read once and held for the step; row tiles go in pairs,
 // the A chunks of the next pair read while the MFMAs of this pair run (8 independent
@@ -364,9 +480,12 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
 template <int MODE, typename S>
 constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP; }
 
-template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT>
+// M32: the 32x32x64 form of the 512 x 64 two-ahead shape (gemm32_*): the same DMA layout, ring and
+// waits; other MFMAs, operand reads and epilogue staging.
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
+  static_assert(!M32 || (RT == 8 && CGW == 2 && S::kTwoAhead), "the 32x32 form: 128 rows x 32 entries per wavefront");
   using G = GemmRecT<NT>;  // the activation records (x or h) of the launch
   constexpr int W = S::W, CG = CGW, kChunks = G::kChunks, kEntryStep = G::kStep;
   // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
@@ -591,6 +710,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   for (int r = 0; r < RT; r++)
 #pragma unroll
     for (int c = 0; c < CG; c++) acc[r][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  f32x16 acc32[M32 ? 4 : 1];  // the 32x32 form's accumulators: row tile R of 32 rows
+#pragma unroll
+  for (int r = 0; r < (M32 ? 4 : 1); r++) acc32[r] = f32x16{};
 
   // ---- bias of the wavefront's rows into LDS by DMA before the K loop (complete at the first
   //      wait), read in the epilogue
@@ -734,11 +856,43 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
     }
     GEMM_BARRIER();
+    if constexpr (M32) {
+      uint32_t sw32_[4][2];
+#define GEMM_STEP32(st, cur, jj)                                                                    \
+  do {                                                                                              \
+    Gemm32Ops<NT> ops_;                                                                             \
+    if ((jj) == 0) gemm32_read_sw4<RT>(sw32_, s_sc[((st) >> 2) & 1], wr, lane);                     \
+    gemm32_read_ops<RT, NT, S::kBufB>(ops_, cur, sw32_, wr, wc, lane, 8 * (jj));                    \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    gemm32_mfma_half<NT, 0, 0>(acc32, ops_, [](int) {});                                            \
+    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));                                                   \
+    GEMM_BARRIER();                                                                                 \
+    const int ld_ = (st) + 2;                                                                       \
+    auto dma_ = [&](int k_) { dma2(k_, ld_, cur); };                                                \
+    if ((st) + 2 < ns)                                                                              \
+      gemm32_mfma_half<NT, 1, S::kDma + S::kDmaA + ((jj) == 2 ? S::kDmaA : 0)>(acc32, ops_, dma_);  \
+    else                                                                                            \
+      gemm32_mfma_half<NT, 1, 0>(acc32, ops_, dma_);                                                \
+    const bool more_ = (st) + 2 < ns;                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    if (more_) GEMM_VM_WAIT(S::kDmaA + ((jj) == 2 ? S::kDmaA : 0));                                 \
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));                                               \
+    GEMM_BARRIER();                                                                                 \
+  } while (0)
+      for (int s = 0; s < ns; s += 4) {
+        GEMM_STEP32(s, s_r0, 0);
+        if (s + 1 < ns) GEMM_STEP32(s + 1, s_r1, 1);
+        if (s + 2 < ns) GEMM_STEP32(s + 2, s_r0, 2);
+        if (s + 3 < ns) GEMM_STEP32(s + 3, s_r1, 3);
+      }
+#undef GEMM_STEP32
+    } else {
     for (int s = 0; s < ns; s += 4) {
       GEMM_STEP2(s, s_r0, 0);
       if (s + 1 < ns) GEMM_STEP2(s + 1, s_r1, 1);
       if (s + 2 < ns) GEMM_STEP2(s + 2, s_r0, 2);
       if (s + 3 < ns) GEMM_STEP2(s + 3, s_r1, 3);
+    }
     }
 #undef GEMM_STEP2
 #undef GEMM_BARRIER
@@ -814,6 +968,25 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
 #pragma unroll
       for (int hbk = 0; hbk < NHB; hbk++) {
         if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
+        if constexpr (M32) {
+          // h block hbk = the wavefront's 32-row tiles 2 hbk, 2 hbk + 1; lane (entry l % 32, u =
+          // l / 32) holds rows 8 v + 4 u .. +3 of each (v = 0..3): h values 16 Rr + 4 v + 2 u, + 1
+          if (nloc <= 0) break;
+          const int e32 = lane & 31, u = lane >> 5;
+          float *se = st32 + (hbk * kWaveCols + e32) * kRow;
+#pragma unroll
+          for (int Rr = 0; Rr < 2; Rr++) {
+            const f32x16 &av = acc32[2 * hbk + Rr];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {  // rows 32 R + 8 v + 4 u: tile16 chunk 2 R + v / 2, row 8 (v % 2) + 4 u
+              const float4 b4 = *reinterpret_cast<const float4 *>(
+                  s_bias + (wv * kBiasTiles + 4 * hbk + 2 * Rr + v / 2) * 16 + 8 * (v % 2) + 4 * u);
+              *reinterpret_cast<float2 *>(se + 16 * Rr + 4 * v + 2 * u) =
+                  make_float2(swiglu_fast(av[4 * v] + b4.x, av[4 * v + 1] + b4.y, a.limit),
+                              swiglu_fast(av[4 * v + 2] + b4.z, av[4 * v + 3] + b4.w, a.limit));
+            }
+          }
+        } else {
 #pragma unroll
         for (int c = 0; c < CG; c++) {
           if (16 * c >= nloc) break;
@@ -825,6 +998,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
             *reinterpret_cast<float2 *>(se + 8 * r + 2 * g) =
                 make_float2(swiglu_fast(av[0] + b4.x, av[1] + b4.y, a.limit), swiglu_fast(av[2] + b4.z, av[3] + b4.w, a.limit));
           }
+        }
         }
       }
       constexpr int kPairs = NHB * kWaveCols;
@@ -922,6 +1096,29 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   } else {
     float *out = reinterpret_cast<float *>(a.out);
     const int R = (int)d.rows;
+    if constexpr (M32) {
+      // lane (entry l % 32, u = l / 32): rows 32 Rt + 8 v + 4 u .. +3 of the wavefront (tile16 chunk
+      // 2 Rt + v / 2, inside the matrix or not as a whole)
+      const int e = 32 * wc + (lane & 31), u = lane >> 5;
+      if (e < ncol) {
+#pragma unroll
+        for (int Rt = 0; Rt < 4; Rt++) {
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const int ch = 2 * Rt + v / 2;
+            if (!tv[ch]) continue;
+            const float4 b4 = *reinterpret_cast<const float4 *>(s_bias + (wv * kBiasTiles + ch) * 16 + 8 * (v % 2) + 4 * u);
+            const f32x16 &av = acc32[Rt];
+            float4 o;
+            o.x = canon_nan(rclamp(av[4 * v] + b4.x, -65504.0f, 65504.0f));
+            o.y = canon_nan(rclamp(av[4 * v + 1] + b4.y, -65504.0f, 65504.0f));
+            o.z = canon_nan(rclamp(av[4 * v + 2] + b4.z, -65504.0f, 65504.0f));
+            o.w = canon_nan(rclamp(av[4 * v + 3] + b4.w, -65504.0f, 65504.0f));
+            *reinterpret_cast<float4 *>(out + (size_t)(beg + e) * R + (t0 + ch) * 16 + 8 * (v % 2) + 4 * u) = o;
+          }
+        }
+      }
+    } else {
 #pragma unroll
     for (int r = 0; r < RT; r++) {
       if (!tv[r]) continue;
@@ -938,6 +1135,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         o.w = canon_nan(rclamp(acc[r][c][3] + b4.w, -65504.0f, 65504.0f));
         *reinterpret_cast<float4 *>(out + (size_t)(beg + e) * R + row) = o;
       }
+    }
     }
   }
     if constexpr (!kPersist) break;  // (no loop at all in the other shapes' code)
@@ -959,7 +1157,7 @@ static int device_cus() {
   return c;
 }
 
-template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT>
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false>
 static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
@@ -973,7 +1171,7 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   a.n_blocks = (int)blocks;
   // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
   const size_t grid = gemm_persistent<MODE, S>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1006,6 +1204,7 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   }
   if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
   if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
+  if (a.shape == 10) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, true>(a, s);
   if (mean >= 48)
     return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
   if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);

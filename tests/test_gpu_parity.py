@@ -623,7 +623,17 @@ def test_batch_gemm_block_shapes_identical(orc):
     d.set_gemm_shape(0)
     for (shape, down), o in zip(shapes[1:], outs[1:]):
         assert np.array_equal(outs[0], o), f"shape {shape} down {down}"
-    assert_rel_l2(outs[1], orc.moe_layer(x, L, k)[0], "gemm shape 1")
+    want = orc.moe_layer(x, L, k)[0]
+    assert_rel_l2(outs[1], want, "gemm shape 1")
+    # the 32 x 32 x 64 form (code 10) sums 64 products per MFMA where the others sum 128: the same
+    # products, another f32 summation order
+    for shape, down in [(10, 10), (1, 10), (0, 10)]:
+        d.set_gemm_shape(shape, down)
+        o = d.layer_forward(0, x, k)
+        e = rel_l2(o, outs[0])
+        assert e < 2e-5, f"shape {shape} down {down}: {e:.2e} from the 16 x 16 x 128 shapes"
+        assert_rel_l2(o, want, f"gemm shape {shape} down {down}")
+    d.set_gemm_shape(0)
     d.close()
 
 
@@ -640,11 +650,15 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
     for shape, down in shapes:
         disp20.set_gemm_shape(shape, down)
         outs.append(disp20.layer_forward(0, x, 4))
+    disp20.set_gemm_shape(10, 10)  # the 32 x 32 x 64 form; experts average 8 entries, so most
+    o32 = disp20.layer_forward(0, x, 4)  # tiles hold fewer than 32 (their second wavefront pair idles)
     disp20.set_gemm_shape(0)
     disp20.set_batch_gemm(1)
     assert_rel_l2(outs[0], want, "20B gemm T=64")
     for (shape, down), o in zip(shapes[1:], outs[1:]):
         assert np.array_equal(outs[0], o), f"shape {shape} down {down}"
+    assert rel_l2(o32, outs[0]) < 1e-4
+    assert_rel_l2(o32, want, "20B gemm T=64 shape 10")
 
 
 def _prefill_parity(orc, d, layer, T, seed, n_sample):
@@ -683,7 +697,14 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
         d.set_gemm_shape(shape, down)
         o = d.layer_forward(0, x, k)
         assert np.array_equal(got, o), f"T={T} E={E} shape {shape} down {down}"
+    # the 32 x 32 x 64 form: the same products in another f32 summation order (an h value whose
+    # third E2M3 term rounds the other way moves its entry by ~2^-14 of the block maximum)
+    d.set_gemm_shape(10, 10)
+    o = d.layer_forward(0, x, k)
     d.set_gemm_shape(0)
+    e = rel_l2(o, got)
+    assert e < 1e-4, f"T={T} E={E} shape 10: {e:.2e} from the default shape"
+    assert_rel_l2(o[sample], want, f"T={T} E={E} shape 10 sampled tokens vs oracle")
 
 
 def test_prefill_4096_tokens_20b(orc, disp20, layer20):
@@ -733,7 +754,7 @@ def test_prefill_partial_router_block_20b(orc, disp20, layer20):
     assert_rel_l2(gq[rows], wq, "T=2053 quantized", tol=2e-4)
 
 
-def _act_quant_check(orc, d, layer, x, k, what, n_sample=None, seed=0, shapes=()):
+def _act_quant_check(orc, d, layer, x, k, what, n_sample=None, seed=0, shapes=(), shapes_close=()):
     """MOE_OPT_ACT_QUANT 1: top-k exact; the output (or n_sample sampled tokens) within the
     tolerance of the fp32 path on MXFP6 activations (orc.moe_layer_mxfp6: the GPU and the oracle
     quantize the same x to the same codes; h differs by summation order, so an h value at a
@@ -748,6 +769,10 @@ def _act_quant_check(orc, d, layer, x, k, what, n_sample=None, seed=0, shapes=()
         for shape, down in shapes:
             d.set_gemm_shape(shape, down)
             assert np.array_equal(d.layer_forward(0, x, k), got), f"{what}: shape {shape} down {down}"
+        for shape, down in shapes_close:  # the 32 x 32 x 64 form: another f32 summation order
+            d.set_gemm_shape(shape, down)
+            e = rel_l2(d.layer_forward(0, x, k), got)
+            assert e < 2e-4, f"{what}: shape {shape} down {down}: {e:.2e}"
         d.set_gemm_shape(0)
     finally:
         d.set_act_quant(0)
@@ -775,7 +800,7 @@ def test_act_quant_small(orc, shape):
         d.preload_layer(0, L)
         x = syn.hidden(T, H, seed=481 + T)
         _act_quant_check(orc, d, L, x, k, f"act_quant {shape}",
-                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9)])
+                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9)], shapes_close=[(10, 10)])
     finally:
         d.close()
 
@@ -787,7 +812,7 @@ def test_act_quant_20b_decode64_and_prefill(orc, disp20, layer20):
     _act_quant_check(orc, disp20, layer20, syn.hidden(64, H20, seed=490), 4, "act_quant 20B T=64",
                      shapes=[(5, 5), (7, 7), (7, 5)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(512, H20, seed=493), 4, "act_quant 20B T=512",
-                     n_sample=32, seed=494, shapes=[(1, 0), (9, 9), (0, 9)])
+                     n_sample=32, seed=494, shapes=[(1, 0), (9, 9), (0, 9)], shapes_close=[(10, 10)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(4096, H20, seed=491), 4, "act_quant 20B T=4096",
                      n_sample=48, seed=492, shapes=[(1, 0), (1, 7), (9, 9), (9, 0)])
 
