@@ -90,8 +90,9 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * wavefronts (each 128 rows x 64 entries; quantized activations only, the default there for
  * experts averaging 96+ entries; with the exact split it selects the default shape), 10 the
  * 512 x 64 block of 8 wavefronts on the 32 x 32 x 64 block-scaled MFMA (each 128 rows x 32
- * entries) (tuning; codes 0-9 give identical results, code 10 the same to f32 rounding: its MFMA
- * sums 64 products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
+ * entries), 11 the 512 x 128 block of 8 wavefronts each holding 256 rows x 32 entries (B held
+ * for a K-step) (tuning; codes 0-9 and 11 give identical results, code 10 the same to f32 rounding:
+ * its MFMA sums 64 products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
  * (0, default: as MOE_OPT_GEMM_SHAPE).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
  * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results

@@ -53,6 +53,16 @@ __device__ __forceinline__ void lds_dma4(const void *g, const void *lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
+// The LDS byte address of p (a pointer into a __shared__ object).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+// LDS-DMA of 16 bytes per lane to the LDS byte address la (wavefront-uniform), from sbase + voff.
+__device__ __forceinline__ void lds_dma16_sa(uint32_t voff, const void *sbase, uint32_t la) {
+  la = __builtin_amdgcn_readfirstlane(la);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(la) : "memory", "m0");
+}
+
 // The same with a wavefront-uniform 64-bit base in SGPRs and a 32-bit per-lane offset
 // (global address = sbase + voff): one VGPR per lane instead of a 64-bit pointer.
 __device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void *sbase, const void *lds) {
@@ -657,7 +667,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   do {                                                                                              \
     const uint8_t *bb_ = a.brec + (size_t)(step) * G::kStep;                                        \
     _Pragma("unroll") for (int i = 0; i < S::kDma; i++) {                                           \
-      lds_dma16_s(boff[i], bb_, W * i + wvu >= S::kGroups ? s_dummy : (sl) + 1024 * (W * i + wvu)); \
+      /* (the two LDS objects as 32-bit LDS addresses before the select: a select of the generic \
+         pointers hit a compiler error in one shape) */                                          \
+      lds_dma16_sa(boff[i], bb_, W * i + wvu >= S::kGroups ? lds_addr(s_dummy) : lds_addr((sl) + 1024 * (W * i + wvu))); \
     }                                                                                               \
     const uint32_t ao_ = min((uint32_t)(step) * 1024u + 16u * lane, a_last);                        \
     _Pragma("unroll") for (int i = 0; i < S::kDmaA; i++)                                            \
@@ -1205,6 +1217,7 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
   if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
   if (a.shape == 10) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, true>(a, s);
+  if (a.shape == 11) return launch_gemm_shape<MODE, 16, 2, 2, 4, 2, NT>(a, s);
   if (mean >= 48)
     return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
   if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);

@@ -616,7 +616,7 @@ def test_batch_gemm_block_shapes_identical(orc):
     d.set_batch_gemm(2)
     outs = []
     shapes = [(0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (8, 0), (0, 4), (2, 5), (5, 4),
-              (7, 6), (8, 8)]
+              (7, 6), (8, 8), (11, 11), (0, 11)]
     for shape, down in shapes:
         d.set_gemm_shape(shape, down)
         outs.append(d.layer_forward(0, x, k))
@@ -693,7 +693,7 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
     d.set_batch_gemm(1)
     e = rel_l2(got, ref)
     assert e < 6e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
-    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4)]:
+    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4), (11, 11)]:
         d.set_gemm_shape(shape, down)
         o = d.layer_forward(0, x, k)
         assert np.array_equal(got, o), f"T={T} E={E} shape {shape} down {down}"
