@@ -160,6 +160,12 @@ class StreamEvents:
     def stop(self):
         self._ok(self.hip.hipEventRecord(self.ev[1], self.stream), "hipEventRecord")
 
+    def sync(self):
+        """hipStreamSynchronize of the stream: the end of a timed window (the library's
+        moe_synchronize also reads the kernels' error word back, a device-to-host copy that is
+        no part of the timed work; callers run it after the window)."""
+        self._ok(self.hip.hipStreamSynchronize(self.stream), "hipStreamSynchronize")
+
     def elapsed_ms(self):
         self._ok(self.hip.hipEventSynchronize(self.ev[1]), "hipEventSynchronize")
         ms = ctypes.c_float()
@@ -236,6 +242,7 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
             graphs.append((capture(disp, step, n_full * G, rem), 1))
     disp.synchronize()
     region = StreamEvents(L.moe_stream(disp.ctx))
+    region.sync()
     t0 = time.perf_counter()
     region.start()
     if G:
@@ -246,8 +253,9 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
         for i in range(steps):
             step(i)
     region.stop()
-    disp.synchronize()
+    region.sync()
     elapsed = time.perf_counter() - t0
+    disp.synchronize()  # the kernels' error word (a bounded wait that ran out) is reported here
     region_ms = region.elapsed_ms()
     region.close()
     for g, _ in graphs:
@@ -377,8 +385,9 @@ def run_matvec(steps, warmup, graph=True):
         for i in range(steps):
             one(i)
     region.stop()
-    disp.synchronize()
+    region.sync()
     el = time.perf_counter() - t0
+    disp.synchronize()
     region_s = region.elapsed_ms() / 1e3
     region.close()
     if g:
@@ -422,8 +431,9 @@ def run_lm_head(steps, warmup, H=2880, V=201088):
     for _ in range(steps):
         disp.dispatch_lm_head_device(x, V, y)
     region.stop()
-    disp.synchronize()
+    region.sync()
     el = time.perf_counter() - t0
+    disp.synchronize()
     region_s = region.elapsed_ms() / 1e3
     region.close()
     byts = V * H * 4 + H * 4 + V * 4
@@ -462,8 +472,9 @@ def run_lm_head_bf16(steps, warmup, H=2880, V=201088):
     for _ in range(steps):
         disp.dispatch_lm_head_device(x, V, y)
     region.stop()
-    disp.synchronize()
+    region.sync()
     el = time.perf_counter() - t0
+    disp.synchronize()
     region_s = region.elapsed_ms() / 1e3
     region.close()
     for b in (x, y):
