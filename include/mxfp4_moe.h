@@ -81,7 +81,8 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * least 4 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
  * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical.
  * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM: 0 (default) by the mean entries per
- * expert (48+: 512 rows x 64 entries in 8 wavefronts; 24+: 128 x 32 in 2; else 128 x 16 in 2);
+ * expert (48+: 512 rows x 64 entries in 8 wavefronts; 24+: 128 x 32 in 2; else the streamed form
+ * of code 12, or 128 x 16 in 2 where that does not fit);
  * for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2; 2 and 3
  * force 256-row x 32- and 16-entry blocks of 4 wavefronts, 4 the 128-row x 16-entry block of 4
  * wavefronts (down only; gate_up takes 3), 5 the 128 x 16 block of 2 wavefronts, 6 a 64 x 16
@@ -91,8 +92,12 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * experts averaging 96+ entries; with the exact split it selects the default shape), 10 the
  * 512 x 64 block of 8 wavefronts on the 32 x 32 x 64 block-scaled MFMA (each 128 rows x 32
  * entries), 11 the 512 x 128 block of 8 wavefronts each holding 256 rows x 32 entries (B held
- * for a K-step) (tuning; codes 0-9 and 11 give identical results, code 10 the same to f32 rounding:
- * its MFMA sums 64 products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
+ * for a K-step), 12 the streamed form for a few entries per expert (one workgroup per CU taking a
+ * contiguous share of the (16-entry chunk x 64 rows (gate_up) or 32 rows (down)) units, four at
+ * a time: the weights through register rings, the shared activation records through an LDS ring
+ * loaded by a fifth wavefront; launches it does not fit take the 128 x 16 block), 13 the same
+ * with other ring depths (tuning; codes 0-9 and 11-13 give identical results, code 10
+ * the same to f32 rounding: its MFMA sums 64 products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
  * (0, default: as MOE_OPT_GEMM_SHAPE).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
  * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results

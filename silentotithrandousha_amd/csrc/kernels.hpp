@@ -122,6 +122,9 @@ struct GemmArgs {
   int terms;                 // E2M3 terms per activation value: kGemmTerms, or 1 (quantized mode)
 };
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
+// The streamed form for batches of a few entries per expert (gemm_stream.hip); hipErrorNotSupported
+// when the launch does not fit it.
+hipError_t launch_gemm_stream(GemvMode mode, const GemmArgs &a, hipStream_t s, bool alt);
 
 // Single-token MoE layer in two launches (decode.hip).
 struct DecodeArgs {

@@ -616,7 +616,7 @@ def test_batch_gemm_block_shapes_identical(orc):
     d.set_batch_gemm(2)
     outs = []
     shapes = [(0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (8, 0), (0, 4), (2, 5), (5, 4),
-              (7, 6), (8, 8), (11, 11), (0, 11)]
+              (7, 6), (8, 8), (11, 11), (0, 11), (12, 12), (13, 13), (12, 0), (0, 13)]
     for shape, down in shapes:
         d.set_gemm_shape(shape, down)
         outs.append(d.layer_forward(0, x, k))
@@ -637,6 +637,37 @@ def test_batch_gemm_block_shapes_identical(orc):
     d.close()
 
 
+@pytest.mark.parametrize("shape", [(512, 512, 16, 4, 300), (256, 128, 8, 2, 2), (1024, 512, 32, 4, 129),
+                                   (256, 256, 8, 4, 64), (512, 1024, 64, 4, 48), (1024, 2880, 8, 4, 2),
+                                   (64, 64, 8, 4, 40)])
+def test_batch_gemm_streamed_identical(orc, shape):
+    """The streamed grouped GEMM (codes 12 and 13, and the default below 24 entries per expert:
+    one workgroup per CU taking four units at a time from a contiguous share of 16-entry chunks
+    x row groups, rings running on across rounds) against the 128 x 16 block (code 5): the same
+    MFMAs in the same order, identical results; ragged expert loads (1 to 75 entries), experts
+    with entries past one 16-entry chunk, rounds and workgroup ranges that cross chunks, K = 512
+    (4 of the 24 loop positions real) and K = 2880 (down: 23); H = I = 64, where gate_up has 2
+    units per chunk, falls back to the block shapes."""
+    H, I, E, k, T = shape
+    L = syn.make_layer(H, I, E, seed=470 + T, scale_lo=120, scale_hi=126, router_sigma=0.1)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    try:
+        d.preload_layer(0, L)
+        x = syn.hidden(T, H, seed=471 + T)
+        d.set_batch_gemm(2)
+        d.set_gemm_shape(5, 5)
+        base = d.layer_forward(0, x, k)
+        for shape_c, down in [(12, 12), (13, 13), (12, 5), (5, 13), (0, 0)]:
+            d.set_gemm_shape(shape_c, down)
+            o = d.layer_forward(0, x, k)
+            assert np.array_equal(base, o), f"{shape}: shape {shape_c} down {down}"
+        d.set_gemm_shape(0)
+        want = orc.moe_layer(x, L, k)[0]
+        assert_rel_l2(base, want, f"gemm {shape}")
+    finally:
+        d.close()
+
+
 def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
     """The block shapes at the 20B dimensions, where K = 2880 takes 23 steps: with a ring of
     three slots the loop ends with the repeat of the last step still loading into the slot that
@@ -646,7 +677,7 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
     want = orc.moe_layer(x, layer20, 4)[0]
     disp20.set_batch_gemm(2)
     outs = []
-    shapes = [(0, 0), (3, 3), (5, 5), (6, 6), (7, 7), (2, 2), (5, 4)]
+    shapes = [(0, 0), (3, 3), (5, 5), (6, 6), (7, 7), (2, 2), (5, 4), (12, 12), (13, 13), (12, 5)]
     for shape, down in shapes:
         disp20.set_gemm_shape(shape, down)
         outs.append(disp20.layer_forward(0, x, 4))
@@ -800,7 +831,8 @@ def test_act_quant_small(orc, shape):
         d.preload_layer(0, L)
         x = syn.hidden(T, H, seed=481 + T)
         _act_quant_check(orc, d, L, x, k, f"act_quant {shape}",
-                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9)], shapes_close=[(10, 10)])
+                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9), (12, 12), (13, 0)],
+                         shapes_close=[(10, 10)])
     finally:
         d.close()
 
@@ -810,7 +842,7 @@ def test_act_quant_20b_decode64_and_prefill(orc, disp20, layer20):
     entries: the 512-row x 64-entry shape at K = 2880) and at 4096 tokens (512 entries: the
     512 x 128 block), quantized activations."""
     _act_quant_check(orc, disp20, layer20, syn.hidden(64, H20, seed=490), 4, "act_quant 20B T=64",
-                     shapes=[(5, 5), (7, 7), (7, 5)])
+                     shapes=[(5, 5), (7, 7), (7, 5), (12, 12), (13, 13)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(512, H20, seed=493), 4, "act_quant 20B T=512",
                      n_sample=32, seed=494, shapes=[(1, 0), (9, 9), (0, 9)], shapes_close=[(10, 10)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(4096, H20, seed=491), 4, "act_quant 20B T=4096",
