@@ -296,6 +296,11 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
         d_bytes = active * gu_b + T * H * 4 + T * k * I * 4
         d_flops = 2.0 * T * k * 2 * I * H
         kname = "k_gemm_fp8<gate_up>" if dom == "gate_up" else "k_decode_gate_up"
+        # the library's choice of the grouped GEMM (gemm.hip launch_gemm_mode): the streamed form
+        # below 24 entries per expert on average, unless a block shape is forced
+        shape = model.disp.gemm_shape
+        if dom == "gate_up" and (shape in (12, 13) or (shape == 0 and T * k // max(1, min(E, T * k)) < 24)):
+            kname = "k_gemm_stream<gate_up>"
     mfma_bound = T >= 4096  # config 4: arithmetic intensity above the MXFP4 ridge point
     res = {
         "value": round(tokens_per_s, 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,

@@ -154,23 +154,26 @@ __global__ __launch_bounds__(64 * kStrWaves) __attribute__((amdgpu_waves_per_eu(
   // ---- the experts' chunks: lane l of round r holds active expert 64 r + l: its entry range,
   //      id, chunk count and first chunk (prefix sum)
   constexpr int kR = kMaxExperts / 64;
+  // (the lists hold max_active (+1) entries: lanes below it load before the count is known, in
+  // the same round trip, and lanes past the count are cleared)
   const int ma = min(a.max_active, kMaxExperts);
-  const int na = min(*a.n_active, ma);
   int lo[kR], hi[kR], id[kR], c0[kR], nc[kR];
-  int NC = 0;
 #pragma unroll
   for (int r = 0; r < kR; r++) {
     const int i = 64 * r + lane;
     lo[r] = hi[r] = 0;
     id[r] = 0;
-    if (i < na) {
+    if (i < ma) {
       lo[r] = a.active_off[i];
       hi[r] = a.active_off[i + 1];
       id[r] = a.active_ids[i];
     }
   }
+  const int na = min(*a.n_active, ma);
+  int NC = 0;
 #pragma unroll
   for (int r = 0; r < kR; r++) {
+    if (64 * r + lane >= na) lo[r] = hi[r] = 0;
     nc[r] = (hi[r] - lo[r] + kStrCols - 1) / kStrCols;
     int incl = nc[r];
 #pragma unroll

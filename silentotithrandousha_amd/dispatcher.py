@@ -78,6 +78,7 @@ class GpuMoeDispatcher:
                                ctypes.byref(ctx)))
         self._ctx = ctx.value
         self.lm_vocab = 0
+        self.gemm_shape = 0  # MOE_OPT_GEMM_SHAPE as last set (set_gemm_shape)
 
     @property
     def ctx(self):
@@ -164,6 +165,7 @@ class GpuMoeDispatcher:
         from ._ffi import MOE_OPT_GEMM_SHAPE, MOE_OPT_GEMM_SHAPE_DOWN
         check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_SHAPE, int(shape)))
         check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_SHAPE_DOWN, int(down)))
+        self.gemm_shape = int(shape)
 
     def set_gemm_band(self, band):
         """Row blocks per band of the grouped GEMM's per-XCD tile order (0 default; tuning only)."""
