@@ -296,11 +296,16 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
         d_bytes = active * gu_b + T * H * 4 + T * k * I * 4
         d_flops = 2.0 * T * k * 2 * I * H
         kname = "k_gemm_fp8<gate_up>" if dom == "gate_up" else "k_decode_gate_up"
-        # the library's choice of the grouped GEMM (gemm.hip launch_gemm_mode): the streamed form
-        # below 24 entries per expert on average, unless a block shape is forced
+        # the library's choice of the grouped GEMM (gemm.hip launch_gemm_mode, by the mean entries
+        # per expert): the wide streamed form at 14-44 and 60-72, the streamed form below 24,
+        # unless a shape is forced
         shape = model.disp.gemm_shape
-        if dom == "gate_up" and (shape in (12, 13) or (shape == 0 and T * k // max(1, min(E, T * k)) < 24)):
-            kname = "k_gemm_stream<gate_up>"
+        mean = T * k // max(1, min(E, T * k))
+        if dom == "gate_up":
+            if shape == 14 or (shape == 0 and 14 <= mean and (mean < 44 or 60 <= mean < 72)):
+                kname = "k_gemm_wide<gate_up>"
+            elif shape in (12, 13) or (shape == 0 and mean < 24):
+                kname = "k_gemm_stream<gate_up>"
     mfma_bound = T >= 4096  # config 4: arithmetic intensity above the MXFP4 ridge point
     res = {
         "value": round(tokens_per_s, 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
@@ -663,8 +668,8 @@ def main():
                          "weights), 0 the five-kernel batch path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
-    ap.add_argument("--gemm-shape", type=int, default=0, choices=range(14), help="grouped GEMM block shape (tuning)")
-    ap.add_argument("--gemm-shape-down", type=int, default=0, choices=range(14),
+    ap.add_argument("--gemm-shape", type=int, default=0, choices=range(15), help="grouped GEMM block shape (tuning)")
+    ap.add_argument("--gemm-shape-down", type=int, default=0, choices=range(15),
                     help="block shape of the down GEMM alone (0: as --gemm-shape; tuning)")
     ap.add_argument("--gemm-band", type=int, default=0, help="grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)")
     ap.add_argument("--batch-gemm", type=int, default=1, choices=(0, 1, 2),

@@ -81,8 +81,9 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * least 4 entries, or always when 2; otherwise, and when 0, through the per-tile GEMV kernels
  * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical.
  * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM: 0 (default) by the mean entries per
- * expert (48+: 512 rows x 64 entries in 8 wavefronts; 24+: 128 x 32 in 2; else the streamed form
- * of code 12, or 128 x 16 in 2 where that does not fit);
+ * expert (14 to 44, 60 to 72, and for the down GEMM 14 to 72: the wide streamed form of code 14;
+ * otherwise 48+: 512 rows x 64 entries in 8 wavefronts; 24+: 128 x 32 in 2; else the streamed form
+ * of code 12, or 128 x 16 in 2 where neither fits);
  * for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2; 2 and 3
  * force 256-row x 32- and 16-entry blocks of 4 wavefronts, 4 the 128-row x 16-entry block of 4
  * wavefronts (down only; gate_up takes 3), 5 the 128 x 16 block of 2 wavefronts, 6 a 64 x 16
@@ -96,8 +97,11 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * contiguous share of the (16-entry chunk x 64 rows (gate_up) or 32 rows (down)) units, four at
  * a time: the weights through register rings, the shared activation records through an LDS ring
  * loaded by a fifth wavefront; launches it does not fit take the 128 x 16 block), 13 the same
- * with other ring depths (tuning; codes 0-9 and 11-13 give identical results, code 10
- * the same to f32 rounding: its MFMA sums 64 products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
+ * with other ring depths, 14 the wide streamed form for tens of entries per expert (units of
+ * 64 (gate_up) or 32 (down) rows x a group of up to 5 16-entry chunks of one expert, so every
+ * weight tile streams once per group; launches it does not fit take the default) (tuning; codes
+ * 0-9 and 11-14 give identical results, code 10 the same to f32 rounding: its MFMA sums 64
+ * products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
  * (0, default: as MOE_OPT_GEMM_SHAPE).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
  * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results

@@ -1218,6 +1218,19 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   }
   if (a.shape == 5) return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
   if (a.shape == 7) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
+  // the wide streamed form (gemm_wide.hip): every weight tile once per group of up to 80 entries.
+  // By default for experts averaging 14 to 44 entries, 60 to 72 (gate_up) and 14 to 72 (down):
+  // measured on the 20B and 120B layers (K = 2880) against the shapes below (gate_up / down, us):
+  // 120B at 1024 tokens (32 entries) 302 / 177 against 425 / 227, at 2048 (64) 394 / 223 against
+  // 417 / 265; 20B at 320 tokens (40) 93 / 58 against 145 / 77. At 48-56 entries the 512 x 64
+  // block's gate_up is faster (309 against 348 us at 120B x 1536: its 64-entry tiles then hold
+  // nearly every expert whole), and from ~80 entries every expert needs two groups.
+  const bool wide_default = mean >= 14 && (mean < 44 || (mean >= 60 && mean < 72) ||
+                                           (MODE == GEMV_DOWN && mean < 72));
+  if (a.shape == 14 || (a.shape == 0 && wide_default)) {
+    const hipError_t e = launch_gemm_wide(MODE == GEMV_GATE_UP ? GEMV_GATE_UP : GEMV_DOWN, a, s);
+    if (e != hipErrorNotSupported) return e;
+  }
   // experts averaging fewer than 24 entries: the streamed form (gemm_stream.hip; measured on the
   // 20B layer at 32-128 tokens: gate_up 6-12 us and down 1-8 us faster than the 128 x 16 blocks)
   if (a.shape == 12 || a.shape == 13 || (a.shape == 0 && mean < 24)) {

@@ -25,18 +25,16 @@
 // wave waiting for one load waits for all older ones). The same MFMAs as k_gemm_fp8 (per output:
 // step by step, terms 0, 1, 2 in turn, from zero) give the same bits.
 //
-// The epilogue's global stores are inline assembly: with stores pending among the loads the
-// compiler treats the counter as unordered and waits for every load (the ring would drain at
-// each round's end), while a store the count does not include can only make a wait longer, never
-// shorter. Each ends with wait states of its own (the compiler's hazard checks do not see an
-// assembly store: it rewrote a store's data registers with the next instruction, before the store
-// had read them; measured, the first 8 bytes of 16-byte stores came out wrong).
+// The epilogue's global stores are inline assembly (str_st*, stream.hpp): with stores pending
+// among the loads the compiler would wait for every load, and the ring would drain at each
+// round's end.
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
 
 #include "device.hpp"
 #include "kernels.hpp"
+#include "stream.hpp"
 
 namespace moe {
 
@@ -48,39 +46,6 @@ constexpr int kStrPos = 24;     // loop positions of a round (kGemmNs steps)
 static_assert(kGemmNs == kStrPos, "one loop position per record step");
 constexpr int kStrRow = 36;     // staging row of the gate_up epilogue (floats)
 constexpr int kStrBiasPos = 12; // position of a round whose loads include the unit's bias
-
-typedef unsigned int str_u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void str_st16(void *p, uint4 v) {
-  const u32x4 w = {v.x, v.y, v.z, v.w};
-  asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 4" ::"v"(p), "v"(w) : "memory");
-}
-__device__ __forceinline__ void str_st8(void *p, uint2 v) {
-  const str_u32x2 w = {v.x, v.y};
-  asm volatile("global_store_dwordx2 %0, %1, off\n\ts_nop 4" ::"v"(p), "v"(w) : "memory");
-}
-__device__ __forceinline__ void str_st1(void *p, uint32_t v) {
-  asm volatile("global_store_byte %0, %1, off\n\ts_nop 4" ::"v"(p), "v"(v) : "memory");
-}
-
-// LDS-DMA of 16 bytes per lane from sbase + voff (wavefront-uniform base, 32-bit lane offset) to
-// LDS byte address la + 16 l.
-__device__ __forceinline__ void str_dma16(uint32_t voff, const void *sbase, uint32_t la) {
-  la = __builtin_amdgcn_readfirstlane(la);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(la) : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t str_lds(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
-}
-
-// f(integral_constant<int, i>) for i = B .. E - 1: loop positions whose index is a constant from
-// the start, so every ring slot, wait count and scale-buffer index is a constant.
-template <int B, int E, typename F>
-__device__ __forceinline__ void str_static_for(F &&f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    str_static_for<B + 1, E>(f);
-  }
-}
 
 // The B loader's DMAs per position and its wait before each step (NSR real steps per round;
 // NSR = 24 takes any ns <= 24, steps from ns on loaded as in-range repeats and not computed).

@@ -125,6 +125,10 @@ hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
 // The streamed form for batches of a few entries per expert (gemm_stream.hip); hipErrorNotSupported
 // when the launch does not fit it.
 hipError_t launch_gemm_stream(GemvMode mode, const GemmArgs &a, hipStream_t s, bool alt);
+// The wide streamed form for batches of tens of entries per expert (gemm_wide.hip): every weight
+// tile streams once per group of up to 5 16-entry chunks; hipErrorNotSupported when the launch
+// does not fit it.
+hipError_t launch_gemm_wide(GemvMode mode, const GemmArgs &a, hipStream_t s);
 
 // Single-token MoE layer in two launches (decode.hip).
 struct DecodeArgs {

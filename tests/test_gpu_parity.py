@@ -616,7 +616,7 @@ def test_batch_gemm_block_shapes_identical(orc):
     d.set_batch_gemm(2)
     outs = []
     shapes = [(0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (7, 0), (8, 0), (0, 4), (2, 5), (5, 4),
-              (7, 6), (8, 8), (11, 11), (0, 11), (12, 12), (13, 13), (12, 0), (0, 13)]
+              (7, 6), (8, 8), (11, 11), (0, 11), (12, 12), (13, 13), (12, 0), (0, 13), (14, 14), (14, 0), (0, 14)]
     for shape, down in shapes:
         d.set_gemm_shape(shape, down)
         outs.append(d.layer_forward(0, x, k))
@@ -639,7 +639,7 @@ def test_batch_gemm_block_shapes_identical(orc):
 
 @pytest.mark.parametrize("shape", [(512, 512, 16, 4, 300), (256, 128, 8, 2, 2), (1024, 512, 32, 4, 129),
                                    (256, 256, 8, 4, 64), (512, 1024, 64, 4, 48), (1024, 2880, 8, 4, 2),
-                                   (64, 64, 8, 4, 40)])
+                                   (64, 64, 8, 4, 40), (256, 256, 4, 4, 600)])
 def test_batch_gemm_streamed_identical(orc, shape):
     """The streamed grouped GEMM (codes 12 and 13, and the default below 24 entries per expert:
     one workgroup per CU taking four units at a time from a contiguous share of 16-entry chunks
@@ -647,7 +647,9 @@ def test_batch_gemm_streamed_identical(orc, shape):
     MFMAs in the same order, identical results; ragged expert loads (1 to 75 entries), experts
     with entries past one 16-entry chunk, rounds and workgroup ranges that cross chunks, K = 512
     (4 of the 24 loop positions real) and K = 2880 (down: 23); H = I = 64, where gate_up has 2
-    units per chunk, falls back to the block shapes."""
+    units per chunk, falls back to the block shapes. The wide streamed form (code 14: units of a
+    group of up to 5 chunks of one expert) on the same cases, including 600 entries per expert (8
+    groups each, rounds of 2 units, most workgroups without a round)."""
     H, I, E, k, T = shape
     L = syn.make_layer(H, I, E, seed=470 + T, scale_lo=120, scale_hi=126, router_sigma=0.1)
     d = GpuMoeDispatcher(H, I, 7.0)
@@ -657,7 +659,7 @@ def test_batch_gemm_streamed_identical(orc, shape):
         d.set_batch_gemm(2)
         d.set_gemm_shape(5, 5)
         base = d.layer_forward(0, x, k)
-        for shape_c, down in [(12, 12), (13, 13), (12, 5), (5, 13), (0, 0)]:
+        for shape_c, down in [(12, 12), (13, 13), (12, 5), (5, 13), (0, 0), (14, 14), (14, 12), (5, 14)]:
             d.set_gemm_shape(shape_c, down)
             o = d.layer_forward(0, x, k)
             assert np.array_equal(base, o), f"{shape}: shape {shape_c} down {down}"
@@ -677,7 +679,8 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
     want = orc.moe_layer(x, layer20, 4)[0]
     disp20.set_batch_gemm(2)
     outs = []
-    shapes = [(0, 0), (3, 3), (5, 5), (6, 6), (7, 7), (2, 2), (5, 4), (12, 12), (13, 13), (12, 5)]
+    shapes = [(0, 0), (3, 3), (5, 5), (6, 6), (7, 7), (2, 2), (5, 4), (12, 12), (13, 13), (12, 5), (14, 14),
+              (14, 5)]
     for shape, down in shapes:
         disp20.set_gemm_shape(shape, down)
         outs.append(disp20.layer_forward(0, x, 4))
@@ -693,8 +696,9 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
 
 
 def _prefill_parity(orc, d, layer, T, seed, n_sample):
-    """A T-token layer through the default path (the 8-token router blocks, the 512-row x
-    64-entry grouped GEMM at the real K): top-k indices of every token exact against the
+    """A T-token layer through the default path (the 8-token router blocks, the grouped GEMM at
+    the real K: the 512-row x 64-entry block at 512 entries per expert, the wide streamed form at
+    64): top-k indices of every token exact against the
     oracle's router; n_sample tokens (per-token outputs do not depend on the other tokens)
     within the tolerance of the oracle; the whole output within 6e-4 of the GEMV path; the
     other large-batch block shape and the 4-wavefront shapes bit-identical.
@@ -724,7 +728,7 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
     d.set_batch_gemm(1)
     e = rel_l2(got, ref)
     assert e < 6e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
-    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4), (11, 11)]:
+    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4), (11, 11), (14, 14), (0, 14)]:
         d.set_gemm_shape(shape, down)
         o = d.layer_forward(0, x, k)
         assert np.array_equal(got, o), f"T={T} E={E} shape {shape} down {down}"
@@ -831,7 +835,8 @@ def test_act_quant_small(orc, shape):
         d.preload_layer(0, L)
         x = syn.hidden(T, H, seed=481 + T)
         _act_quant_check(orc, d, L, x, k, f"act_quant {shape}",
-                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9), (12, 12), (13, 0)],
+                         shapes=[(1, 0), (5, 0), (7, 0), (5, 7), (1, 5), (9, 9), (0, 9), (12, 12), (13, 0),
+                                 (14, 14), (14, 0)],
                          shapes_close=[(10, 10)])
     finally:
         d.close()
@@ -844,7 +849,7 @@ def test_act_quant_20b_decode64_and_prefill(orc, disp20, layer20):
     _act_quant_check(orc, disp20, layer20, syn.hidden(64, H20, seed=490), 4, "act_quant 20B T=64",
                      shapes=[(5, 5), (7, 7), (7, 5), (12, 12), (13, 13)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(512, H20, seed=493), 4, "act_quant 20B T=512",
-                     n_sample=32, seed=494, shapes=[(1, 0), (9, 9), (0, 9)], shapes_close=[(10, 10)])
+                     n_sample=32, seed=494, shapes=[(1, 0), (9, 9), (0, 9), (14, 14)], shapes_close=[(10, 10)])
     _act_quant_check(orc, disp20, layer20, syn.hidden(4096, H20, seed=491), 4, "act_quant 20B T=4096",
                      n_sample=48, seed=492, shapes=[(1, 0), (1, 7), (9, 9), (9, 0)])
 
