@@ -140,22 +140,12 @@ struct WideLoader {
   static_assert(max_outstanding() <= 63, "the DMAs in flight fit the vmcnt field");
 };
 
-// The B operand of one term of one chunk for lane (j, g), as read: the first 16 bytes of the lane's
-// block and the 16-byte chunk holding its last 8 (and those of block g ^ 1), selected at use. Both
-// are 16-byte reads: entries 304 bytes apart put 8 consecutive lanes' 16-byte reads in distinct
-// banks, while 8-byte reads of the tails put lanes j and j + 8 in one bank.
-struct WideT {
+// One item's B operand as read: the first 16 bytes of the lane's block, the 16-byte chunk holding
+// its last 8 (selected by g & 1 at use), and the term's scale word (byte g = the lane's block).
+struct WideT3 {
   uint4 x, y;
+  uint32_t sc;
 };
-template <int NT>
-__device__ __forceinline__ void wide_read_t(WideT &b, const uint8_t *eb, int t, int g) {
-  using G = GemmRecT<NT>;
-  b.x = *reinterpret_cast<const uint4 *>(eb + t * G::kTermBytes + 16 * g);
-  b.y = *reinterpret_cast<const uint4 *>(eb + t * G::kTermBytes + 64 + 16 * (g >> 1));
-}
-__device__ __forceinline__ i32x8 wide_b(const WideT &b, bool odd) {
-  return i32x8{(int)b.x.x, (int)b.x.y, (int)b.x.z, (int)b.x.w, (int)(odd ? b.y.z : b.y.x), (int)(odd ? b.y.w : b.y.y), 0, 0};
-}
 
 // A round: its group's expert (matrix and bias), first entry and entry count, and the first row
 // group of its four units.
@@ -420,7 +410,11 @@ __global__ __launch_bounds__(64 * kWideWaves) __attribute__((amdgpu_waves_per_eu
   constexpr int WT = 2 * RT, NCHH = (L::kEntries / 2 + kWideCols - 1) / kWideCols;
   const int u0 = 2 * (wvu >> 1), eh = wvu & 1;
   WideRound cur = round(0);
-  uint32_t sw[WT];  // the scale words of the current quad
+  constexpr int NI = NCHH * NT, BA = 3, BQ = BA + 1;
+  const bool odd = (g & 1) != 0;
+  WideT3 bq[BQ];          // the item operands in flight
+  uint4 av[2][WT];        // the weight chunks of a step, by step parity
+  uint32_t swq[2][WT];    // the scale words of a quad, by quad parity
   f32x4 acc[NCHH][WT];
 #pragma unroll
   for (int c = 0; c < NCHH; c++)
@@ -437,69 +431,115 @@ __global__ __launch_bounds__(64 * kWideWaves) __attribute__((amdgpu_waves_per_eu
     uint32_t ebo[NCHH];
 #pragma unroll
     for (int c = 0; c < NCHH; c++) ebo[c] = (uint32_t)min(mbeg + kWideCols * c + j, L::kEntries - 1) * G::kStep;
+    // items i = (term i / NCHH, chunk i % NCHH) of a step: per output the terms 0, 1, 2 in turn
+    // (the order of every other shape), and NCHH x WT MFMAs between two on one accumulator (chunk by
+    // chunk, the next term's MFMA waited for the last one's result). Item (P, i) is read BA items
+    // ahead of its MFMAs into bq[(NI P + i) % BQ]: its 24 operand bytes (two 16-byte reads) and its
+    // term's scale word. Every item is read (past the group's entries stale values) and only the
+    // MFMAs of chunks from nchk on are skipped: with reads on both sides of a branch the compiler
+    // could not count the LDS reads in flight and waited for all of them before every item.
+    auto rd_item = [&](auto pc2, auto ic) {
+      constexpr int P2 = decltype(pc2)::value, i = decltype(ic)::value, tt = i / NCHH, c = i % NCHH;
+      const uint8_t *eb = &sB[P2 % kWidePB][0] + ebo[c];
+      WideT3 &b = bq[(NI * P2 + i) % BQ];
+      b.x = *reinterpret_cast<const uint4 *>(eb + tt * G::kTermBytes + 16 * g);
+      b.y = *reinterpret_cast<const uint4 *>(eb + tt * G::kTermBytes + 64 + 16 * (g >> 1));
+      b.sc = *reinterpret_cast<const uint32_t *>(eb + NT * G::kTermBytes + 4 * tt);
+    };
+    // the weight chunks of step P2 (and, at a quad's first step, its scale words), double-buffered
+    // by step parity
+    auto rd_a = [&](auto pc2) {
+      constexpr int P2 = decltype(pc2)::value;
+      if constexpr (P2 % 4 == 0) {
+#pragma unroll
+        for (int r = 0; r < WT; r++) swq[(P2 / 4) & 1][r] = sS[(P2 / 4) % NS][u0 + r / RT][r % RT][lane];
+      }
+#pragma unroll
+      for (int r = 0; r < WT; r++)
+        av[P2 & 1][r] = *reinterpret_cast<const uint4 *>(&sA[P2 % RA][u0 + r / RT][r % RT][16 * lane]);
+    };
+    auto mfma_item = [&](auto pc2, auto ic, int sh) {
+      constexpr int P2 = decltype(pc2)::value, i = decltype(ic)::value, c = i % NCHH;
+      const WideT3 &b = bq[(NI * P2 + i) % BQ];
+      const i32x8 B = {(int)b.x.x, (int)b.x.y, (int)b.x.z, (int)b.x.w, (int)(odd ? b.y.z : b.y.x),
+                       (int)(odd ? b.y.w : b.y.y), 0, 0};
+      const int sb = (int)(b.sc >> (8 * g));
+#pragma unroll
+      for (int r = 0; r < WT; r++) {
+        const uint4 &a4 = av[P2 & 1][r];
+        const i32x8 A = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
+        // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
+        acc[c][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[c][r], 4, 2, 0,
+                                                                      (int)(swq[(P2 / 4) & 1][r] >> sh), 0, sb);
+      }
+    };
     str_static_for<0, kWidePos>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
-      __builtin_amdgcn_sched_barrier(0);
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_barrier();  // the loaders' DMAs of step p complete; their slots of step p - 1 free
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      if constexpr (p < NSR) {
-        if (NSR == 23 || p < ns) {  // (NSR = 24: steps from ns on are repeats)
-          const uint8_t *slot = &sB[p % kWidePB][0];
-          if constexpr (p % 4 == 0) {
-#pragma unroll
-            for (int r = 0; r < WT; r++) sw[r] = sS[(p / 4) % NS][u0 + r / RT][r % RT][lane];
+      // barrier p: the loaders' DMAs of step p complete; their slots of step p - 1 free
+      auto bar = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      };
+      if constexpr (NSR == 23) {
+        // ---- K = 2880, every one of the 23 steps computed: pipelined across steps. Barrier p + 1
+        //      is taken inside step p, right after its last LDS reads complete, and the first BA
+        //      items and the weight chunks of step p + 1 are read during the last BA items' MFMAs
+        //      of step p (with the barrier at each step's start, every wavefront's first reads
+        //      queued at the LDS together while the MFMAs waited, and the last MFMAs ran with the
+        //      LDS idle: a step took about the sum of the two). Not across rounds: the epilogue
+        //      follows step 22.
+        if constexpr (p == 0 || p == kWidePos - 1) bar();
+        if constexpr (p < NSR) {
+          if constexpr (p == 0) {
+            rd_a(std::integral_constant<int, 0>{});
+            str_static_for<0, BA>([&](auto ic) { rd_item(std::integral_constant<int, 0>{}, ic); });
           }
-          uint4 av[WT];
-#pragma unroll
-          for (int r = 0; r < WT; r++) av[r] = *reinterpret_cast<const uint4 *>(&sA[p % RA][u0 + r / RT][r % RT][16 * lane]);
           const int sh = 8 * (p % 4);
-          // items i = (term i / NCHH, chunk i % NCHH): per output the terms 0, 1, 2 in turn (the
-          // order of every other shape), and NCHH x WT MFMAs between two on one accumulator (chunk
-          // by chunk, the next term's MFMA waited for the last one's result). Each item is read BA
-          // items ahead of its MFMAs (a ring of BA + 1 term operands), a chunk's scale words with
-          // its first term. Every item is read (past the group's entries stale values) and only
-          // the MFMAs of chunks from nchk on are skipped: with reads on both sides of a branch the
-          // compiler could not count the LDS reads in flight and waited for all of them before
-          // every item
-          constexpr int NI = NCHH * NT;
-          const bool odd = (g & 1) != 0;
-          constexpr int BA = 3, BQ = BA + 1;
-          WideT bq[BQ];
-          uint4 bsc[NCHH];  // the terms' scale words of each chunk
-          auto rd = [&](auto ic) {
-            constexpr int i = decltype(ic)::value, tt = i / NCHH, c = i % NCHH;
-            const uint8_t *eb = slot + ebo[c];
-            if constexpr (tt == 0) bsc[c] = *reinterpret_cast<const uint4 *>(eb + NT * G::kTermBytes);
-            wide_read_t<NT>(bq[i % BQ], eb, tt, g);
-          };
-          str_static_for<0, BA>([&](auto ic) {
-            constexpr int i = decltype(ic)::value;
-            if constexpr (i < NI) rd(ic);
-          });
           str_static_for<0, NI>([&](auto ic) {
-            constexpr int i = decltype(ic)::value, tt = i / NCHH, c = i % NCHH;
-            if constexpr (i + BA < NI) rd(std::integral_constant<int, i + BA>{});
-            __builtin_amdgcn_sched_barrier(0);  // the reads BA items ahead issue before this item's MFMAs
-            if (c < nchk) {
-              const i32x8 B = wide_b(bq[i % BQ], odd);
-              const uint32_t wsc = tt == 0 ? bsc[c].x : (tt == 1 ? bsc[c].y : bsc[c].z);
-              const int sb = (int)(wsc >> (8 * g));
-#pragma unroll
-              for (int r = 0; r < WT; r++) {
-                const i32x8 A = {(int)av[r].x, (int)av[r].y, (int)av[r].z, (int)av[r].w, 0, 0, 0, 0};
-                // cbsz 4: A is fp4 (E2M1); blgp 2: B is fp6 (E2M3)
-                acc[c][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[c][r], 4, 2, 0,
-                                                                              (int)(sw[r] >> sh), 0, sb);
+            constexpr int i = decltype(ic)::value, c = i % NCHH, ni = i + BA;
+            if constexpr (ni < NI) {
+              rd_item(pc, std::integral_constant<int, ni>{});
+            } else if constexpr (p + 1 < NSR) {
+              if constexpr (ni == NI) {
+                // this wavefront's reads of step p's slots complete before the loaders may refill them
+                __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));
+                bar();
+                rd_a(std::integral_constant<int, p + 1>{});
               }
+              rd_item(std::integral_constant<int, p + 1>{}, std::integral_constant<int, ni - NI>{});
             }
+            __builtin_amdgcn_sched_barrier(0);  // the reads BA items ahead issue before this item's MFMAs
+            if (c < nchk) mfma_item(pc, ic, sh);
             __builtin_amdgcn_sched_barrier(0);
           });
-          // the step's MFMAs stay here (IR passes otherwise sink them towards the epilogue)
 #pragma unroll
           for (int c = 0; c < NCHH; c++)
 #pragma unroll
             for (int r = 0; r < WT; r++) asm volatile("" ::"v"(acc[c][r]) : "memory");
+        }
+      } else {
+        // ---- K below 3072 other than 2880: steps from ns on are repeats, skipped at run time;
+        //      each step's reads follow its barrier
+        bar();
+        if constexpr (p < NSR) {
+          if (p < ns) {
+            rd_a(pc);
+            str_static_for<0, BA>([&](auto ic) { rd_item(pc, ic); });
+            const int sh = 8 * (p % 4);
+            str_static_for<0, NI>([&](auto ic) {
+              constexpr int i = decltype(ic)::value, c = i % NCHH;
+              if constexpr (i + BA < NI) rd_item(pc, std::integral_constant<int, i + BA>{});
+              __builtin_amdgcn_sched_barrier(0);
+              if (c < nchk) mfma_item(pc, ic, sh);
+              __builtin_amdgcn_sched_barrier(0);
+            });
+#pragma unroll
+            for (int c = 0; c < NCHH; c++)
+#pragma unroll
+              for (int r = 0; r < WT; r++) asm volatile("" ::"v"(acc[c][r]) : "memory");
+          }
         }
       }
       if constexpr (p == kWidePos - 1) {
