@@ -119,7 +119,11 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * MOE_OPT_GEMM_SHAPE(_DOWN) codes 2, 3, 4, 6 and 8 select the default shape. Changing it
  * re-lays out the context's h records: the call waits until the whole device is idle
  * (hipDeviceSynchronize), so forwards enqueued on any stream finish first, and it is refused
- * during graph capture. */
+ * during graph capture.
+ * MOE_OPT_LOCAL_GROUP: 1 (default) batches of at most 1024 (token, slot) entries whose gate_up
+ * GEMM runs in the streamed form have the GEMM's workgroups group the entries by expert
+ * themselves, from the top-k indices (the router then skips its grouping); 0 the router groups
+ * them (tuning; results identical). */
 enum moe_option {
   MOE_OPT_FUSED_DECODE = 1,
   MOE_OPT_SPIN_LIMIT = 2,
@@ -128,7 +132,8 @@ enum moe_option {
   MOE_OPT_GEMM_BAND = 5,
   MOE_OPT_MATVEC = 6,
   MOE_OPT_GEMM_SHAPE_DOWN = 7,
-  MOE_OPT_ACT_QUANT = 8
+  MOE_OPT_ACT_QUANT = 8,
+  MOE_OPT_LOCAL_GROUP = 9
 };
 int moe_set_option(moe_ctx *ctx, int option, int64_t value);
 

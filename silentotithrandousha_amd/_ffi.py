@@ -28,6 +28,7 @@ MOE_OPT_GEMM_BAND = 5
 MOE_OPT_MATVEC = 6
 MOE_OPT_GEMM_SHAPE_DOWN = 7
 MOE_OPT_ACT_QUANT = 8
+MOE_OPT_LOCAL_GROUP = 9
 
 _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p

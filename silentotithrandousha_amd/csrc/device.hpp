@@ -779,6 +779,38 @@ __device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ void st_agent64(uint64_t *p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Wavefront 0 of a block: from the per-expert entry counts cnt[0..E), the active experts in
+// ascending id (active_ids, active_off, *n_active; the entries of active expert i are
+// [active_off[i], active_off[i + 1])) and every expert's first entry base[e], by wave prefix
+// sums over 64 experts at a time.
+__device__ __forceinline__ void expert_list_wave(const int *cnt, int E, int lane, int *base, int32_t *active_ids,
+                                                 int32_t *active_off, int32_t *n_active) {
+  int off = 0, na = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e < E ? cnt[e] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o);
+      if (lane >= o) incl += u;
+    }
+    const uint64_t act = __ballot(c > 0);
+    const int slot = na + __popcll(act & ((1ull << lane) - 1ull));
+    if (e < E) base[e] = off + incl - c;
+    if (c > 0) {
+      active_ids[slot] = e;
+      active_off[slot] = off + incl - c;
+    }
+    off += __shfl(incl, 63);
+    na += __popcll(act);
+  }
+  if (lane == 0) {
+    active_off[na] = off;
+    *n_active = na;
+  }
+}
+
 // s_waitcnt immediate that waits until at most n vector-memory operations of the wavefront are
 // outstanding (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima). n must fit
 // the 6-bit vmcnt field: a count outside [0, 63] reaches the non-constexpr function below, and

@@ -1245,6 +1245,19 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
 }
 
+bool gemm_stream_local_ok(const GemmArgs &a);  // gemm_stream.hip
+
+// launch_gemm_mode's choice for gate_up with the exact split: the streamed form by default below 14
+// entries per expert on average (and for codes 12, 13), when it fits and the batch is small enough
+// for its workgroups to group the entries themselves.
+bool gemm_gate_up_groups_locally(const GemmArgs &a) {
+  if (a.terms != kGemmTerms || a.d.ns > (uint32_t)kGemmNs || a.d.rows % 64) return false;
+  const size_t active = std::max<size_t>(1, std::min<size_t>((size_t)a.max_active, a.n_entries));
+  const size_t mean = a.n_entries / active;
+  const bool stream = a.shape == 12 || a.shape == 13 || (a.shape == 0 && mean < 14);
+  return stream && a.n_entries > 0 && gemm_stream_local_ok(a);
+}
+
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s) {
   if (a.d.ns > (uint32_t)kGemmNs || (mode == GEMV_GATE_UP && a.d.rows % 64)) return hipErrorInvalidValue;
   if (a.terms == 1)

@@ -109,6 +109,14 @@ __global__ __launch_bounds__(64 * kStrWaves) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) float s_stage[kStrCompute][MODE == GEMV_GATE_UP ? kStrCols * kStrRow : 4];
   __shared__ int s_seg[kStrMaxSeg][3];         // expert, first entry, entry count
   __shared__ int s_row[kStrMaxSeg][kStrCols];  // B record row of each entry
+  // local grouping: entry n's expert, then its grouped position; grouped entry -> token; the
+  // experts' counts (then running ranks), first entries and the active list
+  __shared__ int s_ge[MODE == GEMV_GATE_UP ? kLocalGroupMax : 1];
+  __shared__ int s_esrc[MODE == GEMV_GATE_UP ? kLocalGroupMax : 1];
+  __shared__ int s_gcnt[MODE == GEMV_GATE_UP ? kMaxExperts : 1], s_gbase[MODE == GEMV_GATE_UP ? kMaxExperts : 1];
+  __shared__ int s_aid[MODE == GEMV_GATE_UP ? kMaxExperts : 1], s_aoff[MODE == GEMV_GATE_UP ? kMaxExperts + 1 : 1];
+  __shared__ int s_na;
+  __shared__ int s_ccnt[MODE == GEMV_GATE_UP ? kLocalGroupMax / 64 : 1][MODE == GEMV_GATE_UP ? kMaxExperts : 1];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int wvu = __builtin_amdgcn_readfirstlane(wv);
   const bool loader = wvu == kStrCompute;
@@ -123,18 +131,105 @@ __global__ __launch_bounds__(64 * kStrWaves) __attribute__((amdgpu_waves_per_eu(
   // the same round trip, and lanes past the count are cleared)
   const int ma = min(a.max_active, kMaxExperts);
   int lo[kR], hi[kR], id[kR], c0[kR], nc[kR];
+  const bool local = MODE == GEMV_GATE_UP && a.group_idx != nullptr;
+  int na;
+  if (local) {
+    // ---- the grouping of session.rs:943-972's entries by expert (k_route / bucket_block's: active
+    //      experts ascending, an expert's entries in entry order t k + slot), from the top-k
+    //      indices, in LDS. Entries in chunks of 64, chunk ch by wavefront ch % 5: per chunk the
+    //      count of each expert and each entry's rank among the chunk's entries of its expert
+    //      (9-bit match by ballots); per expert an exclusive prefix of its counts over the chunks
+    //      (a thread per expert); the expert list (wavefront 0); then every entry's position.
+    const int N = (int)a.n_entries, E = a.group_E, tid = threadIdx.x;
+    constexpr int kCh = kLocalGroupMax / 64, kPerW = (kCh + kStrWaves - 1) / kStrWaves;
+    const int nch = (N + 63) / 64;
+    for (int i = tid; i < nch * E; i += kStrWaves * 64) s_ccnt[i / E][i % E] = 0;
+    __syncthreads();
+    int ge_e[kPerW], ge_r[kPerW];
 #pragma unroll
-  for (int r = 0; r < kR; r++) {
-    const int i = 64 * r + lane;
-    lo[r] = hi[r] = 0;
-    id[r] = 0;
-    if (i < ma) {
-      lo[r] = a.active_off[i];
-      hi[r] = a.active_off[i + 1];
-      id[r] = a.active_ids[i];
+    for (int q = 0; q < kPerW; q++) {
+      const int ch = wv + kStrWaves * q, n = 64 * ch + lane;
+      ge_e[q] = ch < nch && n < N ? a.group_idx[n] : -1;
     }
+#pragma unroll
+    for (int q = 0; q < kPerW; q++) {
+      const int ch = wv + kStrWaves * q, e = ge_e[q];
+      const uint32_t v = (uint32_t)(e + 1);  // 0 .. kMaxExperts: 9 bits
+      uint64_t same = ~0ull;
+#pragma unroll
+      for (int bit = 0; bit < 9; bit++) {
+        const uint64_t bb = __ballot((v >> bit) & 1u);
+        same &= ((v >> bit) & 1u) ? bb : ~bb;
+      }
+      const uint64_t below = same & ((1ull << lane) - 1ull);
+      ge_r[q] = __popcll(below);
+      if (ch < nch && e >= 0 && below == 0) s_ccnt[ch][e] = __popcll(same);  // (the group's first lane)
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kStrWaves * 64) {
+      int run = 0;
+      for (int ch = 0; ch < nch; ch++) {
+        const int c = s_ccnt[ch][e];
+        s_ccnt[ch][e] = run;
+        run += c;
+      }
+      s_gcnt[e] = run;
+    }
+    __syncthreads();
+    if (wv == 0) expert_list_wave(s_gcnt, E, lane, s_gbase, s_aid, s_aoff, &s_na);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPerW; q++) {
+      const int ch = wv + kStrWaves * q, n = 64 * ch + lane, e = ge_e[q];
+      if (ch < nch && n < N) {
+        if (e >= 0) {
+          const int ge = s_gbase[e] + s_ccnt[ch][e] + ge_r[q];
+          s_esrc[ge] = n / a.group_k;
+          s_ge[n] = ge;
+        } else {
+          s_ge[n] = -1;
+        }
+      }
+    }
+    __syncthreads();
+    if (blockIdx.x == 0) {  // the lists for the down GEMM and the combine
+      const int nl = s_na;
+      for (int n = tid; n < N; n += kStrWaves * 64) {
+        a.w_pos[n] = s_ge[n];
+        a.w_entry_src[n] = s_esrc[n];  // (entries past the grouped ones: unread)
+      }
+      for (int i = tid; i <= nl; i += kStrWaves * 64) {
+        a.w_active_off[i] = s_aoff[i];
+        if (i < nl) a.w_active_ids[i] = s_aid[i];
+      }
+      if (tid == 0) *a.w_n_active = nl;
+    }
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const int i = 64 * r + lane;
+      lo[r] = hi[r] = 0;
+      id[r] = 0;
+      if (i < s_na) {
+        lo[r] = s_aoff[i];
+        hi[r] = s_aoff[i + 1];
+        id[r] = s_aid[i];
+      }
+    }
+    na = s_na;
+  } else {
+#pragma unroll
+    for (int r = 0; r < kR; r++) {
+      const int i = 64 * r + lane;
+      lo[r] = hi[r] = 0;
+      id[r] = 0;
+      if (i < ma) {
+        lo[r] = a.active_off[i];
+        hi[r] = a.active_off[i + 1];
+        id[r] = a.active_ids[i];
+      }
+    }
+    na = min(*a.n_active, ma);
   }
-  const int na = min(*a.n_active, ma);
   int NC = 0;
 #pragma unroll
   for (int r = 0; r < kR; r++) {
@@ -190,7 +285,7 @@ __global__ __launch_bounds__(64 * kStrWaves) __attribute__((amdgpu_waves_per_eu(
       if (q < nseg) {
         const int beg = s_seg[q][1], cnt = s_seg[q][2];
         const int e = beg + min(j, max(cnt, 1) - 1);
-        s_row[q][j] = a.entry_src ? a.entry_src[e] : e;
+        s_row[q][j] = local ? s_esrc[e] : (a.entry_src ? a.entry_src[e] : e);
       }
     }
   }
@@ -435,6 +530,10 @@ __global__ __launch_bounds__(64 * kStrWaves) __attribute__((amdgpu_waves_per_eu(
   __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));  // (the last round's repeats and the stores)
 }
 
+// Whether a gate_up launch with these arguments would run the streamed kernel (its shape choice in
+// launch_gemm_fp8 and the fit below) with a batch small enough to group locally.
+bool gemm_stream_local_ok(const GemmArgs &a);
+
 // Whether the launch fits the streamed kernel: whole units, K <= 3072, at least 3 units per chunk
 // (4 consecutive units then touch at most two chunks) and, from the host's upper bound on the
 // chunks (entries / 16 + active experts), at most kStrMaxSeg chunks per workgroup range.
@@ -447,6 +546,11 @@ static bool gemm_stream_fits(const GemmArgs &a, int rt, int n_wg) {
   const long long per = (gu * nc + n_wg - 1) / n_wg;
   const long long segs = per > 0 ? (per + gu - 2) / gu + 1 : 1;
   return segs <= kStrMaxSeg;
+}
+
+static int stream_cus();
+bool gemm_stream_local_ok(const GemmArgs &a) {
+  return a.n_entries <= (size_t)kLocalGroupMax && a.terms == kGemmTerms && gemm_stream_fits(a, 4, stream_cus());
 }
 
 static int stream_cus() {

@@ -28,38 +28,6 @@ namespace moe {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteTokens = 8;  // tokens per block for large batches: the router weights load once per block
 
-// Wavefront 0 of a block: from the per-expert entry counts cnt[0..E), the active experts in
-// ascending id (active_ids, active_off, *n_active; the entries of active expert i are
-// [active_off[i], active_off[i + 1])) and every expert's first entry base[e], by wave prefix
-// sums over 64 experts at a time.
-__device__ __forceinline__ void expert_list_wave(const int *cnt, int E, int lane, int *base, int32_t *active_ids,
-                                                 int32_t *active_off, int32_t *n_active) {
-  int off = 0, na = 0;
-  for (int e0 = 0; e0 < E; e0 += 64) {
-    const int e = e0 + lane;
-    const int c = e < E ? cnt[e] : 0;
-    int incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(incl, o);
-      if (lane >= o) incl += u;
-    }
-    const uint64_t act = __ballot(c > 0);
-    const int slot = na + __popcll(act & ((1ull << lane) - 1ull));
-    if (e < E) base[e] = off + incl - c;
-    if (c > 0) {
-      active_ids[slot] = e;
-      active_off[slot] = off + incl - c;
-    }
-    off += __shfl(incl, 63);
-    na += __popcll(act);
-  }
-  if (lane == 0) {
-    active_off[na] = off;
-    *n_active = na;
-  }
-}
-
 // Groups the T*k (token, slot) entries by expert, in one block of 1024 threads. Active
 // experts are listed in ascending id; entries of one expert are ordered by t*k + slot.
 // pos[t*k + slot] = entry index (or -1). LDS: s_count[E], s_base[E], s_wave[16][E].

@@ -120,7 +120,19 @@ struct GemmArgs {
   int n_tiles;               //                         row blocks x column tiles
   int n_blocks;              //                         workgroups of the tile order (>= n_tiles)
   int terms;                 // E2M3 terms per activation value: kGemmTerms, or 1 (quantized mode)
+  // Local grouping (the streamed gate_up GEMM of a batch of at most kLocalGroupMax entries): with
+  // group_idx set (the top-k indices [T][group_k] over group_E experts, -1 for a dropped slot)
+  // every workgroup groups the entries by expert itself, in place of the router's grouping, and
+  // workgroup 0 writes the expert lists, entry_src and pos (the w_ pointers) for the down GEMM
+  // and the combine.
+  const int32_t *group_idx;
+  int group_k, group_E;
+  int32_t *w_n_active, *w_active_ids, *w_active_off, *w_entry_src, *w_pos;
 };
+constexpr int kLocalGroupMax = 1024;
+// Whether the gate_up launch of these arguments (group_idx unset) runs the streamed kernel with
+// local grouping when asked to (gemm.hip: the same shape choice as launch_gemm_fp8).
+bool gemm_gate_up_groups_locally(const GemmArgs &a);
 hipError_t launch_gemm_fp8(GemvMode mode, const GemmArgs &a, hipStream_t s);
 // The streamed form for batches of a few entries per expert (gemm_stream.hip); hipErrorNotSupported
 // when the launch does not fit it.

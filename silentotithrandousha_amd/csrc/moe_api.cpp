@@ -132,6 +132,7 @@ struct moe_ctx {
   int gemm_band = 0;
   int gemm_shape_down = 0;  // block shape of the down GEMM (0: as gemm_shape)
   int act_quant = 0;  // grouped GEMM activations: 0 the exact kGemmTerms split, 1 one MXFP6 term
+  int local_group = 1;  // small batches on the streamed GEMM: its workgroups group the entries
   DevBuf route_ticket;  // k_route's block counter for the fused bucketing, zero between launches
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
@@ -524,20 +525,10 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
   ra.active_off = w.active_off;
   ra.entry_src = w.entry_src;
   ra.pos = w.pos;
-  const bool fuse_bucket = T > 1 && route_bucket_fits((int)c->H, (int)E);
-  ra.bucket_ticket = fuse_bucket ? (uint32_t *)c->route_ticket.p : nullptr;
-  ra.blk_count = w.blk_count;
-  ra.rank = w.rank;
-  RETURN_IF(timed(c, K_ROUTE, s, [&] { return launch_route(ra, s); }));
-  if (T > 1 && !fuse_bucket)
-    RETURN_IF(timed(c, K_BUCKET, s, [&] {
-      return launch_bucket(w.idx, (int)T, (int)k, (int)E, w.n_active, w.active_ids,
-                           w.active_off, w.entry_src, w.pos, s);
-    }));
   const int max_active = (int)std::min(E, T * k);
+  GemmArgs ga{}, gu{};
   if (use_gemm) {
     const size_t N = T * k;
-    GemmArgs ga{};
     ga.base = (const uint8_t *)Ly.experts.p;
     ga.stride = c->L.stride;
     ga.n_active = w.n_active;
@@ -549,13 +540,40 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
     ga.shape = c->gemm_shape;
     ga.band = c->gemm_band;  // default: gate_up in workgroup order, down in XCD bands of 1 row block
     ga.terms = c->act_quant ? 1 : kGemmTerms;
-    GemmArgs gu = ga;
+    gu = ga;
     gu.mat_off = c->L.gu_off;
     gu.bias_off = c->L.gub_off;
     gu.d = c->L.gu;
     gu.entry_src = w.entry_src;
     gu.brec = w.xrec;
     gu.out = w.hrec;
+  }
+  // small batches on the streamed gate_up GEMM: its workgroups group the entries by expert
+  // themselves (one round trip for the top-k indices, where the router's grouping took a
+  // grid-wide ticket and a pass of its last block, and the GEMM two dependent round trips for
+  // the lists and entry_src); its workgroup 0 writes the lists for the down GEMM and the combine
+  const bool local_group = use_gemm && c->local_group && gemm_gate_up_groups_locally(gu);
+  if (local_group) {
+    gu.group_idx = w.idx;
+    gu.group_k = (int)k;
+    gu.group_E = (int)E;
+    gu.w_n_active = w.n_active;
+    gu.w_active_ids = w.active_ids;
+    gu.w_active_off = w.active_off;
+    gu.w_entry_src = w.entry_src;
+    gu.w_pos = w.pos;
+  }
+  const bool fuse_bucket = T > 1 && !local_group && route_bucket_fits((int)c->H, (int)E);
+  ra.bucket_ticket = fuse_bucket ? (uint32_t *)c->route_ticket.p : nullptr;
+  ra.blk_count = w.blk_count;
+  ra.rank = w.rank;
+  RETURN_IF(timed(c, K_ROUTE, s, [&] { return launch_route(ra, s); }));
+  if (T > 1 && !fuse_bucket && !local_group)
+    RETURN_IF(timed(c, K_BUCKET, s, [&] {
+      return launch_bucket(w.idx, (int)T, (int)k, (int)E, w.n_active, w.active_ids,
+                           w.active_off, w.entry_src, w.pos, s);
+    }));
+  if (use_gemm) {
     RETURN_IF(timed(c, K_GATE_UP, s, [&] { return launch_gemm_fp8(GEMV_GATE_UP, gu, s); }));
     GemmArgs dn = ga;
     if (!c->gemm_band) dn.band = 1;
@@ -1201,6 +1219,10 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
         HIP_TRY(hipDeviceSynchronize());
       }
       c->act_quant = (int)value;
+      return MOE_OK;
+    case MOE_OPT_LOCAL_GROUP:
+      if (value < 0 || value > 1) return fail(MOE_ERR_INVALID, "MOE_OPT_LOCAL_GROUP is 0 or 1");
+      c->local_group = (int)value;
       return MOE_OK;
     case MOE_OPT_SPIN_LIMIT:
       if (value < 1 || value > 0xFFFFFFFFll) return fail(MOE_ERR_INVALID, "spin limit outside [1, 2^32)");

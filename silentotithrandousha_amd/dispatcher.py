@@ -185,6 +185,12 @@ class GpuMoeDispatcher:
         from ._ffi import MOE_OPT_ACT_QUANT
         check(lib().moe_set_option(self._ctx, MOE_OPT_ACT_QUANT, int(on)))
 
+    def set_local_group(self, on):
+        """Small batches on the streamed gate_up GEMM: its workgroups group the entries by expert
+        (1, default) or the router does (0); results identical."""
+        from ._ffi import MOE_OPT_LOCAL_GROUP
+        check(lib().moe_set_option(self._ctx, MOE_OPT_LOCAL_GROUP, int(on)))
+
     def set_spin_limit(self, polls):
         from ._ffi import MOE_OPT_SPIN_LIMIT
         check(lib().moe_set_option(self._ctx, MOE_OPT_SPIN_LIMIT, int(polls)))

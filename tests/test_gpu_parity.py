@@ -663,6 +663,11 @@ def test_batch_gemm_streamed_identical(orc, shape):
             d.set_gemm_shape(shape_c, down)
             o = d.layer_forward(0, x, k)
             assert np.array_equal(base, o), f"{shape}: shape {shape_c} down {down}"
+            # the router's grouping in place of the streamed GEMM's own (small batches)
+            d.set_local_group(0)
+            o = d.layer_forward(0, x, k)
+            d.set_local_group(1)
+            assert np.array_equal(base, o), f"{shape}: shape {shape_c} down {down}, router grouping"
         d.set_gemm_shape(0)
         want = orc.moe_layer(x, L, k)[0]
         assert_rel_l2(base, want, f"gemm {shape}")
@@ -938,7 +943,17 @@ def test_batch_gemm_adaptive_dropped_slots(orc):
     xs = syn.hidden(40, H, seed=421, sigma=1.0)
     want, _, idx, _ = orc.moe_layer(xs, L, 4, adaptive=ad)
     assert (idx < 0).any()
-    assert_rel_l2(d.layer_forward(0, xs, 4), want, "adaptive batch gemm")
+    got = d.layer_forward(0, xs, 4)
+    assert_rel_l2(got, want, "adaptive batch gemm")
+    # the streamed GEMM, whose workgroups group the entries themselves (dropped slots skipped),
+    # and with the router's grouping: the same bits
+    d.set_gemm_shape(12, 12)
+    o_local = d.layer_forward(0, xs, 4)
+    d.set_local_group(0)
+    o_router = d.layer_forward(0, xs, 4)
+    d.set_local_group(1)
+    d.set_gemm_shape(0)
+    assert np.array_equal(o_local, got) and np.array_equal(o_router, got)
     d.close()
 
 
