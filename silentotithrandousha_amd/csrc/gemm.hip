@@ -19,6 +19,7 @@
 
 #include "device.hpp"
 #include "kernels.hpp"
+#include "stream.hpp"
 
 namespace moe {
 
@@ -491,11 +492,13 @@ template <int MODE, typename S>
 constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP; }
 
 // M32: the 32x32x64 form of the 512 x 64 two-ahead shape (gemm32_*): the same DMA layout, ring and
-// waits; other MFMAs, operand reads and epilogue staging.
-template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false>
+// waits; other MFMAs, operand reads and epilogue staging. NSP > 0: the pipelined two-ahead step
+// for launches of exactly NSP K-steps.
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false, int NSP = 0>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(!M32 || (RT == 8 && CGW == 2 && S::kTwoAhead), "the 32x32 form: 128 rows x 32 entries per wavefront");
+  static_assert(NSP == 0 || (!M32 && S::kTwoAhead && NSP <= kGemmNs), "the pipelined form of the two-ahead step");
   using G = GemmRecT<NT>;  // the activation records (x or h) of the launch
   constexpr int W = S::W, CG = CGW, kChunks = G::kChunks, kEntryStep = G::kStep;
   // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
@@ -898,6 +901,80 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         if (s + 3 < ns) GEMM_STEP32(s + 3, s_r1, 3);
       }
 #undef GEMM_STEP32
+    } else if constexpr (NSP > 0) {
+      // ---- the pipelined form (ns == NSP, every step a constant): a wavefront holds two operand
+      //      sets. Step s reads its last column groups' B while its first groups' MFMAs run, then
+      //      waits for its reads and its DMAs of step s + 1 (the only ones in flight), and one
+      //      barrier makes slot s % 2 free (every wavefront has read all of step s) and slot
+      //      (s + 1) % 2 whole. The last groups' MFMAs then run while the slot receives step
+      //      s + 2's DMA and the wavefront reads step s + 1's A chunks and first groups' B from
+      //      the other slot into the other set: every LDS read overlaps MFMAs of the same
+      //      wavefront, where the plain step reads all its operands between two barriers before
+      //      its MFMAs. Same MFMAs in the same order per output, so the same bits.
+      constexpr int kNextA = RT, kNextB = kCSplit * (NT + 1);  // reads of the next step's set
+      // the sets: A chunks and scale words (GemmOps), and the first groups' B as read (selected at
+      // the start of their step, so that no read is waited for among the MFMAs that hide it)
+      GemmOps<RT, CGW, NT> opE_, opO_;
+      GemmBRaw<NT> rbE_[kCSplit], rbO_[kCSplit];
+#pragma unroll
+      for (int r_ = 0; r_ < RT; r_++)
+        sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[0] + (wr * RT + r_) * 256 + 4 * lane);
+      gemm_read_ops<RT, CGW, WR, WC, D, NT, 0>(opE_, s_r0, sw4_, wr, wc, lane, 0);
+#pragma unroll
+      for (int c_ = 0; c_ < kCSplit; c_++) gemm_read_b_raw(rbE_[c_], s_r0 + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
+      str_static_for<0, NSP>([&](auto stc) {
+        constexpr int st = decltype(stc)::value;
+        GemmOps<RT, CGW, NT> &oc = (st & 1) ? opO_ : opE_;
+        GemmOps<RT, CGW, NT> &on = (st & 1) ? opE_ : opO_;
+        GemmBRaw<NT>(&rc)[kCSplit] = (st & 1) ? rbO_ : rbE_;
+        GemmBRaw<NT>(&rn)[kCSplit] = (st & 1) ? rbE_ : rbO_;
+        uint8_t *cur = (st & 1) ? s_r1 : s_r0;
+        const uint8_t *oth = (st & 1) ? s_r0 : s_r1;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c_ = 0; c_ < kCSplit; c_++) gemm_select_b(oc.b[c_], rc[c_], g);
+        GemmBRaw<NT> raw_[CGW - kCSplit];
+#pragma unroll
+        for (int c_ = kCSplit; c_ < CGW; c_++)
+          gemm_read_b_raw(raw_[c_ - kCSplit], cur + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_mfma_ops<RT, CGW, NT, 0, kCSplit, 0>(acc, oc, [](int) {});
+#pragma unroll
+        for (int c_ = kCSplit; c_ < CGW; c_++) gemm_select_b(oc.b[c_], raw_[c_ - kCSplit], g);
+        __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+        GEMM_BARRIER();
+        // hook k: DMAs of step st + 2 first (k < kD), then the reads of step st + 1's set
+        constexpr int kD = st + 2 < NSP ? S::kDma + S::kDmaA + ((st & 3) == 2 ? S::kDmaA : 0) : 0;
+        constexpr int kR = st + 1 < NSP ? kNextA + kNextB : 0;
+        constexpr int sh = 8 * ((st + 1) & 3);
+        const uint8_t *nb = oth + (16 * CGW * wc + j) * kEntryStep, *na = oth + S::kBufB + wr * RT * 1024;
+        auto hook = [&](int k_) {
+          if (k_ < kD) {
+            dma2(k_, st + 2, cur);
+          } else if (k_ - kD < kNextA) {
+            const int r_ = k_ - kD;
+            if (((st + 1) & 3) == 0)  // the scale words of steps st + 1 .. st + 4 (DMA'd with step st + 1)
+              sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[((st + 1) >> 2) & 1] + (wr * RT + r_) * 256 + 4 * lane);
+            on.ar[r_] = *reinterpret_cast<const uint4 *>(na + r_ * 1024 + 16 * lane);
+            on.sw[r_] = sw4_[r_] >> sh;
+          } else {
+            const int i_ = k_ - kD - kNextA, c_ = i_ / (NT + 1), t_ = i_ % (NT + 1);
+            const uint8_t *eb = nb + 16 * c_ * kEntryStep;
+            if (t_ < NT) {
+              rn[c_].x[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + g) * 16);
+              rn[c_].y[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + 4 + (g >> 1)) * 16);
+            } else if constexpr (NT == 1) {
+              rn[c_].sc[0] = *reinterpret_cast<const uint32_t *>(eb + (G::kChunks - 1) * 16);
+            } else {
+              const uint4 sc = *reinterpret_cast<const uint4 *>(eb + (G::kChunks - 1) * 16);
+              const uint32_t w3[3] = {sc.x, sc.y, sc.z};
+#pragma unroll
+              for (int q_ = 0; q_ < NT; q_++) rn[c_].sc[q_] = w3[q_];
+            }
+          }
+        };
+        gemm_mfma_ops<RT, CGW, NT, kCSplit, CGW, kD + kR>(acc, oc, hook);
+      });
     } else {
     for (int s = 0; s < ns; s += 4) {
       GEMM_STEP2(s, s_r0, 0);
@@ -1169,7 +1246,7 @@ static int device_cus() {
   return c;
 }
 
-template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false>
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false, int NSP = 0>
 static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
@@ -1183,7 +1260,8 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   a.n_blocks = (int)blocks;
   // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
   const size_t grid = gemm_persistent<MODE, S>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
+  if (NSP && a.d.ns != (uint32_t)NSP) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32, NSP>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1238,9 +1316,23 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
     if (e != hipErrorNotSupported) return e;
   }
   if (a.shape == 10) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, true>(a, s);
+  // the 512 x 64 block with the pipelined step (K-steps 23 or 24; otherwise the plain step)
+  if (a.shape == 15) {
+    if (a.d.ns == 23) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23>(a, s);
+    if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24>(a, s);
+    return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
+  }
   if (a.shape == 11) return launch_gemm_shape<MODE, 16, 2, 2, 4, 2, NT>(a, s);
-  if (mean >= 48)
-    return a.shape == 1 ? launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s) : launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
+  if (mean >= 48) {
+    if (a.shape == 1) return launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s);
+    // the down GEMM on the pipelined step (measured at prefill, 20B x 4096 tokens: 292 -> 278 us;
+    // gate_up unchanged at 526 us, so it keeps the plain step)
+    if constexpr (MODE == GEMV_DOWN) {
+      if (a.d.ns == 23) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23>(a, s);
+      if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24>(a, s);
+    }
+    return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
+  }
   if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
   return launch_gemm_shape<MODE, 4, 1, 2, 1, 3, NT>(a, s);
 }
