@@ -82,9 +82,9 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * (bf16 hi+lo activations). Results agree to the matmul tolerance; routing is identical.
  * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM: 0 (default) by the mean entries per
  * expert (14 to 44, 60 to 72, and for the down GEMM 14 to 72: the wide streamed form of code 14;
- * otherwise 48+: 512 rows x 64 entries in 8 wavefronts, for the down GEMM at K of 2817-3072 with the
- * pipelined step of code 15; 24+: 128 x 32 in 2; else the streamed form of code 12, or 128 x 16 in
- * 2 where neither fits);
+ * otherwise 48+: 512 rows x 64 entries in 8 wavefronts, at K of 2817-3072 with the pipelined step
+ * of code 15; 24+: 128 x 32 in 2; else the streamed form of code 12, or 128 x 16 in 2 where neither
+ * fits);
  * for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2; 2 and 3
  * force 256-row x 32- and 16-entry blocks of 4 wavefronts, 4 the 128-row x 16-entry block of 4
  * wavefronts (down only; gate_up takes 3), 5 the 128 x 16 block of 2 wavefronts, 6 a 64 x 16

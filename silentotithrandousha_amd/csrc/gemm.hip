@@ -487,9 +487,11 @@ __device__ __forceinline__ void gemm_step_bstat(f32x4 (&acc)[RT][CGW], const uin
   }
 }
 
-// The shapes that run a persistent grid.
-template <int MODE, typename S>
-constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP; }
+// The shapes that run a persistent grid: the plain two-ahead step for gate_up (the pipelined step
+// measured faster on one workgroup per tile: its workgroups then turn over without a loop-top
+// barrier, and the hardware dispatches the next tile's workgroup as soon as one ends).
+template <int MODE, typename S, int NSP>
+constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP && NSP == 0; }
 
 // M32: the 32x32x64 form of the 512 x 64 two-ahead shape (gemm32_*): the same DMA layout, ring and
 // waits; other MFMAs, operand reads and epilogue staging. NSP > 0: the pipelined two-ahead step
@@ -527,7 +529,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   // Workgroup p of the launch's a.n_blocks: the two-ahead gate_up shape runs a persistent grid
   // (one workgroup per CU, each taking p = blockIdx.x, + gridDim.x, ...: the same XCD for every
   // p, p % 8); the others one workgroup per p (for the down shape the loop cost 8 %, measured).
-  constexpr bool kPersist = gemm_persistent<MODE, S>();
+  constexpr bool kPersist = gemm_persistent<MODE, S, NSP>();
   for (int p = (int)blockIdx.x; p < a.n_blocks; p += (int)gridDim.x) {
   if (p != (int)blockIdx.x) __syncthreads();  // the previous tile's LDS reads are done
   int cl, rblk_l;
@@ -1259,7 +1261,7 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   const size_t blocks = a.band ? (tiles + 7) / 8 * 8 : tiles;
   a.n_blocks = (int)blocks;
   // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
-  const size_t grid = gemm_persistent<MODE, S>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
+  const size_t grid = gemm_persistent<MODE, S, NSP>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
   if (NSP && a.d.ns != (uint32_t)NSP) return hipErrorInvalidValue;
   hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32, NSP>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
@@ -1325,12 +1327,11 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
   if (a.shape == 11) return launch_gemm_shape<MODE, 16, 2, 2, 4, 2, NT>(a, s);
   if (mean >= 48) {
     if (a.shape == 1) return launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s);
-    // the down GEMM on the pipelined step (measured at prefill, 20B x 4096 tokens: 292 -> 278 us;
-    // gate_up unchanged at 526 us, so it keeps the plain step)
-    if constexpr (MODE == GEMV_DOWN) {
-      if (a.d.ns == 23) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23>(a, s);
-      if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24>(a, s);
-    }
+    // the pipelined step (measured at prefill, 20B x 4096 tokens, paired runs: down 292 -> 278 us;
+    // gate_up 517.5 -> 493 us on one workgroup per tile, where on the persistent grid it had
+    // stayed at 526 us); other K: the plain step (gate_up on the persistent grid)
+    if (a.d.ns == 23) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23>(a, s);
+    if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24>(a, s);
     return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
   }
   if (mean >= 24) return launch_gemm_shape<MODE, 4, 2, 2, 1, 3, NT>(a, s);
