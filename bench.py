@@ -347,7 +347,9 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
         tf = os.path.join(ROOT, "profiles", "traffic.json")
         if os.path.exists(tf):
             recs = json.load(open(tf))
-            rec = recs.get(f"{kname}@{workload}") or recs.get(kname)
+            # (the quantized mode runs other kernels: its records are keyed apart)
+            key = f"{kname}@{workload}" + ("+act_quant" if act_quant else "")
+            rec = recs.get(key) or (None if act_quant else recs.get(kname))
             if rec and rec.get("workload") == workload:
                 res["roofline"]["traffic"] = rec["bytes_per_launch"]
                 res["roofline"]["traffic_source"] = rec["source"]
