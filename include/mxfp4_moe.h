@@ -83,8 +83,8 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * MOE_OPT_GEMM_SHAPE: block shape of the grouped GEMM: 0 (default) by the mean entries per
  * expert (14 to 44, 60 to 72, and for the down GEMM 14 to 72: the wide streamed form of code 14;
  * otherwise 48+: 512 rows x 64 entries in 8 wavefronts, at K of 2817-3072 with the pipelined step
- * of code 15; 24+: 128 x 32 in 2; else the streamed form of code 12, or 128 x 16 in 2 where neither
- * fits);
+ * of code 15 (the down GEMM: of code 17); 24+: 128 x 32 in 2; else the streamed form of code 12, or
+ * 128 x 16 in 2 where neither fits);
  * for experts averaging 48+ entries 1 selects 8 wavefronts as 8 x 1 instead of 4 x 2; 2 and 3
  * force 256-row x 32- and 16-entry blocks of 4 wavefronts, 4 the 128-row x 16-entry block of 4
  * wavefronts (down only; gate_up takes 3), 5 the 128 x 16 block of 2 wavefronts, 6 a 64 x 16
@@ -102,8 +102,10 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * 64 (gate_up) or 32 (down) rows x a group of up to 5 16-entry chunks of one expert, so every
  * weight tile streams once per group; launches it does not fit take the default), 15 the 512 x 64
  * block with the pipelined step (each wavefront reads the next K-step's operands while its MFMAs
- * run; one barrier per step; K of 2817 to 3072 values, other K the plain step) (tuning; codes
- * 0-9 and 11-15 give identical results, code 10 the same to f32 rounding: its MFMA sums 64
+ * run; one barrier per step; K of 2817 to 3072 values, other K the plain step), 16 and 17 the same
+ * with separate rings for the weights and the activation records (16: records three steps deep,
+ * 17: weights three deep; the default for the down GEMM where code 15's K applies) (tuning; codes
+ * 0-9 and 11-17 give identical results, code 10 the same to f32 rounding: its MFMA sums 64
  * products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
  * (0, default: as MOE_OPT_GEMM_SHAPE).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both

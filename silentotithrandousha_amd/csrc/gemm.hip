@@ -496,17 +496,22 @@ constexpr bool gemm_persistent() { return S::kTwoAhead && MODE == GEMV_GATE_UP &
 // M32: the 32x32x64 form of the 512 x 64 two-ahead shape (gemm32_*): the same DMA layout, ring and
 // waits; other MFMAs, operand reads and epilogue staging. NSP > 0: the pipelined two-ahead step
 // for launches of exactly NSP K-steps.
-template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false, int NSP = 0>
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false, int NSP = 0, int RING = 0>
 __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR * WC / 4, WR * WC / 4))) void k_gemm_fp8(GemmArgs a) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(!M32 || (RT == 8 && CGW == 2 && S::kTwoAhead), "the 32x32 form: 128 rows x 32 entries per wavefront");
   static_assert(NSP == 0 || (!M32 && S::kTwoAhead && NSP <= kGemmNs), "the pipelined form of the two-ahead step");
+  static_assert(RING == 0 || (NSP > 0 && S::kScale4), "separate A and B rings: the pipelined step");
+  // RING 1: A in 2 slots, B in 3; RING 2: A in 3, B in 2 (one LDS area, A slots first)
+  constexpr int kRingA = RING == 1 ? 2 : 3, kRingB = RING == 1 ? 3 : 2;
+  constexpr int kRingBytes = RING ? kRingA * S::kBufA + kRingB * S::kGroups * 1024 : 16;
   using G = GemmRecT<NT>;  // the activation records (x or h) of the launch
   constexpr int W = S::W, CG = CGW, kChunks = G::kChunks, kEntryStep = G::kStep;
   // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
   // alias the reads of another, so those reads do not wait for it
-  __shared__ __attribute__((aligned(1024))) uint8_t s_r0[S::kSlot];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_r1[S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r0[RING ? 16 : S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r1[RING ? 16 : S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_ring[kRingBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t s_sc[2][S::kScale4 ? S::kTilesA * 256 : 16];
   constexpr int kBiasTiles = RT < 4 ? 4 : RT;  // the bias DMA moves 64 rows (4 tiles) per wavefront load
@@ -862,6 +867,146 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     // the A-scale words of the current 4 steps, read from LDS once per 4 steps (their DMA is
     // complete from the step before the first of them until the DMA of the quad after next)
     uint32_t sw4_[RT];
+    if constexpr (RING > 0) {
+      // ---- the pipelined step (below) with separate rings for A and B, one of them three slots
+      //      deep so that its DMA has two steps to land. DMAs issued after step s's barrier:
+      //      RING 1: A(s + 2) (and, for s + 2 = 4q, quad q's scale words), then B(s + 3); RING 2:
+      //      B(s + 2), then A(s + 3). The wait before step s's barrier completes A(s + 1) and
+      //      B(s + 1) and leaves the deeper ring's step s + 2 in flight. B's last piece (only the
+      //      wavefronts inside kGroups load one) is the one DMA issued under a branch: RING 2 issues
+      //      it first (before the MFMAs), RING 1 after them.
+      constexpr int DA = kRingA, DB = kRingB, kBufBr = S::kGroups * 1024;
+      auto slA = [&](int st) { return s_ring + (st % DA) * S::kBufA; };
+      auto slB = [&](int st) { return s_ring + DA * S::kBufA + (st % DB) * kBufBr; };
+      auto dmaB_last = [&](int ld) {
+        if (fullb) lds_dma16_s(boff[S::kDma - 1], a.brec + (size_t)ld * G::kStep, slB(ld) + 1024 * (W * (S::kDma - 1) + wvu));
+      };
+      auto dmaB = [&](int k, int ld) {  // k < kDma - 1: the unconditional pieces
+        lds_dma16_s(boff[k], a.brec + (size_t)ld * G::kStep, slB(ld) + 1024 * (W * k + wvu));
+      };
+      auto dmaA = [&](int k, int ld) {  // k < kDmaA: A tiles; then the scale words (ld % 4 == 0)
+        if (k < S::kDmaA) {
+          lds_dma16_s(min((uint32_t)ld * 1024u + 16u * lane, a_last), asrc[k], slA(ld) + (W * k + wvu) * 1024);
+        } else {
+          const int i = k - S::kDmaA;
+          lds_dma4_s((uint32_t)(ld >> 2) * 256u + 4u * lane, ssrc[i], s_sc[(ld >> 2) & 1] + (W * i + wvu) * 256);
+        }
+      };
+      auto nA = [&](int ld) { return ld < NSP ? S::kDmaA + ((ld & 3) == 0 ? S::kDmaA : 0) : 0; };
+      auto issueA = [&](int ld) {
+        for (int k = 0; k < nA(ld); k++) dmaA(k, ld);
+      };
+      auto issueB = [&](int ld) {
+        if (ld >= NSP) return;
+        for (int k = 0; k < S::kDma - 1; k++) dmaB(k, ld);
+        dmaB_last(ld);
+      };
+      // prologue: step 0 whole, steps 1 (and 2 of the deeper ring) in flight, in the order of
+      // the loop's groups, so that the first wait counts the same way as every later one
+      issueA(0);
+      issueB(0);
+      if constexpr (RING == 1) {
+        issueA(1);
+        issueB(1);
+        issueB(2);
+        if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(nA(1) + 2 * S::kDma));
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(nA(1) + 2 * (S::kDma - 1)));
+      } else {
+        issueB(1);
+        issueA(1);
+        issueA(2);
+        if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + nA(1) + nA(2)));
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + nA(1) + nA(2)));
+      }
+      GEMM_BARRIER();
+      constexpr int kNextA = RT, kNextB = kCSplit * (NT + 1);
+      GemmOps<RT, CGW, NT> opE_, opO_;
+      GemmBRaw<NT> rbE_[kCSplit], rbO_[kCSplit];
+#pragma unroll
+      for (int r_ = 0; r_ < RT; r_++) {
+        sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[0] + (wr * RT + r_) * 256 + 4 * lane);
+        opE_.ar[r_] = *reinterpret_cast<const uint4 *>(slA(0) + (wr * RT + r_) * 1024 + 16 * lane);
+        opE_.sw[r_] = sw4_[r_];
+      }
+#pragma unroll
+      for (int c_ = 0; c_ < kCSplit; c_++) gemm_read_b_raw(rbE_[c_], slB(0) + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
+      str_static_for<0, NSP>([&](auto stc) {
+        constexpr int st = decltype(stc)::value;
+        GemmOps<RT, CGW, NT> &oc = (st & 1) ? opO_ : opE_;
+        GemmOps<RT, CGW, NT> &on = (st & 1) ? opE_ : opO_;
+        GemmBRaw<NT>(&rc)[kCSplit] = (st & 1) ? rbO_ : rbE_;
+        GemmBRaw<NT>(&rn)[kCSplit] = (st & 1) ? rbE_ : rbO_;
+        const uint8_t *bc = slB(st);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c_ = 0; c_ < kCSplit; c_++) gemm_select_b(oc.b[c_], rc[c_], g);
+        GemmBRaw<NT> raw_[CGW - kCSplit];
+#pragma unroll
+        for (int c_ = kCSplit; c_ < CGW; c_++)
+          gemm_read_b_raw(raw_[c_ - kCSplit], bc + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_mfma_ops<RT, CGW, NT, 0, kCSplit, 0>(acc, oc, [](int) {});
+#pragma unroll
+        for (int c_ = kCSplit; c_ < CGW; c_++) gemm_select_b(oc.b[c_], raw_[c_ - kCSplit], g);
+        // A(st + 1) and B(st + 1) complete; the deeper ring's step st + 2 may stay in flight
+        if constexpr (RING == 1) {
+          if constexpr (st + 2 < NSP) {
+            if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma));
+            else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1));
+          } else {
+            __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+          }
+        } else {
+          constexpr int kOut = st + 2 < NSP ? S::kDmaA + (((st + 2) & 3) == 0 ? S::kDmaA : 0) : 0;
+          __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(kOut));
+        }
+        GEMM_BARRIER();
+        // hooks: this step's DMA group (RING 1: A(st + 2), B(st + 3)'s unconditional pieces;
+        // RING 2: B(st + 2), A(st + 3)), then the reads of step st + 1's set
+        constexpr int ldA = RING == 1 ? st + 2 : st + 3, ldB = RING == 1 ? st + 3 : st + 2;
+        constexpr int kNA = ldA < NSP ? S::kDmaA + ((ldA & 3) == 0 ? S::kDmaA : 0) : 0;
+        constexpr int kNB = ldB < NSP ? (RING == 1 ? S::kDma - 1 : S::kDma) : 0;
+        constexpr int kD = kNA + kNB;
+        constexpr int kR = st + 1 < NSP ? kNextA + kNextB : 0;
+        constexpr int sh = 8 * ((st + 1) & 3);
+        const uint8_t *nb = slB(st + 1) + (16 * CGW * wc + j) * kEntryStep;
+        const uint8_t *na = slA(st + 1) + wr * RT * 1024;
+        auto hook = [&](int k_) {
+          if (k_ < kD) {
+            if constexpr (RING == 1) {
+              if (k_ < kNA) dmaA(k_, ldA);
+              else dmaB(k_ - kNA, ldB);
+            } else {
+              if (k_ == 0) dmaB_last(ldB);  // (the branch: before the MFMAs)
+              else if (k_ < kNB) dmaB(k_ - 1, ldB);
+              else dmaA(k_ - kNB, ldA);
+            }
+          } else if (k_ - kD < kNextA) {
+            const int r_ = k_ - kD;
+            if (((st + 1) & 3) == 0)
+              sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[((st + 1) >> 2) & 1] + (wr * RT + r_) * 256 + 4 * lane);
+            on.ar[r_] = *reinterpret_cast<const uint4 *>(na + r_ * 1024 + 16 * lane);
+            on.sw[r_] = sw4_[r_] >> sh;
+          } else {
+            const int i_ = k_ - kD - kNextA, c_ = i_ / (NT + 1), t_ = i_ % (NT + 1);
+            const uint8_t *eb = nb + 16 * c_ * kEntryStep;
+            if (t_ < NT) {
+              rn[c_].x[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + g) * 16);
+              rn[c_].y[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + 4 + (g >> 1)) * 16);
+            } else if constexpr (NT == 1) {
+              rn[c_].sc[0] = *reinterpret_cast<const uint32_t *>(eb + (G::kChunks - 1) * 16);
+            } else {
+              const uint4 sc = *reinterpret_cast<const uint4 *>(eb + (G::kChunks - 1) * 16);
+              const uint32_t w3[3] = {sc.x, sc.y, sc.z};
+#pragma unroll
+              for (int q_ = 0; q_ < NT; q_++) rn[c_].sc[q_] = w3[q_];
+            }
+          }
+        };
+        gemm_mfma_ops<RT, CGW, NT, kCSplit, CGW, kD + kR>(acc, oc, hook);
+        if constexpr (RING == 1 && ldB < NSP) dmaB_last(ldB);
+      });
+    } else {
     constexpr int kAll = S::kDma + 2 * S::kDmaA;  // the DMAs of a step whose scale words load
 #pragma unroll
     for (int k = 0; k < kAll; k++) dma2(k, 0, s_r0);
@@ -985,6 +1130,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       if (s + 3 < ns) GEMM_STEP2(s + 3, s_r1, 3);
     }
     }
+    }  // RING == 0
 #undef GEMM_STEP2
 #undef GEMM_BARRIER
 #undef GEMM_VM_WAIT
@@ -1055,7 +1201,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     constexpr int kStageW = NHB * kWaveCols * kRow * 4;  // staging bytes per wavefront
     constexpr int kHalf = W > 1 ? W / 2 : 1;           // wavefronts per ring slot
     if constexpr (kHalf * kStageW <= S::kSlot && NHB * kWaveCols <= 64) {  // one lane pass
-      float *st32 = reinterpret_cast<float *>((wv < kHalf ? s_r0 : s_r1) + (wv % kHalf) * kStageW);
+      float *st32 = RING ? reinterpret_cast<float *>(s_ring + wv * kStageW)
+                         : reinterpret_cast<float *>((wv < kHalf ? s_r0 : s_r1) + (wv % kHalf) * kStageW);
+      static_assert(!RING || W * kStageW <= kRingBytes, "staging fits the separate rings");
 #pragma unroll
       for (int hbk = 0; hbk < NHB; hbk++) {
         if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
@@ -1248,7 +1396,7 @@ static int device_cus() {
   return c;
 }
 
-template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false, int NSP = 0>
+template <int MODE, int RT, int CGW, int WR, int WC, int D, int NT, bool M32 = false, int NSP = 0, int RING = 0>
 static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(S::kLds <= 160 * 1024 - 64, "LDS");
@@ -1263,7 +1411,7 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   // persistent shapes: one workgroup per CU (a multiple of 8, so p % 8 stays the XCD of p)
   const size_t grid = gemm_persistent<MODE, S, NSP>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
   if (NSP && a.d.ns != (uint32_t)NSP) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32, NSP>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
+  hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32, NSP, RING>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1324,12 +1472,27 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
     if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24>(a, s);
     return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
   }
+  if (a.shape == 16 || a.shape == 17) {  // the pipelined step with separate A and B rings
+    if (a.d.ns == 23)
+      return a.shape == 16 ? launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23, 1>(a, s)
+                           : launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23, 2>(a, s);
+    if (a.d.ns == 24)
+      return a.shape == 16 ? launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24, 1>(a, s)
+                           : launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24, 2>(a, s);
+    return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
+  }
   if (a.shape == 11) return launch_gemm_shape<MODE, 16, 2, 2, 4, 2, NT>(a, s);
   if (mean >= 48) {
     if (a.shape == 1) return launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s);
     // the pipelined step (measured at prefill, 20B x 4096 tokens, paired runs: down 292 -> 278 us;
     // gate_up 517.5 -> 493 us on one workgroup per tile, where on the persistent grid it had
-    // stayed at 526 us); other K: the plain step (gate_up on the persistent grid)
+    // stayed at 526 us); the down GEMM with its weights in a ring of 3 (278 -> 264 us; gate_up
+    // unchanged with either ring three deep, so it keeps the shared ring); other K: the plain
+    // step (gate_up on the persistent grid)
+    if constexpr (MODE == GEMV_DOWN) {
+      if (a.d.ns == 23) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23, 2>(a, s);
+      if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24, 2>(a, s);
+    }
     if (a.d.ns == 23) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 23>(a, s);
     if (a.d.ns == 24) return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT, false, 24>(a, s);
     return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);

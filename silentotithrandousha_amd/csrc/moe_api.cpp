@@ -1190,7 +1190,7 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
       c->batch_gemm = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_SHAPE:
-      if (value < 0 || value > 15) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..15");
+      if (value < 0 || value > 17) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..17");
       c->gemm_shape = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_BAND:
@@ -1198,7 +1198,7 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
       c->gemm_band = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_SHAPE_DOWN:
-      if (value < 0 || value > 15) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE_DOWN is 0..15");
+      if (value < 0 || value > 17) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE_DOWN is 0..17");
       c->gemm_shape_down = (int)value;
       return MOE_OK;
     case MOE_OPT_MATVEC:
