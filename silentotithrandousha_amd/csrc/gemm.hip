@@ -501,16 +501,17 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   using S = GemmShape<RT, CGW, WR, WC, D, NT>;
   static_assert(!M32 || (RT == 8 && CGW == 2 && S::kTwoAhead), "the 32x32 form: 128 rows x 32 entries per wavefront");
   static_assert(NSP == 0 || (!M32 && S::kTwoAhead && NSP <= kGemmNs), "the pipelined form of the two-ahead step");
-  static_assert(RING == 0 || (NSP > 0 && S::kScale4), "separate A and B rings: the pipelined step");
-  // RING 1: A in 2 slots, B in 3; RING 2: A in 3, B in 2 (one LDS area, A slots first)
-  constexpr int kRingA = RING == 1 ? 2 : 3, kRingB = RING == 1 ? 3 : 2;
-  constexpr int kRingBytes = RING ? kRingA * S::kBufA + kRingB * S::kGroups * 1024 : 16;
+  static_assert(RING == 0 || NSP > 0, "separate ring depths: the pipelined step");
+  // the pipelined step's rings, in one LDS area (A slots first): RING 0 both 2 slots deep; RING 1
+  // A 2 and B 3; RING 2 A 3 and B 2
+  constexpr int kRingA = RING == 2 ? 3 : 2, kRingB = RING == 1 ? 3 : 2;
+  constexpr int kRingBytes = NSP ? kRingA * S::kBufA + kRingB * S::kGroups * 1024 : 16;
   using G = GemmRecT<NT>;  // the activation records (x or h) of the launch
   constexpr int W = S::W, CG = CGW, kChunks = G::kChunks, kEntryStep = G::kStep;
   // the ring slots as separate LDS objects: the LDS-DMA into one slot is then known not to
   // alias the reads of another, so those reads do not wait for it
-  __shared__ __attribute__((aligned(1024))) uint8_t s_r0[RING ? 16 : S::kSlot];
-  __shared__ __attribute__((aligned(1024))) uint8_t s_r1[RING ? 16 : S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r0[NSP ? 16 : S::kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_r1[NSP ? 16 : S::kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t s_ring[kRingBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t s_r2[D == 3 ? S::kSlot : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t s_sc[2][S::kScale4 ? S::kTilesA * 256 : 16];
@@ -867,14 +868,23 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     // the A-scale words of the current 4 steps, read from LDS once per 4 steps (their DMA is
     // complete from the step before the first of them until the DMA of the quad after next)
     uint32_t sw4_[RT];
-    if constexpr (RING > 0) {
-      // ---- the pipelined step (below) with separate rings for A and B, one of them three slots
-      //      deep so that its DMA has two steps to land. DMAs issued after step s's barrier:
-      //      RING 1: A(s + 2) (and, for s + 2 = 4q, quad q's scale words), then B(s + 3); RING 2:
-      //      B(s + 2), then A(s + 3). The wait before step s's barrier completes A(s + 1) and
-      //      B(s + 1) and leaves the deeper ring's step s + 2 in flight. B's last piece (only the
-      //      wavefronts inside kGroups load one) is the one DMA issued under a branch: RING 2 issues
-      //      it first (before the MFMAs), RING 1 after them.
+    if constexpr (NSP > 0) {
+      // ---- the pipelined step (ns == NSP, every step a constant): a wavefront holds two operand
+      //      sets. Step s reads its last column groups' B while its first groups' MFMAs run, then
+      //      waits for its reads and for its DMAs of step s + 1, and one barrier makes step s's
+      //      ring slots free (every wavefront has read all of step s) and step s + 1's whole. The
+      //      last groups' MFMAs then run while the freed slots receive DMAs and the wavefront reads
+      //      step s + 1's A chunks and first groups' B into the other set: every LDS read overlaps
+      //      MFMAs of the same wavefront, where the plain step reads all its operands between two
+      //      barriers before its MFMAs. Same MFMAs in the same order per output, so the same bits.
+      //      The A chunks and the B records have rings of their own: both two slots deep (RING 0;
+      //      the slots of step s receive step s + 2), or one of them three deep, so that its DMA
+      //      has two steps to land. DMAs issued after step s's barrier: RING 0: B(s + 2), A(s + 2);
+      //      RING 1: A(s + 2), then B(s + 3); RING 2: B(s + 2), then A(s + 3); the A-scale words of
+      //      quad q go with A(4q). The wait before step s's barrier completes A(s + 1) and B(s + 1)
+      //      and leaves the deeper ring's step s + 2 in flight. B's last piece (only the wavefronts
+      //      inside kGroups load one) is the one DMA issued under a branch: RINGs 0 and 2 issue it
+      //      first (before the MFMAs), RING 1 after them.
       constexpr int DA = kRingA, DB = kRingB, kBufBr = S::kGroups * 1024;
       auto slA = [&](int st) { return s_ring + (st % DA) * S::kBufA; };
       auto slB = [&](int st) { return s_ring + DA * S::kBufA + (st % DB) * kBufBr; };
@@ -911,12 +921,17 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         issueB(2);
         if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(nA(1) + 2 * S::kDma));
         else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(nA(1) + 2 * (S::kDma - 1)));
-      } else {
+      } else if constexpr (RING == 2) {
         issueB(1);
         issueA(1);
         issueA(2);
         if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + nA(1) + nA(2)));
         else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + nA(1) + nA(2)));
+      } else {
+        issueB(1);
+        issueA(1);
+        if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + nA(1)));
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + nA(1)));
       }
       GEMM_BARRIER();
       constexpr int kNextA = RT, kNextB = kCSplit * (NT + 1);
@@ -956,14 +971,16 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
           } else {
             __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
           }
-        } else {
+        } else if constexpr (RING == 2) {
           constexpr int kOut = st + 2 < NSP ? S::kDmaA + (((st + 2) & 3) == 0 ? S::kDmaA : 0) : 0;
           __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(kOut));
+        } else {
+          __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
         }
         GEMM_BARRIER();
         // hooks: this step's DMA group (RING 1: A(st + 2), B(st + 3)'s unconditional pieces;
-        // RING 2: B(st + 2), A(st + 3)), then the reads of step st + 1's set
-        constexpr int ldA = RING == 1 ? st + 2 : st + 3, ldB = RING == 1 ? st + 3 : st + 2;
+        // RINGs 0 and 2: B, then A, into the slots just freed), then the reads of step st + 1's set
+        constexpr int ldA = st + DA, ldB = st + DB;
         constexpr int kNA = ldA < NSP ? S::kDmaA + ((ldA & 3) == 0 ? S::kDmaA : 0) : 0;
         constexpr int kNB = ldB < NSP ? (RING == 1 ? S::kDma - 1 : S::kDma) : 0;
         constexpr int kD = kNA + kNB;
@@ -1048,80 +1065,6 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
         if (s + 3 < ns) GEMM_STEP32(s + 3, s_r1, 3);
       }
 #undef GEMM_STEP32
-    } else if constexpr (NSP > 0) {
-      // ---- the pipelined form (ns == NSP, every step a constant): a wavefront holds two operand
-      //      sets. Step s reads its last column groups' B while its first groups' MFMAs run, then
-      //      waits for its reads and its DMAs of step s + 1 (the only ones in flight), and one
-      //      barrier makes slot s % 2 free (every wavefront has read all of step s) and slot
-      //      (s + 1) % 2 whole. The last groups' MFMAs then run while the slot receives step
-      //      s + 2's DMA and the wavefront reads step s + 1's A chunks and first groups' B from
-      //      the other slot into the other set: every LDS read overlaps MFMAs of the same
-      //      wavefront, where the plain step reads all its operands between two barriers before
-      //      its MFMAs. Same MFMAs in the same order per output, so the same bits.
-      constexpr int kNextA = RT, kNextB = kCSplit * (NT + 1);  // reads of the next step's set
-      // the sets: A chunks and scale words (GemmOps), and the first groups' B as read (selected at
-      // the start of their step, so that no read is waited for among the MFMAs that hide it)
-      GemmOps<RT, CGW, NT> opE_, opO_;
-      GemmBRaw<NT> rbE_[kCSplit], rbO_[kCSplit];
-#pragma unroll
-      for (int r_ = 0; r_ < RT; r_++)
-        sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[0] + (wr * RT + r_) * 256 + 4 * lane);
-      gemm_read_ops<RT, CGW, WR, WC, D, NT, 0>(opE_, s_r0, sw4_, wr, wc, lane, 0);
-#pragma unroll
-      for (int c_ = 0; c_ < kCSplit; c_++) gemm_read_b_raw(rbE_[c_], s_r0 + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
-      str_static_for<0, NSP>([&](auto stc) {
-        constexpr int st = decltype(stc)::value;
-        GemmOps<RT, CGW, NT> &oc = (st & 1) ? opO_ : opE_;
-        GemmOps<RT, CGW, NT> &on = (st & 1) ? opE_ : opO_;
-        GemmBRaw<NT>(&rc)[kCSplit] = (st & 1) ? rbO_ : rbE_;
-        GemmBRaw<NT>(&rn)[kCSplit] = (st & 1) ? rbE_ : rbO_;
-        uint8_t *cur = (st & 1) ? s_r1 : s_r0;
-        const uint8_t *oth = (st & 1) ? s_r0 : s_r1;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int c_ = 0; c_ < kCSplit; c_++) gemm_select_b(oc.b[c_], rc[c_], g);
-        GemmBRaw<NT> raw_[CGW - kCSplit];
-#pragma unroll
-        for (int c_ = kCSplit; c_ < CGW; c_++)
-          gemm_read_b_raw(raw_[c_ - kCSplit], cur + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
-        __builtin_amdgcn_sched_barrier(0);
-        gemm_mfma_ops<RT, CGW, NT, 0, kCSplit, 0>(acc, oc, [](int) {});
-#pragma unroll
-        for (int c_ = kCSplit; c_ < CGW; c_++) gemm_select_b(oc.b[c_], raw_[c_ - kCSplit], g);
-        __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
-        GEMM_BARRIER();
-        // hook k: DMAs of step st + 2 first (k < kD), then the reads of step st + 1's set
-        constexpr int kD = st + 2 < NSP ? S::kDma + S::kDmaA + ((st & 3) == 2 ? S::kDmaA : 0) : 0;
-        constexpr int kR = st + 1 < NSP ? kNextA + kNextB : 0;
-        constexpr int sh = 8 * ((st + 1) & 3);
-        const uint8_t *nb = oth + (16 * CGW * wc + j) * kEntryStep, *na = oth + S::kBufB + wr * RT * 1024;
-        auto hook = [&](int k_) {
-          if (k_ < kD) {
-            dma2(k_, st + 2, cur);
-          } else if (k_ - kD < kNextA) {
-            const int r_ = k_ - kD;
-            if (((st + 1) & 3) == 0)  // the scale words of steps st + 1 .. st + 4 (DMA'd with step st + 1)
-              sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[((st + 1) >> 2) & 1] + (wr * RT + r_) * 256 + 4 * lane);
-            on.ar[r_] = *reinterpret_cast<const uint4 *>(na + r_ * 1024 + 16 * lane);
-            on.sw[r_] = sw4_[r_] >> sh;
-          } else {
-            const int i_ = k_ - kD - kNextA, c_ = i_ / (NT + 1), t_ = i_ % (NT + 1);
-            const uint8_t *eb = nb + 16 * c_ * kEntryStep;
-            if (t_ < NT) {
-              rn[c_].x[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + g) * 16);
-              rn[c_].y[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + 4 + (g >> 1)) * 16);
-            } else if constexpr (NT == 1) {
-              rn[c_].sc[0] = *reinterpret_cast<const uint32_t *>(eb + (G::kChunks - 1) * 16);
-            } else {
-              const uint4 sc = *reinterpret_cast<const uint4 *>(eb + (G::kChunks - 1) * 16);
-              const uint32_t w3[3] = {sc.x, sc.y, sc.z};
-#pragma unroll
-              for (int q_ = 0; q_ < NT; q_++) rn[c_].sc[q_] = w3[q_];
-            }
-          }
-        };
-        gemm_mfma_ops<RT, CGW, NT, kCSplit, CGW, kD + kR>(acc, oc, hook);
-      });
     } else {
     for (int s = 0; s < ns; s += 4) {
       GEMM_STEP2(s, s_r0, 0);
@@ -1130,7 +1073,7 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
       if (s + 3 < ns) GEMM_STEP2(s + 3, s_r1, 3);
     }
     }
-    }  // RING == 0
+    }  // NSP == 0
 #undef GEMM_STEP2
 #undef GEMM_BARRIER
 #undef GEMM_VM_WAIT
@@ -1201,9 +1144,9 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
     constexpr int kStageW = NHB * kWaveCols * kRow * 4;  // staging bytes per wavefront
     constexpr int kHalf = W > 1 ? W / 2 : 1;           // wavefronts per ring slot
     if constexpr (kHalf * kStageW <= S::kSlot && NHB * kWaveCols <= 64) {  // one lane pass
-      float *st32 = RING ? reinterpret_cast<float *>(s_ring + wv * kStageW)
-                         : reinterpret_cast<float *>((wv < kHalf ? s_r0 : s_r1) + (wv % kHalf) * kStageW);
-      static_assert(!RING || W * kStageW <= kRingBytes, "staging fits the separate rings");
+      float *st32 = NSP ? reinterpret_cast<float *>(s_ring + wv * kStageW)
+                        : reinterpret_cast<float *>((wv < kHalf ? s_r0 : s_r1) + (wv % kHalf) * kStageW);
+      static_assert(!NSP || W * kStageW <= kRingBytes, "staging fits the rings");
 #pragma unroll
       for (int hbk = 0; hbk < NHB; hbk++) {
         if (!tv[4 * hbk]) break;  // the matrix has whole h blocks (rows % 64 == 0)
