@@ -701,6 +701,33 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
     assert_rel_l2(o32, want, "20B gemm T=64 shape 10")
 
 
+def test_batch_gemm_pipelined_k3072(orc):
+    """The pipelined 512 x 64 step at its other compile-time length, 24 K-steps (K = 3072 for
+    both GEMMs: the default there, codes 15-17 forced), against the 128 x 16 block (code 5) and
+    the 256 x 32 block of 4 wavefronts (code 2): the same MFMAs in the same order, identical
+    results; sampled tokens within the tolerance of the oracle."""
+    H = I = 3072
+    E, k, T = 8, 4, 160  # 80 entries per expert: the 512 x 64 block
+    L = syn.make_layer(H, I, E, seed=490, scale_lo=120, scale_hi=126, router_sigma=0.1)
+    d = GpuMoeDispatcher(H, I, 7.0)
+    try:
+        d.preload_layer(0, L)
+        x = syn.hidden(T, H, seed=491)
+        d.set_batch_gemm(2)
+        d.set_gemm_shape(5, 5)
+        base = d.layer_forward(0, x, k)
+        for shape_c, down in [(0, 0), (15, 15), (16, 16), (17, 17), (2, 2)]:
+            d.set_gemm_shape(shape_c, down)
+            o = d.layer_forward(0, x, k)
+            assert np.array_equal(base, o), f"K=3072: shape {shape_c} down {down}"
+        d.set_gemm_shape(0)
+        sample = np.arange(0, T, 20)
+        want = orc.moe_layer(x[sample], L, k)[0]
+        assert_rel_l2(base[sample], want, "K=3072 sampled tokens vs oracle")
+    finally:
+        d.close()
+
+
 def _prefill_parity(orc, d, layer, T, seed, n_sample):
     """A T-token layer through the default path (the 8-token router blocks, the grouped GEMM at
     the real K: the 512-row x 64-entry block at 512 entries per expert, the wide streamed form at
