@@ -670,8 +670,8 @@ def main():
                          "weights), 0 the five-kernel batch path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
-    ap.add_argument("--gemm-shape", type=int, default=0, choices=range(18), help="grouped GEMM block shape (tuning)")
-    ap.add_argument("--gemm-shape-down", type=int, default=0, choices=range(18),
+    ap.add_argument("--gemm-shape", type=int, default=0, choices=range(20), help="grouped GEMM block shape (tuning)")
+    ap.add_argument("--gemm-shape-down", type=int, default=0, choices=range(20),
                     help="block shape of the down GEMM alone (0: as --gemm-shape; tuning)")
     ap.add_argument("--gemm-band", type=int, default=0, help="grouped GEMM row blocks per band of the XCD tile order (tuning; 0 default)")
     ap.add_argument("--batch-gemm", type=int, default=1, choices=(0, 1, 2),

@@ -104,9 +104,13 @@ int moe_set_adaptive_topk(moe_ctx *ctx, int enabled, size_t min_k, float top1_mi
  * block with the pipelined step (each wavefront reads the next K-step's operands while its MFMAs
  * run; one barrier per step; K of 2817 to 3072 values, other K the plain step), 16 and 17 the same
  * with separate rings for the weights and the activation records (16: records three steps deep,
- * 17: weights three deep; the default for the down GEMM where code 15's K applies) (tuning; codes
- * 0-9 and 11-17 give identical results, code 10 the same to f32 rounding: its MFMA sums 64
- * products where the others sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
+ * 17: weights three deep; the default for the down GEMM where code 15's K applies), 18 and 19 the
+ * pipelined step (each GEMM with its default rings) on one workgroup per CU taking its tiles from
+ * a queue, the next tile's first DMAs issued inside the current tile's epilogue (18: the per-XCD
+ * ranges of MOE_OPT_GEMM_BAND's order when that applies; 19: one queue in the plain order; exact
+ * split, K of 2817 to 3072 values, otherwise as code 0) (tuning; codes 0-9 and 11-19 give
+ * identical results, code 10 the same to f32 rounding: its MFMA sums 64 products where the others
+ * sum 128). MOE_OPT_GEMM_SHAPE_DOWN: the same codes for the down GEMM alone
  * (0, default: as MOE_OPT_GEMM_SHAPE).
  * MOE_OPT_GEMM_BAND: row blocks per band of the grouped GEMM's per-XCD tile order for both
  * matrices, 1..64; 0 (default): gate_up in workgroup order, down in bands of 1 (tuning; results

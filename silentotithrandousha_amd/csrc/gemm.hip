@@ -1324,6 +1324,461 @@ __global__ __launch_bounds__(64 * WR * WC) __attribute__((amdgpu_waves_per_eu(WR
   }  // workgroup p
 }
 
+// ------------------------------------------------------------------ the pipelined step on a
+// persistent grid with a tile queue
+//
+// k_gemm_fp8's pipelined 512 x 64 step (NSP K-steps, rings RING) on one workgroup per CU that takes
+// its tiles from a queue in device memory, a.queue: [0, 8) the counters of the XCDs' ranges of the
+// banded tile order, [8] the counter of the plain order, [9] the workgroups done; all zero between
+// launches (the last workgroup to finish clears them). One workgroup per tile pays, per tile, the
+// tile search, the first DMAs' round trip and the workgroup turnover after the epilogue (measured at
+// prefill: 1.1, 2.3 and 2.3 us for gate_up, 1.1, 4.2 and 0.8 us for down, against ~30 us of steps).
+// Here they overlap: wavefront 0 takes and searches tile i + 1 while the DMAs of tile i's first
+// steps are in flight, and tile i + 1's bias and first steps' DMAs are issued inside tile i's
+// epilogue as soon as the ring is free (down: at its start; gate_up: once the SwiGLU values staged
+// in the ring have been read back). Same steps and epilogue as k_gemm_fp8: bit-identical results.
+// GLOBALQ: one queue in the plain order (row blocks fastest) whatever a.band asks.
+__device__ __forceinline__ void pq_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int MODE, int NSP, int RING, bool GLOBALQ>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_pq(GemmArgs a) {
+  constexpr int RT = 8, CGW = 2, WR = 4, WC = 2, D = 2, NT = kGemmTerms;
+  using S = GemmShape<RT, CGW, WR, WC, D, NT>;
+  static_assert(S::kTwoAhead && S::kSAddr && NSP >= 4 && NSP <= kGemmNs, "the pipelined 512 x 64 step");
+  constexpr int kRingA = RING == 2 ? 3 : 2, kRingB = RING == 1 ? 3 : 2;
+  constexpr int kRingBytes = kRingA * S::kBufA + kRingB * S::kGroups * 1024;
+  using G = GemmRecT<NT>;
+  constexpr int W = S::W, CG = CGW, kEntryStep = G::kStep;
+  constexpr int kCSplit = CGW / 2;
+  constexpr int kBiasTiles = RT;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_ring[kRingBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_sc[2][S::kTilesA * 256];
+  __shared__ __attribute__((aligned(16))) float s_bias[W * kBiasTiles * 16];
+  __shared__ int s_tile[2][4];  // tile i in s_tile[i & 1]: expert record index (-1: none), first entry, entries, row block
+  __shared__ int s_off[kMaxExperts + 1], s_id[kMaxExperts];  // the launch's expert lists
+  // lane and its parts are redefined (opaquely) at the top of every tile, so that the compiler
+  // does not hoist the steps' lane-dependent LDS addresses out of the tile loop and keep them live
+  const int tid = threadIdx.x, wv = tid >> 6;
+  int lane = tid & 63;
+  const int wr = wv % WR, wc = wv / WR;
+  int j = lane & 15, g = lane >> 4;
+  const int wvu = __builtin_amdgcn_readfirstlane(wv);
+  const PackDims d = a.d;
+  const int band = GLOBALQ ? 0 : a.band;
+  const int xcd = (int)blockIdx.x % 8;  // (workgroups go to the XCDs round-robin)
+  int *const ctr = a.queue + (band ? xcd : 8);
+
+  // ---- the expert lists into LDS once; the launch's tiles: n_real = row blocks x the column tiles
+  //      the experts' entries fill (kCols entries each), in k_gemm_fp8's orders over those
+  const int ma = min(a.max_active, kMaxExperts);
+  for (int i = tid; i <= ma; i += 64 * W) s_off[i] = a.active_off[i];
+  for (int i = tid; i < ma; i += 64 * W) s_id[i] = a.active_ids[i];
+  const int na = min(*a.n_active, ma);
+  __syncthreads();
+  constexpr int kQ = (kMaxExperts + 63) / 64;
+  int nct_real = 0;
+#pragma unroll
+  for (int qq = 0; qq < kQ; qq++) {
+    const int ai = 64 * qq + lane;
+    const int n = ai < na ? (s_off[ai + 1] - s_off[ai] + S::kCols - 1) / S::kCols : 0;
+    int v = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+    nct_real += v;
+  }
+  nct_real = __builtin_amdgcn_readfirstlane(nct_real);
+  const int nrb = a.n_row_blocks, n_real = nrb * nct_real;
+
+  // ---- wavefront 0: take a queue position (its atomic is issued a tile before the position is
+  //      used, so its round trip stays off the path); the tile at queue position q, its expert,
+  //      entries and row block into dst (expert -1: the queue is exhausted)
+  auto take = [&]() {
+    int q = 0;
+    if (lane == 0) q = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return q;
+  };
+  auto find_next = [&](int qv, int *dst) {
+    const int q = __builtin_amdgcn_readfirstlane(__shfl(qv, 0));
+    const int C = (n_real + 7) / 8;
+    const int L = band ? (q < C ? xcd * C + q : n_real) : q;
+    int ex = -1, beg = 0, cnt = 0, rblk_l = 0;
+    if (L < n_real) {
+      int cl;
+      const int nct = nct_real, RB = band ? min(band, nrb) : nrb, full = nrb / RB;
+      if (L < full * RB * nct) {
+        const int bd = L / (RB * nct), r = L - bd * RB * nct;
+        cl = r / RB;
+        rblk_l = bd * RB + r % RB;
+      } else {
+        const int rem = nrb - full * RB, r = L - full * RB * nct;
+        cl = r / rem;
+        rblk_l = full * RB + r % rem;
+      }
+      int base = 0;
+#pragma unroll
+      for (int qq = 0; qq < kQ; qq++) {
+        const int q0 = 64 * qq;
+        if (q0 >= na) break;
+        const int ai = q0 + lane;
+        const int o0 = ai < na ? s_off[ai] : 0, o1 = ai < na ? s_off[ai + 1] : 0;
+        const int nct_e = (o1 - o0 + S::kCols - 1) / S::kCols;
+        int incl = nct_e;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int v = __shfl_up(incl, o);
+          if (lane >= o) incl += v;
+        }
+        const int start = base + incl - nct_e;
+        const uint64_t hit = __ballot(ai < na && cl >= start && cl < start + nct_e);
+        if (hit) {
+          const int hl = __builtin_ctzll(hit);
+          if (lane == hl) {
+            ex = s_id[ai];
+            beg = o0 + (cl - start) * S::kCols;
+            cnt = min(S::kCols, o1 - beg);
+          }
+          ex = __shfl(ex, hl);
+          beg = __shfl(beg, hl);
+          cnt = __shfl(cnt, hl);
+          break;
+        }
+        base += __shfl(incl, 63);
+      }
+    }
+    if (lane == 0) {
+      dst[0] = ex;
+      dst[1] = beg;
+      dst[2] = cnt;
+      dst[3] = rblk_l;
+    }
+  };
+
+  // ---- per tile: the DMA sources (as in k_gemm_fp8) and the epilogue's bounds
+  int ex, beg, ncol, t0;
+  const uint8_t *rec, *mat;
+  uint32_t boff[S::kDma];
+  const uint8_t *asrc[S::kDmaA];
+  const uint8_t *ssrc[S::kDmaA];
+  // set_tile in two parts: the tile's bounds and its entries' record rows (loads, issued early),
+  // then the DMA sources once the rows are needed
+  int rowv[S::kDma];
+  int tb = 0;
+  auto load_tile = [&](const int *src) {
+    ex = __builtin_amdgcn_readfirstlane(src[0]);
+    beg = __builtin_amdgcn_readfirstlane(src[1]);
+    ncol = __builtin_amdgcn_readfirstlane(src[2]);
+    const int rblk = __builtin_amdgcn_readfirstlane(src[3]);
+    if (ex < 0) return;
+    tb = rblk * S::kRows / 16;
+    t0 = tb + wr * RT;
+    rec = a.base + (size_t)ex * a.stride;
+    mat = rec + a.mat_off;
+#pragma unroll
+    for (int i = 0; i < S::kDma; i++) {
+      const int c = min(64 * (W * i + wv) + lane, S::kStepChunks - 1);
+      const int ge = beg + min(c / G::kChunks, ncol - 1);
+      rowv[i] = a.entry_src ? a.entry_src[ge] : ge;
+    }
+  };
+  auto set_tile = [&]() {
+    if (ex < 0) return;
+#pragma unroll
+    for (int i = 0; i < S::kDma; i++) {
+      const int c = min(64 * (W * i + wv) + lane, S::kStepChunks - 1);
+      boff[i] = (uint32_t)rowv[i] * (uint32_t)G::kBytes + 16u * (c % G::kChunks);
+    }
+#pragma unroll
+    for (int i = 0; i < S::kDmaA; i++) {
+      const int tl = min(tb + W * i + wvu, (int)d.tiles - 1);
+      asrc[i] = mat + (size_t)tl * 16 * d.nb * 16;
+      ssrc[i] = mat + pack_weight_bytes(d) + (size_t)tl * d.nq * 256;
+    }
+  };
+  const uint32_t a_last = 16u * d.nb * 16u - 16u;
+  const bool fullb = W * (S::kDma - 1) + wvu < S::kGroups;
+  static_assert(W * (S::kDma - 1) < S::kGroups, "only the last B piece can fall past the step");
+
+  constexpr int DA = kRingA, DB = kRingB, kBufBr = S::kGroups * 1024;
+  auto slA = [&](int st) { return s_ring + (st % DA) * S::kBufA; };
+  auto slB = [&](int st) { return s_ring + DA * S::kBufA + (st % DB) * kBufBr; };
+  auto dmaB_last = [&](int ld) {
+    if (fullb) lds_dma16_s(boff[S::kDma - 1], a.brec + (size_t)ld * G::kStep, slB(ld) + 1024 * (W * (S::kDma - 1) + wvu));
+  };
+  auto dmaB = [&](int k, int ld) {
+    lds_dma16_s(boff[k], a.brec + (size_t)ld * G::kStep, slB(ld) + 1024 * (W * k + wvu));
+  };
+  auto dmaA = [&](int k, int ld) {
+    if (k < S::kDmaA) {
+      lds_dma16_s(min((uint32_t)ld * 1024u + 16u * lane, a_last), asrc[k], slA(ld) + (W * k + wvu) * 1024);
+    } else {
+      const int i = k - S::kDmaA;
+      lds_dma4_s((uint32_t)(ld >> 2) * 256u + 4u * lane, ssrc[i], s_sc[(ld >> 2) & 1] + (W * i + wvu) * 256);
+    }
+  };
+  auto nA = [&](int ld) { return ld < NSP ? S::kDmaA + ((ld & 3) == 0 ? S::kDmaA : 0) : 0; };
+  auto issueA = [&](int ld) {
+    for (int k = 0; k < nA(ld); k++) dmaA(k, ld);
+  };
+  auto issueB = [&](int ld) {
+    if (ld >= NSP) return;
+    for (int k = 0; k < S::kDma - 1; k++) dmaB(k, ld);
+    dmaB_last(ld);
+  };
+  // the tile's bias (into the wavefront's part of s_bias) and the DMAs of its first steps, in the
+  // order of k_gemm_fp8's prologue
+  auto issue_first = [&]() {
+    const float *bias = reinterpret_cast<const float *>(rec + a.bias_off);
+#pragma unroll
+    for (int k = 0; k < kBiasTiles / 4; k++)
+      lds_dma4(bias + min(t0 * 16 + 64 * k + lane, (int)d.rows - 1), s_bias + (wv * kBiasTiles + 4 * k) * 16);
+    issueA(0);
+    issueB(0);
+    if constexpr (RING == 1) {
+      issueA(1);
+      issueB(1);
+      issueB(2);
+    } else if constexpr (RING == 2) {
+      issueB(1);
+      issueA(1);
+      issueA(2);
+    } else {
+      issueB(1);
+      issueA(1);
+    }
+  };
+
+  int qn = 0;  // wavefront 0: the queue position of the tile after the next
+  if (wv == 0) {
+    find_next(take(), s_tile[0]);
+    qn = take();
+  }
+  __syncthreads();
+  load_tile(s_tile[0]);
+  set_tile();
+  if (ex >= 0) issue_first();
+  for (int it = 0; ex >= 0; it++) {
+    asm volatile("" : "+v"(lane), "+v"(j), "+v"(g));
+    if (wv == 0) find_next(qn, s_tile[(it + 1) & 1]);  // read by every wavefront after the barrier below
+    // step 0 whole, the deeper ring's steps in flight (whatever the previous epilogue stored
+    // after them is waited for too: loads and stores complete in order)
+    if constexpr (RING == 1) {
+      if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(nA(1) + 2 * S::kDma));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(nA(1) + 2 * (S::kDma - 1)));
+    } else if constexpr (RING == 2) {
+      if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + nA(1) + nA(2)));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + nA(1) + nA(2)));
+    } else {
+      if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma + nA(1)));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1 + nA(1)));
+    }
+    pq_barrier();
+    f32x4 acc[RT][CG];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int c = 0; c < CG; c++) acc[r][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t sw4_[RT];
+    {
+      constexpr int kNextA = RT, kNextB = kCSplit * (NT + 1);
+      GemmOps<RT, CGW, NT> opE_, opO_;
+      GemmBRaw<NT> rbE_[kCSplit], rbO_[kCSplit];
+#pragma unroll
+      for (int r_ = 0; r_ < RT; r_++) {
+        sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[0] + (wr * RT + r_) * 256 + 4 * lane);
+        opE_.ar[r_] = *reinterpret_cast<const uint4 *>(slA(0) + (wr * RT + r_) * 1024 + 16 * lane);
+        opE_.sw[r_] = sw4_[r_];
+      }
+#pragma unroll
+      for (int c_ = 0; c_ < kCSplit; c_++) gemm_read_b_raw(rbE_[c_], slB(0) + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
+      str_static_for<0, NSP>([&](auto stc) {
+        constexpr int st = decltype(stc)::value;
+        GemmOps<RT, CGW, NT> &oc = (st & 1) ? opO_ : opE_;
+        GemmOps<RT, CGW, NT> &on = (st & 1) ? opE_ : opO_;
+        GemmBRaw<NT>(&rc)[kCSplit] = (st & 1) ? rbO_ : rbE_;
+        GemmBRaw<NT>(&rn)[kCSplit] = (st & 1) ? rbE_ : rbO_;
+        const uint8_t *bc = slB(st);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c_ = 0; c_ < kCSplit; c_++) gemm_select_b(oc.b[c_], rc[c_], g);
+        GemmBRaw<NT> raw_[CGW - kCSplit];
+#pragma unroll
+        for (int c_ = kCSplit; c_ < CGW; c_++)
+          gemm_read_b_raw(raw_[c_ - kCSplit], bc + (16 * CGW * wc + j + 16 * c_) * kEntryStep, g);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_mfma_ops<RT, CGW, NT, 0, kCSplit, 0>(acc, oc, [](int) {});
+#pragma unroll
+        for (int c_ = kCSplit; c_ < CGW; c_++) gemm_select_b(oc.b[c_], raw_[c_ - kCSplit], g);
+        if constexpr (RING == 1) {
+          if constexpr (st + 2 < NSP) {
+            if (fullb) __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma));
+            else __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(S::kDma - 1));
+          } else {
+            __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+          }
+        } else if constexpr (RING == 2) {
+          constexpr int kOut = st + 2 < NSP ? S::kDmaA + (((st + 2) & 3) == 0 ? S::kDmaA : 0) : 0;
+          __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(kOut));
+        } else {
+          __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(0));
+        }
+        pq_barrier();
+        constexpr int ldA = st + DA, ldB = st + DB;
+        constexpr int kNA = ldA < NSP ? S::kDmaA + ((ldA & 3) == 0 ? S::kDmaA : 0) : 0;
+        constexpr int kNB = ldB < NSP ? (RING == 1 ? S::kDma - 1 : S::kDma) : 0;
+        constexpr int kD = kNA + kNB;
+        constexpr int kR = st + 1 < NSP ? kNextA + kNextB : 0;
+        constexpr int sh = 8 * ((st + 1) & 3);
+        const uint8_t *nb = slB(st + 1) + (16 * CGW * wc + j) * kEntryStep;
+        const uint8_t *na = slA(st + 1) + wr * RT * 1024;
+        auto hook = [&](int k_) {
+          if (k_ < kD) {
+            if constexpr (RING == 1) {
+              if (k_ < kNA) dmaA(k_, ldA);
+              else dmaB(k_ - kNA, ldB);
+            } else {
+              if (k_ == 0) dmaB_last(ldB);
+              else if (k_ < kNB) dmaB(k_ - 1, ldB);
+              else dmaA(k_ - kNB, ldA);
+            }
+          } else if (k_ - kD < kNextA) {
+            const int r_ = k_ - kD;
+            if (((st + 1) & 3) == 0)
+              sw4_[r_] = *reinterpret_cast<const uint32_t *>(s_sc[((st + 1) >> 2) & 1] + (wr * RT + r_) * 256 + 4 * lane);
+            on.ar[r_] = *reinterpret_cast<const uint4 *>(na + r_ * 1024 + 16 * lane);
+            on.sw[r_] = sw4_[r_] >> sh;
+          } else {
+            const int i_ = k_ - kD - kNextA, c_ = i_ / (NT + 1), t_ = i_ % (NT + 1);
+            const uint8_t *eb = nb + 16 * c_ * kEntryStep;
+            if (t_ < NT) {
+              rn[c_].x[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + g) * 16);
+              rn[c_].y[t_] = *reinterpret_cast<const uint4 *>(eb + (6 * t_ + 4 + (g >> 1)) * 16);
+            } else {
+              const uint4 sc = *reinterpret_cast<const uint4 *>(eb + (G::kChunks - 1) * 16);
+              const uint32_t w3[3] = {sc.x, sc.y, sc.z};
+#pragma unroll
+              for (int q_ = 0; q_ < NT; q_++) rn[c_].sc[q_] = w3[q_];
+            }
+          }
+        };
+        gemm_mfma_ops<RT, CGW, NT, kCSplit, CGW, kD + kR>(acc, oc, hook);
+        if constexpr (RING == 1 && ldB < NSP) dmaB_last(ldB);
+      });
+    }
+
+    // ---- epilogue of this tile; the next tile's first DMAs as soon as the ring is free
+    const int cex = ex, cbeg = beg, cncol = ncol, ct0 = t0;
+    bool tv[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) tv[r] = ct0 + r < (int)d.tiles;
+    float4 bv[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) bv[r] = *reinterpret_cast<const float4 *>(s_bias + (wv * kBiasTiles + r) * 16 + 4 * g);
+    __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));  // (the bias reads done before its next DMA)
+    (void)cex;
+    // the next tile's record rows in flight from the start of the epilogue
+    load_tile(s_tile[(it + 1) & 1]);
+    auto next_first = [&]() {
+      set_tile();
+      if (ex >= 0) issue_first();
+    };
+    if constexpr (MODE == GEMV_GATE_UP) {
+      // as k_gemm_fp8's one-pass split: the wavefront's 2 h blocks x 32 entries staged in the ring
+      constexpr int kWaveCols = 16 * CGW, NHB = RT / 4, kRow = 36;
+      constexpr int kStageW = NHB * kWaveCols * kRow * 4;
+      static_assert(W * kStageW <= kRingBytes && NHB * kWaveCols == 64, "one lane pass, staged in the ring");
+      uint8_t *hout = reinterpret_cast<uint8_t *>(a.out);
+      const int e0 = kWaveCols * wc;
+      const int nloc = max(0, min(kWaveCols, cncol - e0));
+      float *st32 = reinterpret_cast<float *>(s_ring + wv * kStageW);
+#pragma unroll
+      for (int hbk = 0; hbk < NHB; hbk++) {
+        if (!tv[4 * hbk]) break;
+#pragma unroll
+        for (int c = 0; c < CG; c++) {
+          if (16 * c >= nloc) break;
+          float *se = st32 + (hbk * kWaveCols + 16 * c + j) * kRow;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const f32x4 &av = acc[4 * hbk + r][c];
+            const float4 &b4 = bv[4 * hbk + r];
+            *reinterpret_cast<float2 *>(se + 8 * r + 2 * g) =
+                make_float2(swiglu_fast(av[0] + b4.x, av[1] + b4.y, a.limit), swiglu_fast(av[2] + b4.z, av[3] + b4.w, a.limit));
+          }
+        }
+      }
+      const int hbk = min(lane / kWaveCols, NHB - 1), e = lane % kWaveCols;
+      const bool valid = tv[4 * hbk] && e < nloc;
+      const float *row = st32 + (valid ? hbk * kWaveCols + e : 0) * kRow;
+      float v[32];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float4 x = *reinterpret_cast<const float4 *>(row + 4 * q);
+        v[4 * q] = x.x;
+        v[4 * q + 1] = x.y;
+        v[4 * q + 2] = x.z;
+        v[4 * q + 3] = x.w;
+      }
+      __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));  // the staging reads done
+      pq_barrier();                              // ... in every wavefront: the ring is free
+      next_first();
+      float m = 0.0f;
+      bool bad = false;
+#pragma unroll
+      for (int k = 0; k < 32; k++) {
+        m = fmaxf(m, fabsf(v[k]));
+        bad = bad || !isfinite(v[k]);
+      }
+      uint32_t dq[NT][6], sb;
+      split32_fp6<NT>(v, m, bad, dq, sb);
+      if (valid) {
+        const int hb = ct0 / 4 + hbk, st = hb >> 2, i = hb & 3;
+        uint8_t *hr = hout + (size_t)(cbeg + e0 + e) * G::kBytes;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          *reinterpret_cast<uint4 *>(hr + G::dword(st, t, i, 0)) = make_uint4(dq[t][0], dq[t][1], dq[t][2], dq[t][3]);
+          *reinterpret_cast<uint2 *>(hr + G::dword(st, t, i, 4)) = make_uint2(dq[t][4], dq[t][5]);
+          hr[G::scale(st, t) + i] = (uint8_t)(sb >> (8 * t));
+        }
+      }
+    } else {
+      next_first();
+      float *out = reinterpret_cast<float *>(a.out);
+      const int R = (int)d.rows;
+#pragma unroll
+      for (int r = 0; r < RT; r++) {
+        if (!tv[r]) continue;
+        const float4 b4 = bv[r];
+        const int row = (ct0 + r) * 16 + 4 * g;
+#pragma unroll
+        for (int c = 0; c < CG; c++) {
+          const int e = 16 * (CGW * wc + c) + j;
+          if (e >= cncol) continue;
+          float4 o;
+          o.x = canon_nan(rclamp(acc[r][c][0] + b4.x, -65504.0f, 65504.0f));
+          o.y = canon_nan(rclamp(acc[r][c][1] + b4.y, -65504.0f, 65504.0f));
+          o.z = canon_nan(rclamp(acc[r][c][2] + b4.z, -65504.0f, 65504.0f));
+          o.w = canon_nan(rclamp(acc[r][c][3] + b4.w, -65504.0f, 65504.0f));
+          *reinterpret_cast<float4 *>(out + (size_t)(cbeg + e) * R + row) = o;
+        }
+      }
+    }
+    // the queue position of the tile after the next, last of the epilogue's memory operations (a
+    // wait for anything issued before it would otherwise wait for its round trip too)
+    if (wv == 0 && ex >= 0) qn = take();
+  }
+  // the queue is exhausted for this workgroup: the last one out clears the counters
+  if (tid == 0) {
+    const int n = __hip_atomic_fetch_add(a.queue + 9, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n == (int)gridDim.x - 1) {
+      for (int q = 0; q < 10; q++) st_agent(reinterpret_cast<uint32_t *>(a.queue + q), 0u);
+    }
+  }
+}
+
 // Compute units of the current device (cached per device).
 static int device_cus() {
   static std::atomic<int> cus[64] = {};  // (threads racing here store the same value)
@@ -1355,6 +1810,22 @@ static hipError_t launch_gemm_shape(GemmArgs a, hipStream_t s) {
   const size_t grid = gemm_persistent<MODE, S, NSP>() ? std::min<size_t>(blocks, (size_t)device_cus()) : blocks;
   if (NSP && a.d.ns != (uint32_t)NSP) return hipErrorInvalidValue;
   hipLaunchKernelGGL((k_gemm_fp8<MODE, RT, CGW, WR, WC, D, NT, M32, NSP, RING>), dim3((unsigned)grid), dim3(S::kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+// The pipelined 512 x 64 step on one workgroup per CU taking tiles from the queue (k_gemm_pq).
+template <int MODE, int NSP, int RING, bool GLOBALQ>
+static hipError_t launch_gemm_pq(GemmArgs a, hipStream_t s) {
+  using S = GemmShape<8, 2, 4, 2, 2, kGemmTerms>;
+  if (!a.queue || a.d.ns != (uint32_t)NSP) return hipErrorInvalidValue;
+  a.n_row_blocks = (int)((a.d.rows + S::kRows - 1) / S::kRows);
+  const size_t col_tiles = (size_t)a.max_active + (a.n_entries + S::kCols - 1) / S::kCols;
+  const size_t tiles = (size_t)a.n_row_blocks * col_tiles;
+  if (!tiles) return hipSuccess;
+  if (tiles > (size_t)INT32_MAX - 8) return hipErrorInvalidValue;
+  a.n_tiles = (int)tiles;
+  a.n_blocks = (int)tiles;
+  hipLaunchKernelGGL((k_gemm_pq<MODE, NSP, RING, GLOBALQ>), dim3((unsigned)device_cus()), dim3(S::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1425,6 +1896,17 @@ static hipError_t launch_gemm_mode(const GemmArgs &a, hipStream_t s) {
     return launch_gemm_shape<MODE, 8, 2, 4, 2, 2, NT>(a, s);
   }
   if (a.shape == 11) return launch_gemm_shape<MODE, 16, 2, 2, 4, 2, NT>(a, s);
+  if constexpr (NT == kGemmTerms) {
+    // the pipelined step on a persistent grid with a tile queue (18: the XCD ranges of the banded
+    // order when the launch asks for one; 19: one queue in the plain order), each GEMM with the
+    // rings of its default
+    if ((a.shape == 18 || a.shape == 19) && (a.d.ns == 23 || a.d.ns == 24)) {
+      constexpr int kR = MODE == GEMV_DOWN ? 2 : 0;
+      if (a.d.ns == 23)
+        return a.shape == 18 ? launch_gemm_pq<MODE, 23, kR, false>(a, s) : launch_gemm_pq<MODE, 23, kR, true>(a, s);
+      return a.shape == 18 ? launch_gemm_pq<MODE, 24, kR, false>(a, s) : launch_gemm_pq<MODE, 24, kR, true>(a, s);
+    }
+  }
   if (mean >= 48) {
     if (a.shape == 1) return launch_gemm_shape<MODE, 4, 4, 8, 1, 2, NT>(a, s);
     // the pipelined step (measured at prefill, 20B x 4096 tokens, paired runs: down 292 -> 278 us;

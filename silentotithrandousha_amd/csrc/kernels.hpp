@@ -120,6 +120,7 @@ struct GemmArgs {
   int n_tiles;               //                         row blocks x column tiles
   int n_blocks;              //                         workgroups of the tile order (>= n_tiles)
   int terms;                 // E2M3 terms per activation value: kGemmTerms, or 1 (quantized mode)
+  int32_t *queue;            // tile queue of the persistent pipelined step: 10 counters, zero between launches
   // Local grouping (the streamed gate_up GEMM of a batch of at most kLocalGroupMax entries): with
   // group_idx set (the top-k indices [T][group_k] over group_E experts, -1 for a dropped slot)
   // every workgroup groups the entries by expert itself, in place of the router's grouping, and

@@ -134,6 +134,7 @@ struct moe_ctx {
   int act_quant = 0;  // grouped GEMM activations: 0 the exact kGemmTerms split, 1 one MXFP6 term
   int local_group = 1;  // small batches on the streamed GEMM: its workgroups group the entries
   DevBuf route_ticket;  // k_route's block counter for the fused bucketing, zero between launches
+  DevBuf gemm_queue;    // the persistent grouped GEMM's tile queue (10 counters), zero between launches
   DevBuf layer_sync;  // cross-block signalling of the one-launch kernel, zero between launches
   DevBuf layer_h;     // h records of the one-launch kernel's slots (values past I stay zero)
   int n_cu = 256;     // compute units of the device (the one-launch grid is sized to it)
@@ -540,6 +541,7 @@ int forward_device(moe_ctx *c, const Work &w, size_t layer, const float *x, size
     ga.shape = c->gemm_shape;
     ga.band = c->gemm_band;  // default: gate_up in workgroup order, down in XCD bands of 1 row block
     ga.terms = c->act_quant ? 1 : kGemmTerms;
+    ga.queue = (int32_t *)c->gemm_queue.p;
     gu = ga;
     gu.mat_off = c->L.gu_off;
     gu.bias_off = c->L.gub_off;
@@ -643,6 +645,7 @@ int moe_create(size_t hidden_size, size_t inter_size, float swiglu_clamp, moe_ct
   const size_t sb = layer_sync_bytes(), hb = layer_hterm_bytes();
   if (c->layer_sync.ensure(sb) != MOE_OK || hipMemset(c->layer_sync.p, 0, sb) != hipSuccess ||
       c->route_ticket.ensure(256) != MOE_OK || hipMemset(c->route_ticket.p, 0, 256) != hipSuccess ||
+      c->gemm_queue.ensure(256) != MOE_OK || hipMemset(c->gemm_queue.p, 0, 256) != hipSuccess ||
       c->layer_h.ensure(hb) != MOE_OK || hipMemset(c->layer_h.p, 0, hb) != hipSuccess) {
     moe_destroy(c);
     return fail(MOE_ERR_OOM, "signalling area of %zu bytes", sb);
@@ -668,6 +671,7 @@ void moe_destroy(moe_ctx *c) {
   c->work.release();
   c->layer_sync.release();
   c->route_ticket.release();
+  c->gemm_queue.release();
   c->layer_h.release();
   c->scratch_experts.release();
   c->stage.release();
@@ -1190,7 +1194,7 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
       c->batch_gemm = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_SHAPE:
-      if (value < 0 || value > 17) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..17");
+      if (value < 0 || value > 19) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE is 0..19");
       c->gemm_shape = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_BAND:
@@ -1198,7 +1202,7 @@ int moe_set_option(moe_ctx *c, int option, int64_t value) {
       c->gemm_band = (int)value;
       return MOE_OK;
     case MOE_OPT_GEMM_SHAPE_DOWN:
-      if (value < 0 || value > 17) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE_DOWN is 0..17");
+      if (value < 0 || value > 19) return fail(MOE_ERR_INVALID, "MOE_OPT_GEMM_SHAPE_DOWN is 0..19");
       c->gemm_shape_down = (int)value;
       return MOE_OK;
     case MOE_OPT_MATVEC:

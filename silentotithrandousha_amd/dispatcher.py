@@ -160,7 +160,7 @@ class GpuMoeDispatcher:
         check(lib().moe_set_option(self._ctx, MOE_OPT_BATCH_GEMM, int(mode)))
 
     def set_gemm_shape(self, shape, down=0):
-        """Grouped GEMM block shape (0 by batch size, 1..17 forced alternatives; down: the same
+        """Grouped GEMM block shape (0 by batch size, 1..19 forced alternatives; down: the same
         codes for the down GEMM alone, 0 = as shape; tuning only)."""
         from ._ffi import MOE_OPT_GEMM_SHAPE, MOE_OPT_GEMM_SHAPE_DOWN
         check(lib().moe_set_option(self._ctx, MOE_OPT_GEMM_SHAPE, int(shape)))

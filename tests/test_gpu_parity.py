@@ -686,7 +686,7 @@ def test_batch_gemm_block_shapes_identical_20b(orc, disp20, layer20):
     disp20.set_batch_gemm(2)
     outs = []
     shapes = [(0, 0), (3, 3), (5, 5), (6, 6), (7, 7), (2, 2), (5, 4), (12, 12), (13, 13), (12, 5), (14, 14),
-              (14, 5), (15, 15), (15, 5), (5, 15), (16, 16), (17, 17)]
+              (14, 5), (15, 15), (15, 5), (5, 15), (16, 16), (17, 17), (18, 18), (19, 19)]
     for shape, down in shapes:
         disp20.set_gemm_shape(shape, down)
         outs.append(disp20.layer_forward(0, x, 4))
@@ -716,7 +716,7 @@ def test_batch_gemm_pipelined_k3072(orc):
         d.set_batch_gemm(2)
         d.set_gemm_shape(5, 5)
         base = d.layer_forward(0, x, k)
-        for shape_c, down in [(0, 0), (15, 15), (16, 16), (17, 17), (2, 2)]:
+        for shape_c, down in [(0, 0), (15, 15), (16, 16), (17, 17), (18, 18), (19, 19), (18, 0), (2, 2)]:
             d.set_gemm_shape(shape_c, down)
             o = d.layer_forward(0, x, k)
             assert np.array_equal(base, o), f"K=3072: shape {shape_c} down {down}"
@@ -761,7 +761,7 @@ def _prefill_parity(orc, d, layer, T, seed, n_sample):
     d.set_batch_gemm(1)
     e = rel_l2(got, ref)
     assert e < 6e-4, f"T={T} E={E} grouped GEMM vs GEMV path {e:.2e}"
-    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4), (11, 11), (14, 14), (0, 14), (15, 15), (15, 0), (0, 15), (16, 16), (17, 17)]:
+    for shape, down in [(1, 0), (8, 8), (2, 2), (3, 3), (0, 4), (11, 11), (14, 14), (0, 14), (15, 15), (15, 0), (0, 15), (16, 16), (17, 17), (18, 18), (19, 19), (18, 0), (0, 18)]:
         d.set_gemm_shape(shape, down)
         o = d.layer_forward(0, x, k)
         assert np.array_equal(got, o), f"T={T} E={E} shape {shape} down {down}"
