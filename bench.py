@@ -343,17 +343,24 @@ def _run_layer(model, workload, steps, warmup, graph, copy_mib, traffic_kib, act
                                peak=MXFP4_PEAK_TFLOPS, unit="TFLOP/s",
                                frac=round(d_flops / d_avg_s / 1e12 / MXFP4_PEAK_TFLOPS, 5),
                                hbm_GBps=round(d_bytes / d_avg_s / 1e9, 1))
-    if not traffic_kib:  # calibrated PMC measurement of the same kernel and workload
-        tf = os.path.join(ROOT, "profiles", "traffic.json")
-        if os.path.exists(tf):
-            recs = json.load(open(tf))
-            # (the quantized mode runs other kernels: its records are keyed apart)
-            key = f"{kname}@{workload}" + ("+act_quant" if act_quant else "")
-            rec = recs.get(key) or (None if act_quant else recs.get(kname))
-            if rec and rec.get("workload") == workload:
-                res["roofline"]["traffic"] = rec["bytes_per_launch"]
-                res["roofline"]["traffic_source"] = rec["source"]
+    if not traffic_kib:
+        attach_traffic(res["roofline"], kname, workload, act_quant)
     return res
+
+
+def attach_traffic(roofline, kname, workload, act_quant=False):
+    """The calibrated PMC measurement (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE per launch) of the
+    same kernel on the same workload, from profiles/traffic.json, into roofline["traffic"]."""
+    tf = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(tf):
+        return
+    recs = json.load(open(tf))
+    # (the quantized mode runs other kernels: its records are keyed apart)
+    key = f"{kname}@{workload}" + ("+act_quant" if act_quant else "")
+    rec = recs.get(key) or (None if act_quant else recs.get(kname))
+    if rec and rec.get("workload") == workload:
+        roofline["traffic"] = rec["bytes_per_launch"]
+        roofline["traffic_source"] = rec["source"]
 
 
 # ------------------------------------------------------------------ config 1: one MXFP4 matvec
@@ -707,14 +714,20 @@ def main():
     elif head == "beaver32":
         common["metric"] = "Beaver triples/s, p = 2^31 - 1, n = 5, t = 1"
     t_start = time.perf_counter()
+    def with_traffic(r, workload):  # the measured HBM traffic of the dominant kernel, when recorded
+        attach_traffic(r["roofline"], r["roofline"]["kernel"], workload)
+        return r
+
+    if head in ("matvec", "lm_head", "lm_head_bf16", "beaver32") and args.copy_mib:
+        copy_calibration(args.copy_mib)
     if head == "matvec":
-        res = run_matvec(steps, warmup, args.graph)
+        res = with_traffic(run_matvec(steps, warmup, args.graph), head)
     elif head == "lm_head":
-        res = run_lm_head(steps, warmup)
+        res = with_traffic(run_lm_head(steps, warmup), head)
     elif head == "lm_head_bf16":
-        res = run_lm_head_bf16(steps, warmup)
+        res = with_traffic(run_lm_head_bf16(steps, warmup), head)
     elif head == "beaver32":
-        res = run_beaver32(steps, warmup)
+        res = with_traffic(run_beaver32(steps, warmup), head)
     else:
         E = WORKLOADS[head][1]
         m = Model(H20, I20, E, args.layers if E == 32 else args.layers_120b, args)
@@ -732,11 +745,11 @@ def main():
                 extras[key] = run_layer(m, w, WORKLOADS[w][4], WORKLOADS[w][5], args.graph)
                 log(f"{w}: {extras[key]['value']} tokens/s")
             m.close()
-            extras["config1_matvec"] = run_matvec(4800, 480, args.graph)
+            extras["config1_matvec"] = with_traffic(run_matvec(4800, 480, args.graph), "matvec")
             log(f"matvec: {extras['config1_matvec']['value']} GB/s")
-            extras["next_lm_head_bf16"] = run_lm_head_bf16(80, 8)
+            extras["next_lm_head_bf16"] = with_traffic(run_lm_head_bf16(80, 8), "lm_head_bf16")
             log(f"lm head bf16: {extras['next_lm_head_bf16']['value']} GB/s")
-            extras["next_beaver32"] = run_beaver32(20, 3)
+            extras["next_beaver32"] = with_traffic(run_beaver32(20, 3), "beaver32")
             log(f"beaver32: {extras['next_beaver32']['value']} triples/s")
             res["configs"] = extras
         else:
