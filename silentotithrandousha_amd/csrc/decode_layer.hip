@@ -350,6 +350,8 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
   // that wait for the routing come after them.
   if ((int)blockIdx.x < la.n_rt) {
     const int e = (int)blockIdx.x * kLayerWaves + wv;
+    MOE_TRACE(0);
+    MOE_TRACE_WHERE();
     if (e < E) {
       float xr[XI];
 #pragma unroll
@@ -372,6 +374,7 @@ __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(2
         }
       }
       const float lg = router_logit<RNQ>(a.rw, a.rb, xr, e, lane);
+      MOE_TRACE(1);
       if (lane < nrep) st_agent64(&logit_copy(la.sync, lane)->logit[e], (1ull << 32) | __float_as_uint(lg));
     }
     return;

@@ -13,7 +13,8 @@ start), which blocks share a CU, and the gate_up end time by the number of weigh
 streams. Stamps (decode_layer.hip, MOE_TRACE): gate_up blocks 0 start, 1 x split in LDS,
 2 routing known, 3 tiles computed, 5 after the block barrier, 6 h stores acknowledged, 4 flag
 stored; down blocks 0 start, 1 routing known, 2 all flags seen, 3 h copy issued, 5 sweep done,
-4 output stored. Development tool: not used by the library, the tests or the benchmark.
+4 output stored; router blocks (wavefront 0) 0 start, 1 logit computed (its stores follow).
+Development tool: not used by the library, the tests or the benchmark.
 """
 import ctypes
 import os
@@ -88,6 +89,10 @@ def main():
         for name, (a, b_) in {"down: routing": (0, 1), "down: flag wait": (1, 2), "down: copy + sweep": (3, 5),
                               "down: combine": (5, 4)}.items():
             ph[name].append(np.median([us[i, b_] - us[i, a] for i in dn]))
+        rt = range(0, n_rt)
+        ph["router: x, weights and logit"].append(np.median([us[i, 1] - us[i, 0] for i in rt]))
+        ends["router blocks start (min)"].append(us[list(rt), 0].min())
+        ends["router logits computed (max)"].append(us[list(rt), 1].max())
         ends["routing known (gate_up, p50)"].append(np.median(us[list(gu), 2]))
         ends["gate_up flags stored (max)"].append(us[list(gu), 4].max())
         ends["down: all flags seen (p50)"].append(np.median(us[list(dn), 2]))
